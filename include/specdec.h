@@ -1,0 +1,230 @@
+/*
+ * specdec.h - C ABI of libspecdec.so, the gfx950 (MI355X) kernels behind the
+ * speculative-decoding hot path of beriltatli/speculative-decoder.
+ *
+ * Every entry point takes plain device pointers, element counts and strides
+ * (in elements, not bytes) and a HIP stream passed as `void *` (0 = the null
+ * stream).  Nothing here allocates device memory: buffers are owned by the
+ * caller.  Every call returns an `int` status:
+ *
+ *   SPECDEC_OK           0  launched
+ *   SPECDEC_EINVAL       1  a size, stride or pointer argument is out of range
+ *   SPECDEC_EHIP         2  the HIP launch failed (hipGetLastError)
+ *   SPECDEC_EUNSUPPORTED 3  a shape the kernels do not implement (e.g. head_dim != 64)
+ *
+ * Data-dependent conditions that the reference raises on (a drafted token
+ * with zero draft probability, a double free) are reported through status
+ * words written by the kernel into caller memory, so the host decides which
+ * exception to raise after it reads them.
+ *
+ * Element types are selected with SPECDEC_F32 / SPECDEC_F64 / SPECDEC_BF16.
+ *
+ * Per-call batch metadata ("meta") is one int32 array of 3*batch entries:
+ *   meta[0*batch + b] = table row of batch entry b (row in `tables`)
+ *   meta[1*batch + b] = cached length before this call (past)
+ *   meta[2*batch + b] = tokens appended by this call (n_new, <= width)
+ * Block tables are int32 [rows, table_stride]; entry [r, j] is the physical
+ * block holding positions j*block_size .. j*block_size+block_size-1 of row r.
+ *
+ * KV pool layout, per layer:
+ *   K: [num_blocks, n_kv_heads, block_size, head_dim]   (token-major tile)
+ *   V: [num_blocks, n_kv_heads, head_dim, block_size]   (dim-major tile)
+ * so that one (block, head) tile of K or V is contiguous in HBM.
+ */
+#ifndef SPECDEC_H
+#define SPECDEC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPECDEC_OK 0
+#define SPECDEC_EINVAL 1
+#define SPECDEC_EHIP 2
+#define SPECDEC_EUNSUPPORTED 3
+
+#define SPECDEC_F32 0
+#define SPECDEC_F64 1
+#define SPECDEC_BF16 2
+
+/* ABI version; bumped whenever a signature below changes. */
+int specdec_abi_version(void);
+
+/* ---------------------------------------------------------------- accept --- */
+
+/* Temperature softmax, or one-hot argmax at temperature 0 (ties -> lowest id).
+ * logits [rows, vocab] (row_stride apart, dtype F32/F64/BF16) -> out fp32.
+ * Replaces lm/sampling.py:13-18 `probabilities`. */
+int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
+                          int64_t row_stride, float temperature, float *out,
+                          int64_t out_stride, void *stream);
+
+/* Fused accept-reject for a batch: gather p(x), q(x) of the drafted tokens,
+ * test u*q(x) < p(x), count the leading accepts n, build the residual
+ * norm(max(0, p[n] - q[n])) (q[k] is the implicit zero row, so n == k is the
+ * bonus token sampled from p[k]) and sample it by inverse CDF with u_residual.
+ * p [batch, k+1, vocab], q [batch, k, vocab] (dtype F32 or F64, strides in
+ * elements), draft int64 [batch, k], u_accept [batch, k] and u_residual [batch]
+ * of the same dtype as p.  out int64 [3, batch]: n_accepted, next_token, and
+ * a flag that is 1 when a drafted token had q(x) <= 0.
+ * Replaces spec/accept.py:44-79 `accept_reject` with the default residual
+ * (spec/accept.py:18-26) and spec/accept.py:29-35 `sample_inverse_cdf`. */
+int specdec_accept_reject(const void *p, const void *q, int dtype,
+                          int64_t p_batch_stride, int64_t p_row_stride,
+                          int64_t q_batch_stride, int64_t q_row_stride,
+                          const int64_t *draft, const void *u_accept,
+                          const void *u_residual, int64_t batch, int64_t k,
+                          int64_t vocab, int64_t *out, void *stream);
+
+/* First stage of accept-reject alone (for a caller-supplied residual):
+ * out int64 [2, batch]: n_accepted and the zero-q flag.
+ * Replaces spec/accept.py:65-71. */
+int specdec_accept_count(const void *p, const void *q, int dtype,
+                         int64_t p_batch_stride, int64_t p_row_stride,
+                         int64_t q_batch_stride, int64_t q_row_stride,
+                         const int64_t *draft, const void *u_accept, int64_t batch,
+                         int64_t k, int64_t *out, void *stream);
+
+/* Inverse-CDF sampling: token i is chosen iff u*total lies in
+ * [cdf[i-1], cdf[i]) with the prefix sums accumulated in fp64 and rounded to
+ * the element type (searchsorted right, clamped to vocab-1).
+ * probs [batch, vocab] (row_stride apart), u [batch] of the same dtype, out int64 [batch].
+ * Replaces spec/accept.py:29-35 `sample_inverse_cdf`. */
+int specdec_sample_inverse_cdf(const void *probs, int dtype, int64_t batch,
+                               int64_t vocab, int64_t row_stride, const void *u,
+                               int64_t *out, void *stream);
+
+/* out fp32 [n, vocab] = one_hot(ids[n], vocab).  Replaces the
+ * `one_hot(...).float()` of spec/ngram.py:23 and lm/sampling.py:17. */
+int specdec_one_hot(const int64_t *ids, int64_t n, int64_t vocab, float *out,
+                    void *stream);
+
+/* ----------------------------------------------------------------- n-gram --- */
+
+/* Prompt lookup for a batch of token histories.  history int32 [batch,
+ * row_stride], lengths int32 [batch] (>= 1).  For n = min(max_n, len-1) down
+ * to 1 the most recent earlier occurrence of the last n tokens is found; the
+ * k tokens that followed it are proposed, the copy reading its own output
+ * once it passes the end of the history.  Without a match the last token is
+ * repeated k times.  draft int64 [batch, k]; match int32 [batch, 2] = (start
+ * of the matched n-gram, n), or (-1, 0) when nothing matched.
+ * Replaces spec/ngram.py:32-45 `lookup` (and the per-row loop of :19-23). */
+int specdec_ngram_lookup(const int32_t *history, int64_t row_stride,
+                         const int32_t *lengths, int64_t batch, int32_t k,
+                         int32_t max_n, int64_t *draft, int32_t *match,
+                         void *stream);
+
+/* ------------------------------------------------------------------ cache --- */
+
+/* One batched pass of the LIFO block allocator.  free_stack int32
+ * [num_blocks] holds the free ids, top of stack at index top-1; used uint8
+ * [num_blocks] marks allocated blocks.  entries int32 [(n_push+n_pop), 4]
+ * rows of (table row, first column, count, stack offset):
+ *   push e (rollback / release, in order): for j < count
+ *       free_stack[top + off + j] = tables[row, col + j]; used[...] = 0
+ *   pop e (growth, after every push):      for j < count
+ *       tables[row, col + j] = free_stack[top + n_pushed - 1 - off - j]
+ * `popped` (optional, int32 [total popped]) receives the popped ids in order.
+ * Replaces cache/paged.py:28-40 (allocate/free) as driven by
+ * cache/paged.py:54-71 (grow_to/shrink_to) and cache/kv.py:79-87,114-118. */
+int specdec_block_plan(int32_t *tables, int64_t table_stride, int32_t *free_stack,
+                       uint8_t *used, int64_t num_blocks, int32_t top,
+                       const int32_t *entries, int32_t n_push, int32_t n_pop,
+                       int32_t *popped, void *stream);
+
+/* Single checked free: if used[block] is 0, status[0] = 1 and nothing changes
+ * (double free); otherwise the block is pushed at free_stack[top] and
+ * status[0] = 0.  Replaces cache/paged.py:36-40. */
+int specdec_block_free_checked(int32_t *free_stack, uint8_t *used,
+                               int64_t num_blocks, int32_t top, int32_t block,
+                               int32_t *status, void *stream);
+
+/* Slot ids of positions [start, stop) through one table row:
+ * out[i] = row[p / bs] * bs + p % bs.  Replaces cache/paged.py:73-76. */
+int specdec_block_slots(const int32_t *table_row, int64_t start, int64_t stop,
+                        int32_t block_size, int64_t *out, void *stream);
+
+/* The reference's slot map for one append (cache/kv.py:88-99): write int64
+ * [sum n_new] slots of the new tokens, write_index int64 [sum n_new] =
+ * b*width + j, read int64 [batch, read_width] (slot of every cached position,
+ * 0 past the row's total).  write_offsets int32 [batch] = exclusive scan of
+ * n_new. */
+int specdec_slot_map(const int32_t *tables, int64_t table_stride,
+                     const int32_t *meta, int32_t batch, int32_t block_size,
+                     int32_t width, int32_t read_width,
+                     const int32_t *write_offsets, int64_t *write,
+                     int64_t *write_index, int64_t *read, void *stream);
+
+/* Fused RoPE + cache append for one layer.  qkv [batch, width, (H + 2*Hkv) *
+ * head_dim] (token_stride elements between tokens; q heads, then k heads,
+ * then v heads).  For every real token (t < n_new[b]) at position
+ * past[b] + t: q and k are rotated in place (HF rotate_half convention, cos
+ * and sin fp32 tables [max_positions, head_dim/2]) and k, v are written into
+ * the layer's paged pools at the slot given by the block table.
+ * Replaces lm/forward.py:53,60 (rotary) + cache/kv.py:101-106 (write). */
+int specdec_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t n_heads,
+                        int32_t n_kv_heads, int32_t head_dim, const float *cos_table,
+                        const float *sin_table, int64_t max_positions,
+                        const int32_t *meta, int32_t batch, int32_t width,
+                        const int32_t *tables, int64_t table_stride,
+                        int32_t block_size, void *k_pool, void *v_pool, void *stream);
+
+/* Cache append without rotation: k, v [batch, Hkv, width, head_dim]
+ * contiguous (the reference's write() argument layout).
+ * Replaces cache/kv.py:101-106. */
+int specdec_kv_write(const void *k, const void *v, int dtype, int32_t n_kv_heads,
+                     int32_t head_dim, const int32_t *meta, int32_t batch,
+                     int32_t width, const int32_t *tables, int64_t table_stride,
+                     int32_t block_size, void *k_pool, void *v_pool, void *stream);
+
+/* Copy of every cached position, k_out/v_out [batch, Hkv, read_width,
+ * head_dim] (zeros past each row's total).  Diagnostic counterpart of
+ * cache/kv.py:108-112; the attention kernel reads blocks in place instead. */
+int specdec_kv_gather(const void *k_pool, const void *v_pool, int dtype,
+                      int32_t n_kv_heads, int32_t head_dim, const int32_t *meta,
+                      int32_t batch, const int32_t *tables, int64_t table_stride,
+                      int32_t block_size, int32_t read_width, void *k_out,
+                      void *v_out, void *stream);
+
+/* -------------------------------------------------------------- attention --- */
+
+/* Workspace needed by specdec_paged_attention for a call shape: `floats`
+ * fp32 elements of split partials and `counters` int32 arrival counters (the
+ * counters must be zero before the first call; the kernel leaves them zero). */
+int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
+                                int32_t n_kv_heads, int32_t head_dim,
+                                int32_t max_kv_len, int32_t split_tokens,
+                                int64_t *floats, int64_t *counters);
+
+/* Split-KV size the attention kernel uses for a call shape (tokens per
+ * workgroup; a fixed 256 whenever all queries of a kv head fit one 16-row
+ * tile, so that a query's reduction order does not depend on how many
+ * tokens are verified with it). */
+int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
+                            int32_t n_kv_heads, int32_t max_kv_len);
+
+/* Causal paged attention of `width` new query tokens per row over the paged
+ * cache (keys 0 .. past+t for query t, read through the block table in
+ * place).  q token (b, t), head h at q + (b*width + t)*q_token_stride +
+ * h*head_dim; out likewise with out_token_stride.  Softmax in fp32 with
+ * `scale`; QK^T and PV on MFMA (bf16) or fp32 MFMA (F32).  Query rows with
+ * t >= n_new[b] are not written.  head_dim must be 64.
+ * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
+ * cache/kv.py:108-112. */
+int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
+                            const void *k_pool, const void *v_pool,
+                            const int32_t *tables, int64_t table_stride,
+                            const int32_t *meta, int32_t batch, int32_t width,
+                            int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                            int32_t block_size, float scale, int32_t max_kv_len,
+                            float *workspace, int64_t workspace_floats,
+                            int32_t *counters, int64_t n_counters, void *out,
+                            int64_t out_token_stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECDEC_H */

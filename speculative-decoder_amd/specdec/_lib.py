@@ -1,0 +1,67 @@
+"""ctypes binding of libspecdec.so.  Every symbol of include/specdec.h is
+declared here with its argument types; `lib()` loads the library once."""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libspecdec.so")
+
+P = c_void_p
+I32 = c_int32
+I64 = c_int64
+
+# name -> argument types (all return int)
+SIGNATURES: dict[str, list] = {
+    "specdec_abi_version": [],
+    "specdec_probabilities": [P, c_int, I64, I64, I64, c_float, P, I64, P],
+    "specdec_accept_reject": [P, P, c_int, I64, I64, I64, I64, P, P, P, I64, I64, I64, P, P],
+    "specdec_accept_count": [P, P, c_int, I64, I64, I64, I64, P, P, I64, I64, P, P],
+    "specdec_sample_inverse_cdf": [P, c_int, I64, I64, I64, P, P, P],
+    "specdec_one_hot": [P, I64, I64, P, P],
+    "specdec_ngram_lookup": [P, I64, P, I64, I32, I32, P, P, P],
+    "specdec_block_plan": [P, I64, P, P, I64, I32, P, I32, I32, P, P],
+    "specdec_block_free_checked": [P, P, I64, I32, I32, P, P],
+    "specdec_block_slots": [P, I64, I64, I32, P, P],
+    "specdec_slot_map": [P, I64, P, I32, I32, I32, I32, P, P, P, P, P],
+    "specdec_rope_append": [P, c_int, I64, I32, I32, I32, P, P, I64, P, I32, I32, P, I64, I32, P, P, P],
+    "specdec_kv_write": [P, P, c_int, I32, I32, P, I32, I32, P, I64, I32, P, P, P],
+    "specdec_kv_gather": [P, P, c_int, I32, I32, P, I32, P, I64, I32, I32, P, P, P],
+    "specdec_attention_workspace": [I32, I32, I32, I32, I32, I32, I32, P, P],
+    "specdec_attention_split": [I32, I32, I32, I32, I32],
+    "specdec_paged_attention": [P, c_int, I64, P, P, P, I64, P, I32, I32, I32, I32, I32, I32, c_float,
+                                I32, P, I64, P, I64, P, I64, P],
+}
+
+ABI_VERSION = 1
+_lib: ctypes.CDLL | None = None
+
+
+def available() -> bool:
+    return LIB_PATH.exists()
+
+
+def load(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """Load the library and declare every entry point (no GPU needed)."""
+    handle = ctypes.CDLL(str(path))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = c_int
+    version = handle.specdec_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    return handle
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: the hot path has no CPU fallback. "
+                "Build it with `python speculative-decoder_amd/specdec/build.py`."
+            )
+        _lib = load()
+    return _lib

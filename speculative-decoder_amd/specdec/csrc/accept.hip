@@ -1,0 +1,331 @@
+// Accept-reject kernels: temperature softmax / one-hot argmax, the fused
+// accept test + residual + inverse-CDF sample, the accept stage alone, the
+// inverse-CDF sampler alone, and a one-hot writer.
+//
+// Reference semantics: lm/sampling.py:13-18 (probabilities),
+// spec/accept.py:18-26 (residual), :29-35 (inverse CDF), :44-79 (accept).
+//
+// Layout: one workgroup per row (softmax) or per batch entry (accept), the
+// vocab split into contiguous per-thread chunks so the inverse-CDF scan is a
+// chunk sum, a workgroup exclusive scan of the chunk sums, and a re-walk of
+// each chunk.  The vocab rows are streamed from HBM; re-reads of the same
+// row within one workgroup hit L2.
+#include "common.h"
+
+#include <float.h>
+#include <math.h>
+
+namespace specdec {
+
+constexpr int kAcceptThreads = 1024;
+constexpr int kSoftmaxThreads = 1024;
+
+template <typename T> struct Tiny;
+template <> struct Tiny<float> { static constexpr float v = FLT_MIN; };
+template <> struct Tiny<double> { static constexpr double v = DBL_MIN; };
+
+// Round an fp64 running sum to the element type: prefixes of an fp32 cumsum
+// are accumulated in fp64 and rounded once per prefix.
+__device__ __forceinline__ float round_to(double x, float) { return static_cast<float>(x); }
+__device__ __forceinline__ double round_to(double x, double) { return x; }
+
+// ------------------------------------------------------------ softmax ----
+template <typename TIn>
+__global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
+    const TIn *__restrict__ logits, int64_t row_stride, int64_t vocab, float temperature,
+    float *__restrict__ out, int64_t out_stride) {
+  __shared__ float red_f[kSoftmaxThreads / kWave];
+  __shared__ int red_i[kSoftmaxThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const TIn *x = logits + row * row_stride;
+  float *y = out + row * out_stride;
+  const int tid = threadIdx.x;
+
+  if (temperature == 0.0f) {
+    // argmax of the raw logits, first index among equal maxima
+    float best = -INFINITY;
+    int best_i = INT32_MAX;
+    for (int64_t i = tid; i < vocab; i += blockDim.x) {
+      float v = to_f32(x[i]);
+      if (v > best || (v == best && i < best_i)) { best = v; best_i = (int)i; }
+    }
+    // wave level
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+      float ov = __shfl_xor(best, o, kWave);
+      int oi = __shfl_xor(best_i, o, kWave);
+      if (ov > best || (ov == best && oi < best_i)) { best = ov; best_i = oi; }
+    }
+    const int lane = tid & (kWave - 1), wid = tid / kWave;
+    if (lane == 0) { red_f[wid] = best; red_i[wid] = best_i; }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < (int)(blockDim.x / kWave); ++w) {
+        if (red_f[w] > best || (red_f[w] == best && red_i[w] < best_i)) {
+          best = red_f[w]; best_i = red_i[w];
+        }
+      }
+      red_i[0] = best_i;
+    }
+    __syncthreads();
+    const int hot = red_i[0];
+    for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = (i == hot) ? 1.0f : 0.0f;
+    return;
+  }
+
+  // logits.float() / T, then a max-shifted softmax with fp32 exp and sum
+  float m = -INFINITY;
+  for (int64_t i = tid; i < vocab; i += blockDim.x) m = fmaxf(m, to_f32(x[i]) / temperature);
+  m = block_max(m, red_f);
+  float s = 0.0f;
+  for (int64_t i = tid; i < vocab; i += blockDim.x) s += expf(to_f32(x[i]) / temperature - m);
+  s = block_sum(s, red_f);
+  for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = expf(to_f32(x[i]) / temperature - m) / s;
+}
+
+// ------------------------------------------- accept stage (per batch) ----
+// Leading-accept count and the zero-q flag for batch entry b.  Runs on one
+// thread; k is small (the draft length).
+template <typename T>
+__device__ __forceinline__ void accept_stage(const T *p, const T *q, int64_t p_bs, int64_t p_rs,
+                                             int64_t q_bs, int64_t q_rs, const int64_t *draft,
+                                             const T *u_accept, int64_t b, int64_t k, int64_t vocab,
+                                             int64_t *n_out, int64_t *bad_out) {
+  int64_t n = k, bad = 0;
+  for (int64_t t = 0; t < k; ++t) {
+    const int64_t x = draft[b * k + t];
+    if (x < 0 || x >= vocab) { bad = 1; n = (n == k) ? t : n; continue; }
+    const T px = p[b * p_bs + t * p_rs + x];
+    const T qx = q[b * q_bs + t * q_rs + x];
+    if (!(qx > T(0))) bad = 1;
+    const T u = u_accept[b * k + t];
+    // u < p/q written as a product, as the reference does
+    if (n == k && !(u * qx < px)) n = t;
+  }
+  *n_out = n;
+  *bad_out = bad;
+}
+
+// Inverse-CDF sample of one row whose element i is produced by `elem(i)`.
+// Thread chunks are contiguous so the scan order is: fp64 chunk sums, an
+// fp64 workgroup scan over chunks, then a sequential fp64 walk per chunk,
+// each prefix rounded to T and compared against target = T(u * cdf[-1]).
+template <typename T, typename Elem>
+__device__ int64_t inverse_cdf_row(Elem elem, int64_t vocab, T u, double *scratch) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t chunk = (vocab + nt - 1) / nt;
+  const int64_t lo = min<int64_t>((int64_t)tid * chunk, vocab);
+  const int64_t hi = min<int64_t>(lo + chunk, vocab);
+  double local = 0.0;
+  for (int64_t i = lo; i < hi; ++i) local += (double)elem(i);
+  double total;
+  const double prefix = block_exclusive_scan(local, scratch, &total);
+  const T last = round_to(total, T());
+  const T target = u * last;
+  // count prefixes <= target; cdf is monotone, so this is searchsorted(right)
+  int64_t count = 0;
+  double acc = prefix;
+  for (int64_t i = lo; i < hi; ++i) {
+    acc += (double)elem(i);
+    if (round_to(acc, T()) <= target) ++count;
+  }
+  __syncthreads();
+  const double all = block_sum((double)count, scratch);
+  int64_t idx = (int64_t)all;
+  return idx > vocab - 1 ? vocab - 1 : idx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kAcceptThreads) void accept_reject_kernel(
+    const T *__restrict__ p, const T *__restrict__ q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
+    int64_t q_rs, const int64_t *__restrict__ draft, const T *__restrict__ u_accept,
+    const T *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab,
+    int64_t *__restrict__ out) {
+  __shared__ double scratch[kAcceptThreads / kWave + 1];
+  __shared__ int64_t s_n;
+  const int64_t b = blockIdx.x;
+  if (threadIdx.x == 0) {
+    int64_t n, bad;
+    accept_stage(p, q, p_bs, p_rs, q_bs, q_rs, draft, u_accept, b, k, vocab, &n, &bad);
+    s_n = n;
+    out[b] = n;
+    out[2 * batch + b] = bad;
+  }
+  __syncthreads();
+  const int64_t n = s_n;
+  const T *pr = p + b * p_bs + n * p_rs;
+  const T *qr = (n < k) ? q + b * q_bs + n * q_rs : nullptr;  // zero row at n == k
+
+  // total = sum(max(0, p - q)), accumulated in fp64 and rounded once
+  double local = 0.0;
+  for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) {
+    T r = qr ? pr[i] - qr[i] : pr[i];
+    local += (double)(r > T(0) ? r : T(0));
+  }
+  const double tot64 = block_sum(local, scratch);
+  const T total = round_to(tot64, T());
+  const T denom = total > Tiny<T>::v ? total : Tiny<T>::v;
+  const bool use_residual = total > T(0);
+  __syncthreads();
+
+  auto elem = [=](int64_t i) -> T {
+    if (!use_residual) return pr[i];
+    T r = qr ? pr[i] - qr[i] : pr[i];
+    r = r > T(0) ? r : T(0);
+    return r / denom;
+  };
+  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u_residual[b], scratch);
+  if (threadIdx.x == 0) out[batch + b] = idx;
+}
+
+template <typename T>
+__global__ void accept_count_kernel(const T *__restrict__ p, const T *__restrict__ q, int64_t p_bs,
+                                    int64_t p_rs, int64_t q_bs, int64_t q_rs,
+                                    const int64_t *__restrict__ draft,
+                                    const T *__restrict__ u_accept, int64_t batch, int64_t k,
+                                    int64_t vocab, int64_t *__restrict__ out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  int64_t n, bad;
+  accept_stage(p, q, p_bs, p_rs, q_bs, q_rs, draft, u_accept, b, k, vocab, &n, &bad);
+  out[b] = n;
+  out[batch + b] = bad;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_kernel(
+    const T *__restrict__ probs, int64_t vocab, int64_t row_stride, const T *__restrict__ u,
+    int64_t *__restrict__ out) {
+  __shared__ double scratch[kAcceptThreads / kWave + 1];
+  const int64_t b = blockIdx.x;
+  const T *row = probs + b * row_stride;
+  auto elem = [=](int64_t i) -> T { return row[i]; };
+  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u[b], scratch);
+  if (threadIdx.x == 0) out[b] = idx;
+}
+
+__global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64_t vocab,
+                               float *__restrict__ out) {
+  const int64_t total = n * vocab;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / vocab, c = i - r * vocab;
+    out[i] = (ids[r] == c) ? 1.0f : 0.0f;
+  }
+}
+
+}  // namespace specdec
+
+using namespace specdec;
+
+SPECDEC_API int specdec_abi_version(void) { return 1; }
+
+SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
+                                      int64_t row_stride, float temperature, float *out,
+                                      int64_t out_stride, void *stream) {
+  if (rows < 0 || vocab <= 0 || vocab > INT32_MAX || temperature < 0.0f) return SPECDEC_EINVAL;
+  if (rows == 0) return SPECDEC_OK;
+  if (!logits || !out) return SPECDEC_EINVAL;
+  dim3 grid((unsigned)rows), block(kSoftmaxThreads);
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case SPECDEC_F32:
+      probabilities_kernel<float><<<grid, block, 0, s>>>((const float *)logits, row_stride, vocab,
+                                                        temperature, out, out_stride);
+      break;
+    case SPECDEC_F64:
+      probabilities_kernel<double><<<grid, block, 0, s>>>((const double *)logits, row_stride,
+                                                         vocab, temperature, out, out_stride);
+      break;
+    case SPECDEC_BF16:
+      probabilities_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
+          (const __hip_bfloat16 *)logits, row_stride, vocab, temperature, out, out_stride);
+      break;
+    default: return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
+                                      int64_t p_batch_stride, int64_t p_row_stride,
+                                      int64_t q_batch_stride, int64_t q_row_stride,
+                                      const int64_t *draft, const void *u_accept,
+                                      const void *u_residual, int64_t batch, int64_t k,
+                                      int64_t vocab, int64_t *out, void *stream) {
+  if (batch < 0 || k < 0 || vocab <= 0) return SPECDEC_EINVAL;
+  if (batch == 0) return SPECDEC_OK;
+  if (!p || !out || !u_residual || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
+  dim3 grid((unsigned)batch), block(kAcceptThreads);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_F32) {
+    accept_reject_kernel<float><<<grid, block, 0, s>>>(
+        (const float *)p, (const float *)q, p_batch_stride, p_row_stride, q_batch_stride,
+        q_row_stride, draft, (const float *)u_accept, (const float *)u_residual, batch, k, vocab,
+        out);
+  } else if (dtype == SPECDEC_F64) {
+    accept_reject_kernel<double><<<grid, block, 0, s>>>(
+        (const double *)p, (const double *)q, p_batch_stride, p_row_stride, q_batch_stride,
+        q_row_stride, draft, (const double *)u_accept, (const double *)u_residual, batch, k,
+        vocab, out);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_accept_count(const void *p, const void *q, int dtype,
+                                     int64_t p_batch_stride, int64_t p_row_stride,
+                                     int64_t q_batch_stride, int64_t q_row_stride,
+                                     const int64_t *draft, const void *u_accept, int64_t batch,
+                                     int64_t k, int64_t *out, void *stream) {
+  if (batch < 0 || k < 0) return SPECDEC_EINVAL;
+  if (batch == 0) return SPECDEC_OK;
+  if (!p || !out || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
+  // vocab is only used to range-check draft ids; the caller validated them
+  const int64_t vocab = INT64_MAX;
+  dim3 block(64), grid((unsigned)((batch + 63) / 64));
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_F32) {
+    accept_count_kernel<float><<<grid, block, 0, s>>>(
+        (const float *)p, (const float *)q, p_batch_stride, p_row_stride, q_batch_stride,
+        q_row_stride, draft, (const float *)u_accept, batch, k, vocab, out);
+  } else if (dtype == SPECDEC_F64) {
+    accept_count_kernel<double><<<grid, block, 0, s>>>(
+        (const double *)p, (const double *)q, p_batch_stride, p_row_stride, q_batch_stride,
+        q_row_stride, draft, (const double *)u_accept, batch, k, vocab, out);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_sample_inverse_cdf(const void *probs, int dtype, int64_t batch,
+                                           int64_t vocab, int64_t row_stride, const void *u,
+                                           int64_t *out, void *stream) {
+  if (batch < 0 || vocab <= 0) return SPECDEC_EINVAL;
+  if (batch == 0) return SPECDEC_OK;
+  if (!probs || !u || !out) return SPECDEC_EINVAL;
+  dim3 grid((unsigned)batch), block(kAcceptThreads);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_F32) {
+    sample_inverse_cdf_kernel<float><<<grid, block, 0, s>>>((const float *)probs, vocab,
+                                                           row_stride, (const float *)u, out);
+  } else if (dtype == SPECDEC_F64) {
+    sample_inverse_cdf_kernel<double><<<grid, block, 0, s>>>((const double *)probs, vocab,
+                                                            row_stride, (const double *)u, out);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_one_hot(const int64_t *ids, int64_t n, int64_t vocab, float *out,
+                                void *stream) {
+  if (n < 0 || vocab <= 0) return SPECDEC_EINVAL;
+  if (n == 0) return SPECDEC_OK;
+  if (!ids || !out) return SPECDEC_EINVAL;
+  const int64_t total = n * vocab;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65535) blocks = 65535;
+  one_hot_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_stream(stream)>>>(ids, n, vocab, out);
+  return launch_status();
+}

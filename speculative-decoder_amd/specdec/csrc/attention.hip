@@ -1,0 +1,512 @@
+// Causal paged verify attention on gfx950 MFMA.
+//
+// Reference semantics: lm/forward.py:44-49 (positions and the mask
+// "key j visible to query t iff j <= past+t and j < total") and :62-63
+// (gather of every cached K/V, then scaled_dot_product_attention).  Here the
+// blocks are read in place through the block table.
+//
+// Work split: grid.x = (batch, kv head, 16-row query tile), grid.y = KV
+// split of `split` tokens; 4 waves per workgroup, each wave walking its
+// quarter of the split in 32-token chunks (two 16-token groups).
+//
+// Per chunk and wave, with lane = 16*g + c (g = lane/16, c = lane%16):
+//   S^T[token, query] = K . Q^T      A = K rows (token c, dims 32kk+8g..+7)
+//                                    B = Q^T    (query c, same dims)
+//   D layout: lane holds S^T[4g+i, c], i = 0..3, i.e. 4 tokens of query c
+//   online softmax per query column (fp32), p = exp(s - m)
+//   O^T[dim, query] += V^T . P^T     A = V^T rows (dim c+16t, tokens of g)
+//                                    B = P^T (the lane's own 8 p values)
+// The MFMA k index of lane group g is mapped to tokens {4g..4g+3} of the
+// first group and {4g..4g+3} of the second, so P^T comes straight out of the
+// S^T accumulators and V^T is read as two 8-byte runs from the dim-major V
+// tile.  All per-query statistics live in lane column c, so the running
+// rescale is lane-local.
+//
+// Splits are combined through a workspace by the last workgroup of each
+// (batch, head, tile) to arrive (atomic counter, reset by that workgroup).
+// Every query's reduction order depends only on the absolute key positions,
+// never on how many queries share the call, so a token verified among k+1
+// gets the same bits as the same token decoded alone.
+#include "common.h"
+
+#include <math.h>
+
+namespace specdec {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+constexpr int kD = 64;            // head dim
+constexpr int kAttnThreads = 256;  // 4 waves
+constexpr int kRows = 16;          // query rows per tile
+constexpr int kDefaultSplit = 256;
+
+struct AttnArgs {
+  const void *q;
+  int64_t q_stride;
+  const void *k;
+  const void *v;
+  const int32_t *tables;
+  int64_t table_stride;
+  const int32_t *meta;
+  int batch, width, H, Hkv, bs;
+  float scale;
+  int split, max_splits, n_qtiles;
+  float *ws;
+  int32_t *counters;
+  void *out;
+  int64_t out_stride;
+};
+
+struct TileInfo {
+  int b, h, qt, group, row, past, nrows, kv_len, nsplit, unit;
+};
+
+__device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti) {
+  const int unit = blockIdx.x;
+  ti.unit = unit;
+  ti.qt = unit % a.n_qtiles;
+  const int bh = unit / a.n_qtiles;
+  ti.h = bh % a.Hkv;
+  ti.b = bh / a.Hkv;
+  ti.group = a.H / a.Hkv;
+  ti.row = a.meta[ti.b];
+  ti.past = a.meta[a.batch + ti.b];
+  const int nnew = a.meta[2 * a.batch + ti.b];
+  ti.nrows = nnew * ti.group;
+  const int r0 = ti.qt * kRows;
+  if (r0 >= ti.nrows) return false;
+  const int t_hi = min(r0 + kRows - 1, ti.nrows - 1) / ti.group;
+  ti.kv_len = ti.past + t_hi + 1;
+  ti.nsplit = (ti.kv_len + a.split - 1) / a.split;
+  if ((int)blockIdx.y >= ti.nsplit || ti.nsplit > a.max_splits) return false;
+  return true;
+}
+
+__device__ __forceinline__ int64_t block_of(const AttnArgs &a, const TileInfo &ti, int pos) {
+  return a.tables[(int64_t)ti.row * a.table_stride + pos / a.bs];
+}
+
+template <typename T> __device__ __forceinline__ float elem_f32(const T *p) { return to_f32(*p); }
+
+// Combine the 4 waves of this workgroup, then the splits (last arriving
+// workgroup), and write the normalised output rows.
+template <typename T>
+__device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
+  __shared__ float s_m[4][kRows], s_l[4][kRows];
+  __shared__ float s_o[4][kRows][kD + 1];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  if (g == 0) {
+    s_m[wave][c] = m;
+    s_l[wave][c] = l;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_o[wave][c][16 * t + 4 * g + i] = o[t][i];
+  __syncthreads();
+
+  float wm[4], wl[4], wo[4];
+  int qs[4], ds[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + kAttnThreads * j;
+    const int qq = idx >> 6, d = idx & 63;
+    qs[j] = qq;
+    ds[j] = d;
+    float M = s_m[0][qq];
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
+    float L = 0.0f, O = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+      const float mw = s_m[w][qq];
+      const float f = (mw == -INFINITY) ? 0.0f : expf(mw - M);
+      L += f * s_l[w][qq];
+      O += f * s_o[w][qq][d];
+    }
+    wm[j] = M;
+    wl[j] = L;
+    wo[j] = O;
+  }
+
+  T *out = reinterpret_cast<T *>(a.out);
+  const int r0 = ti.qt * kRows;
+  auto store = [&](int qq, int d, float val) {
+    const int r = r0 + qq;
+    if (r >= ti.nrows) return;
+    const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
+    out[((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d] = from_f32<T>(val);
+  };
+
+  if (ti.nsplit == 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store(qs[j], ds[j], wo[j] / wl[j]);
+    return;
+  }
+
+  // split partial: O[16][64] then (m, l)[16]
+  const int64_t base = ((int64_t)ti.unit * a.max_splits + blockIdx.y) * (kRows * (kD + 2));
+  float *ws = a.ws + base;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ws[qs[j] * kD + ds[j]] = wo[j];
+    if (ds[j] == 0) {
+      ws[kRows * kD + 2 * qs[j]] = wm[j];
+      ws[kRows * kD + 2 * qs[j] + 1] = wl[j];
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = (atomicAdd(&a.counters[ti.unit], 1) == ti.nsplit - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * (kRows * (kD + 2));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int qq = qs[j], d = ds[j];
+    float M = -INFINITY;
+    for (int s = 0; s < ti.nsplit; ++s)
+      M = fmaxf(M, __builtin_nontemporal_load(ws0 + s * (kRows * (kD + 2)) + kRows * kD + 2 * qq));
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < ti.nsplit; ++s) {
+      const float *p = ws0 + s * (kRows * (kD + 2));
+      const float ms = __builtin_nontemporal_load(p + kRows * kD + 2 * qq);
+      const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+      L += f * __builtin_nontemporal_load(p + kRows * kD + 2 * qq + 1);
+      O += f * __builtin_nontemporal_load(p + qq * kD + d);
+    }
+    store(qq, d, O / L);
+  }
+  if (tid == 0) a.counters[ti.unit] = 0;
+}
+
+// Online-softmax update shared by both element types.  sv[8]: scaled,
+// masked scores of this lane's 8 tokens (-inf where not visible).
+__device__ __forceinline__ float online_update(float (&sv)[8], float &m, float &l, f32x4 (&o)[4]) {
+  float cm = sv[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) cm = fmaxf(cm, sv[j]);
+  cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+  cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+  const float m_new = fmaxf(m, cm);
+  const float alpha = (m == -INFINITY) ? 0.0f : expf(m - m_new);
+  float ps = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    sv[j] = (sv[j] == -INFINITY) ? 0.0f : expf(sv[j] - m_new);
+    ps += sv[j];
+  }
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  l = l * alpha + ps;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] *= alpha;
+  m = m_new;
+  return alpha;
+}
+
+// ---------------------------------------------------------------- bf16 ----
+template <bool BS16>
+__global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a) {
+  TileInfo ti;
+  if (!tile_info(a, ti)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int r = ti.qt * kRows + c;
+  const bool row_ok = r < ti.nrows;
+  const int t = row_ok ? r / ti.group : 0;
+  const int hq = ti.h * ti.group + (row_ok ? r % ti.group : 0);
+  const int qpos = ti.past + t;
+
+  typedef unsigned short u16;
+  const u16 *kp = reinterpret_cast<const u16 *>(a.k);
+  const u16 *vp = reinterpret_cast<const u16 *>(a.v);
+  const u16 *qrow =
+      reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
+
+  bf16x8 qop[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (row_ok) raw = *reinterpret_cast<const u32x4 *>(qrow + 32 * kk + 8 * g);
+    qop[kk] = __builtin_bit_cast(bf16x8, raw);
+  }
+
+  f32x4 o[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  const int Hkv = a.Hkv, bs = a.bs;
+  const int wave_tokens = a.split / 4;
+  const int w_lo = blockIdx.y * a.split + wave * wave_tokens;
+  const int w_hi = min(w_lo + wave_tokens, ti.kv_len);
+
+  for (int c0 = w_lo; c0 < w_hi; c0 += 32) {
+    u32x4 kraw[2][2];
+    u32x2 vraw[2][4];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int gs = c0 + 16 * gi;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) kraw[gi][kk] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) vraw[gi][tt] = u32x2{0u, 0u};
+      if (gs >= ti.kv_len) continue;
+      if (BS16) {
+        // the 16-token group lies inside one block
+        const int64_t blk = block_of(a, ti, gs);
+        const int off = gs % bs;
+        const u16 *kb = kp + ((blk * Hkv + ti.h) * bs + off + c) * kD;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) kraw[gi][kk] = *reinterpret_cast<const u32x4 *>(kb + 32 * kk + 8 * g);
+        const u16 *vb = vp + (blk * Hkv + ti.h) * (int64_t)kD * bs + off + 4 * g;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          vraw[gi][tt] = *reinterpret_cast<const u32x2 *>(vb + (int64_t)(16 * tt + c) * bs);
+      } else {
+        const int pos = gs + c;
+        if (pos < ti.kv_len) {
+          const int64_t blk = block_of(a, ti, pos);
+          const u16 *kb = kp + ((blk * Hkv + ti.h) * bs + pos % bs) * kD;
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const u16 *src = kb + 32 * kk + 8 * g;
+            unsigned int w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (unsigned)src[2 * e] | ((unsigned)src[2 * e + 1] << 16);
+            kraw[gi][kk] = u32x4{w[0], w[1], w[2], w[3]};
+          }
+        }
+        u16 vv[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int vpos = gs + 4 * g + i;
+          const bool ok = vpos < ti.kv_len;
+          const int64_t blk = ok ? block_of(a, ti, vpos) : 0;
+          const u16 *vb = vp + (blk * Hkv + ti.h) * (int64_t)kD * bs + vpos % bs;
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) vv[tt][i] = ok ? vb[(int64_t)(16 * tt + c) * bs] : (u16)0;
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          vraw[gi][tt] = u32x2{(unsigned)vv[tt][0] | ((unsigned)vv[tt][1] << 16),
+                               (unsigned)vv[tt][2] | ((unsigned)vv[tt][3] << 16)};
+      }
+    }
+
+    float sv[8];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[gi][0]), qop[0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[gi][1]), qop[1], s, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = c0 + 16 * gi + 4 * g + i;
+        const bool ok = row_ok && pos <= qpos && pos < ti.kv_len;
+        sv[4 * gi + i] = ok ? s[i] * a.scale : -INFINITY;
+      }
+    }
+    online_update(sv, m, l, o);
+
+    bf16x8 pop;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[j];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      u32x4 vr = u32x4{vraw[0][tt][0], vraw[0][tt][1], vraw[1][tt][0], vraw[1][tt][1]};
+      o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr), pop, o[tt], 0, 0, 0);
+    }
+  }
+  finish<__hip_bfloat16>(a, ti, m, l, o);
+}
+
+// ---------------------------------------------------------------- fp32 ----
+// Same structure on v_mfma_f32_16x16x4_f32: per 16-token group the k index
+// of lane group g is dim 16g+s at step s (QK^T) and token 4g+i at step i (PV).
+template <bool BS16>
+__global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a) {
+  TileInfo ti;
+  if (!tile_info(a, ti)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int r = ti.qt * kRows + c;
+  const bool row_ok = r < ti.nrows;
+  const int t = row_ok ? r / ti.group : 0;
+  const int hq = ti.h * ti.group + (row_ok ? r % ti.group : 0);
+  const int qpos = ti.past + t;
+
+  const float *kp = reinterpret_cast<const float *>(a.k);
+  const float *vp = reinterpret_cast<const float *>(a.v);
+  const float *qrow =
+      reinterpret_cast<const float *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
+  float qv[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) qv[s] = row_ok ? qrow[16 * g + s] : 0.0f;
+
+  f32x4 o[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  const int Hkv = a.Hkv, bs = a.bs;
+  const int wave_tokens = a.split / 4;
+  const int w_lo = blockIdx.y * a.split + wave * wave_tokens;
+  const int w_hi = min(w_lo + wave_tokens, ti.kv_len);
+
+  for (int c0 = w_lo; c0 < w_hi; c0 += 32) {
+    float sv[8];
+    float vv[2][4][4];  // [group][tile][token i]
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int gs = c0 + 16 * gi;
+      float kv[16];
+#pragma unroll
+      for (int s = 0; s < 16; ++s) kv[s] = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[gi][tt][i] = 0.0f;
+      if (gs < ti.kv_len) {
+        const int pos = gs + c;
+        if (BS16 || pos < ti.kv_len) {
+          const int64_t blk = block_of(a, ti, BS16 ? gs : pos);
+          const float *kb = kp + ((blk * Hkv + ti.h) * bs + (BS16 ? gs % bs + c : pos % bs)) * kD + 16 * g;
+#pragma unroll
+          for (int s = 0; s < 16; ++s) kv[s] = kb[s];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int vpos = gs + 4 * g + i;
+          const bool ok = BS16 || vpos < ti.kv_len;
+          const int64_t blk = ok ? block_of(a, ti, vpos) : 0;
+          const float *vb = vp + (blk * Hkv + ti.h) * (int64_t)kD * bs + vpos % bs;
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) vv[gi][tt][i] = ok ? vb[(int64_t)(16 * tt + c) * bs] : 0.0f;
+        }
+      }
+      f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 16; ++s) s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[s], qv[s], s4, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = gs + 4 * g + i;
+        const bool ok = row_ok && pos <= qpos && pos < ti.kv_len;
+        sv[4 * gi + i] = ok ? s4[i] * a.scale : -INFINITY;
+      }
+    }
+    online_update(sv, m, l, o);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[gi][tt][i], sv[4 * gi + i], o[tt], 0, 0, 0);
+  }
+  finish<float>(a, ti, m, l, o);
+}
+
+inline int qtiles(int width, int H, int Hkv) { return (width * (H / Hkv) + kRows - 1) / kRows; }
+
+inline int choose_split(int batch, int width, int H, int Hkv, int max_kv_len) {
+  const int nqt = qtiles(width, H, Hkv);
+  if (nqt == 1) return kDefaultSplit;
+  // many query tiles (prefill): fewer, longer splits keep the workspace small
+  const int64_t units = (int64_t)batch * Hkv * nqt;
+  const int want = units >= 1024 ? 1 : (int)((2048 + units - 1) / units);
+  int split = (max_kv_len + want - 1) / want;
+  split = ((split + 127) / 128) * 128;
+  return split < kDefaultSplit ? kDefaultSplit : split;
+}
+
+}  // namespace specdec
+
+using namespace specdec;
+
+SPECDEC_API int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
+                                        int32_t n_kv_heads, int32_t max_kv_len) {
+  if (batch <= 0 || width <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) return -1;
+  return choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
+}
+
+SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
+                                            int32_t n_kv_heads, int32_t head_dim,
+                                            int32_t max_kv_len, int32_t split_tokens,
+                                            int64_t *floats, int64_t *counters) {
+  if (!floats || !counters || batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 ||
+      n_heads % n_kv_heads || max_kv_len < 0)
+    return SPECDEC_EINVAL;
+  if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
+  if (split_tokens <= 0)
+    split_tokens = choose_split(batch > 0 ? batch : 1, width > 0 ? width : 1, n_heads, n_kv_heads,
+                                max_kv_len);
+  const int64_t units = (int64_t)batch * n_kv_heads * qtiles(width, n_heads, n_kv_heads);
+  const int64_t splits = (max_kv_len + split_tokens - 1) / split_tokens;
+  *floats = units * splits * kRows * (kD + 2);
+  *counters = units;
+  return SPECDEC_OK;
+}
+
+SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
+                                        const void *k_pool, const void *v_pool,
+                                        const int32_t *tables, int64_t table_stride,
+                                        const int32_t *meta, int32_t batch, int32_t width,
+                                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                        int32_t block_size, float scale, int32_t max_kv_len,
+                                        float *workspace, int64_t workspace_floats,
+                                        int32_t *counters, int64_t n_counters, void *out,
+                                        int64_t out_token_stride, void *stream) {
+  if (batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads ||
+      block_size <= 0 || max_kv_len < 0)
+    return SPECDEC_EINVAL;
+  if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
+  if (batch == 0 || width == 0 || max_kv_len == 0) return SPECDEC_OK;
+  if (!q || !k_pool || !v_pool || !tables || !meta || !out) return SPECDEC_EINVAL;
+  AttnArgs a;
+  a.q = q;
+  a.q_stride = q_token_stride;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.meta = meta;
+  a.batch = batch;
+  a.width = width;
+  a.H = n_heads;
+  a.Hkv = n_kv_heads;
+  a.bs = block_size;
+  a.scale = scale;
+  a.split = choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
+  a.max_splits = (max_kv_len + a.split - 1) / a.split;
+  a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
+  a.ws = workspace;
+  a.counters = counters;
+  a.out = out;
+  a.out_stride = out_token_stride;
+  const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
+  if (a.max_splits > 1) {
+    if (!workspace || !counters) return SPECDEC_EINVAL;
+    if (workspace_floats < units * a.max_splits * kRows * (kD + 2) || n_counters < units)
+      return SPECDEC_EINVAL;
+  }
+  if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
+  dim3 grid((unsigned)units, (unsigned)a.max_splits), block(kAttnThreads);
+  hipStream_t s = as_stream(stream);
+  const bool bs16 = (block_size % 16) == 0;
+  if (dtype == SPECDEC_BF16) {
+    if (bs16) attention_bf16_kernel<true><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<false><<<grid, block, 0, s>>>(a);
+  } else if (dtype == SPECDEC_F32) {
+    if (bs16) attention_f32_kernel<true><<<grid, block, 0, s>>>(a);
+    else attention_f32_kernel<false><<<grid, block, 0, s>>>(a);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}

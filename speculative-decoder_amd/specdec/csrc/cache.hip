@@ -1,0 +1,346 @@
+// Paged KV-cache index kernels: the LIFO block allocator (push = rollback or
+// release, pop = growth) applied to device block tables, slot arithmetic,
+// the fused RoPE + append of new K/V, and a gather used for inspection.
+//
+// Reference semantics: cache/paged.py:11-76 (allocator, tables, slots),
+// cache/kv.py:79-118 (append, write, gather, truncate), lm/forward.py:53,60
+// (rotary embedding).
+//
+// Pool layout per layer: K [num_blocks, Hkv, bs, d], V [num_blocks, Hkv, d, bs].
+#include "common.h"
+
+namespace specdec {
+
+constexpr int kPlanThreads = 256;
+
+// entries: (row, col, count, off) x (n_push + n_pop); pushes first.
+__global__ __launch_bounds__(kPlanThreads) void block_plan_kernel(
+    int32_t *__restrict__ tables, int64_t table_stride, int32_t *__restrict__ stack,
+    uint8_t *__restrict__ used, int32_t top, const int32_t *__restrict__ entries, int32_t n_push,
+    int32_t n_pop, int32_t *__restrict__ popped) {
+  __shared__ int32_t s_pushed;
+  if (threadIdx.x == 0) {
+    int32_t total = 0;
+    for (int e = 0; e < n_push; ++e) total += entries[4 * e + 2];
+    s_pushed = total;
+  }
+  // phase 1: rollbacks/releases push their blocks in table order
+  for (int e = threadIdx.x; e < n_push; e += blockDim.x) {
+    const int32_t row = entries[4 * e], col = entries[4 * e + 1];
+    const int32_t cnt = entries[4 * e + 2], off = entries[4 * e + 3];
+    for (int j = 0; j < cnt; ++j) {
+      const int32_t blk = tables[(int64_t)row * table_stride + col + j];
+      stack[top + off + j] = blk;
+      used[blk] = 0;
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  // phase 2: growth pops from the top of the stack, rows in call order
+  const int32_t top2 = top + s_pushed;
+  for (int e = threadIdx.x; e < n_pop; e += blockDim.x) {
+    const int32_t *ent = entries + 4 * (n_push + e);
+    const int32_t row = ent[0], col = ent[1], cnt = ent[2], off = ent[3];
+    for (int j = 0; j < cnt; ++j) {
+      const int32_t blk = stack[top2 - 1 - off - j];
+      tables[(int64_t)row * table_stride + col + j] = blk;
+      used[blk] = 1;
+      if (popped) popped[off + j] = blk;
+    }
+  }
+}
+
+__global__ void block_free_checked_kernel(int32_t *__restrict__ stack, uint8_t *__restrict__ used,
+                                          int32_t top, int32_t block, int32_t *__restrict__ status) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if (!used[block]) {
+    status[0] = 1;
+    return;
+  }
+  used[block] = 0;
+  stack[top] = block;
+  status[0] = 0;
+}
+
+__global__ void block_slots_kernel(const int32_t *__restrict__ row, int64_t start, int64_t n,
+                                   int32_t bs, int64_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t pos = start + i;
+  out[i] = (int64_t)row[pos / bs] * bs + pos % bs;
+}
+
+__device__ __forceinline__ int64_t slot_of(const int32_t *tables, int64_t table_stride, int32_t row,
+                                           int64_t pos, int32_t bs) {
+  return (int64_t)tables[(int64_t)row * table_stride + pos / bs] * bs + pos % bs;
+}
+
+__global__ void slot_map_kernel(const int32_t *__restrict__ tables, int64_t table_stride,
+                                const int32_t *__restrict__ meta, int32_t batch, int32_t bs,
+                                int32_t width, int32_t read_width,
+                                const int32_t *__restrict__ write_offsets,
+                                int64_t *__restrict__ write, int64_t *__restrict__ write_index,
+                                int64_t *__restrict__ read) {
+  const int b = blockIdx.y;
+  const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
+  const int32_t total = past + n;
+  for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < read_width;
+       pos += gridDim.x * blockDim.x) {
+    read[(int64_t)b * read_width + pos] = pos < total ? slot_of(tables, table_stride, row, pos, bs) : 0;
+    if (pos < n) {
+      const int64_t o = write_offsets[b] + pos;
+      write[o] = slot_of(tables, table_stride, row, past + pos, bs);
+      write_index[o] = (int64_t)b * width + pos;
+    }
+  }
+}
+
+// One thread per (token, head, rotation pair).  Heads [0, H) are queries,
+// [H, H+Hkv) keys, [H+Hkv, H+2Hkv) values (copied, not rotated).
+template <typename T>
+__global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, int32_t H,
+                                   int32_t Hkv, int32_t d, const float *__restrict__ cos_t,
+                                   const float *__restrict__ sin_t, const int32_t *__restrict__ meta,
+                                   int32_t batch, int32_t width, const int32_t *__restrict__ tables,
+                                   int64_t table_stride, int32_t bs, T *__restrict__ kpool,
+                                   T *__restrict__ vpool) {
+  const int half = d / 2;
+  const int heads = H + 2 * Hkv;
+  const int64_t total = (int64_t)batch * width * heads * half;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(idx % half);
+    const int head = (int)((idx / half) % heads);
+    const int64_t tok = idx / ((int64_t)half * heads);
+    const int b = (int)(tok / width), t = (int)(tok % width);
+    const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
+    if (t >= n) continue;  // right padding
+    const int64_t pos = past + t;
+    T *x = qkv + tok * token_stride + (int64_t)head * d;
+    float x1 = to_f32(x[i]), x2 = to_f32(x[i + half]);
+    if (head < H + Hkv) {
+      // q*cos + rotate_half(q)*sin, each product and the sum rounded
+      // separately (no fused multiply-add), cos/sin in fp32
+      const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+      const float y1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+      const float y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+      x1 = y1;
+      x2 = y2;
+      if (head < H) {
+        x[i] = from_f32<T>(x1);
+        x[i + half] = from_f32<T>(x2);
+        continue;
+      }
+    }
+    const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
+    const int off = (int)(pos % bs);
+    if (head < H + Hkv) {
+      const int h = head - H;
+      T *dst = kpool + ((blk * Hkv + h) * bs + off) * d;
+      const T v1 = from_f32<T>(x1), v2 = from_f32<T>(x2);
+      dst[i] = v1;
+      dst[i + half] = v2;
+      x[i] = v1;  // keep the rotated key in qkv as well
+      x[i + half] = v2;
+    } else {
+      const int h = head - H - Hkv;
+      T *dst = vpool + (blk * Hkv + h) * (int64_t)d * bs + off;
+      dst[(int64_t)i * bs] = x[i];
+      dst[(int64_t)(i + half) * bs] = x[i + half];
+    }
+  }
+}
+
+template <typename T>
+__global__ void kv_write_kernel(const T *__restrict__ k, const T *__restrict__ v, int32_t Hkv,
+                                int32_t d, const int32_t *__restrict__ meta, int32_t batch,
+                                int32_t width, const int32_t *__restrict__ tables,
+                                int64_t table_stride, int32_t bs, T *__restrict__ kpool,
+                                T *__restrict__ vpool) {
+  const int64_t total = (int64_t)batch * Hkv * width * d;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % d);
+    const int t = (int)((idx / d) % width);
+    const int h = (int)((idx / ((int64_t)d * width)) % Hkv);
+    const int b = (int)(idx / ((int64_t)d * width * Hkv));
+    const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
+    if (t >= n) continue;
+    const int64_t pos = past + t;
+    const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
+    const int off = (int)(pos % bs);
+    kpool[((blk * Hkv + h) * bs + off) * d + c] = k[idx];
+    vpool[((blk * Hkv + h) * d + c) * bs + off] = v[idx];
+  }
+}
+
+template <typename T>
+__global__ void kv_gather_kernel(const T *__restrict__ kpool, const T *__restrict__ vpool,
+                                 int32_t Hkv, int32_t d, const int32_t *__restrict__ meta,
+                                 int32_t batch, const int32_t *__restrict__ tables,
+                                 int64_t table_stride, int32_t bs, int32_t read_width,
+                                 T *__restrict__ k_out, T *__restrict__ v_out) {
+  const int64_t total = (int64_t)batch * Hkv * read_width * d;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % d);
+    const int pos = (int)((idx / d) % read_width);
+    const int h = (int)((idx / ((int64_t)d * read_width)) % Hkv);
+    const int b = (int)(idx / ((int64_t)d * read_width * Hkv));
+    const int32_t row = meta[b], total_b = meta[batch + b] + meta[2 * batch + b];
+    if (pos >= total_b) {
+      k_out[idx] = from_f32<T>(0.0f);
+      v_out[idx] = from_f32<T>(0.0f);
+      continue;
+    }
+    const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
+    const int off = pos % bs;
+    k_out[idx] = kpool[((blk * Hkv + h) * bs + off) * d + c];
+    v_out[idx] = vpool[((blk * Hkv + h) * d + c) * bs + off];
+  }
+}
+
+inline unsigned grid_for(int64_t n, int threads) {
+  int64_t g = (n + threads - 1) / threads;
+  if (g < 1) g = 1;
+  if (g > 1 << 20) g = 1 << 20;
+  return (unsigned)g;
+}
+
+}  // namespace specdec
+
+using namespace specdec;
+
+SPECDEC_API int specdec_block_plan(int32_t *tables, int64_t table_stride, int32_t *free_stack,
+                                   uint8_t *used, int64_t num_blocks, int32_t top,
+                                   const int32_t *entries, int32_t n_push, int32_t n_pop,
+                                   int32_t *popped, void *stream) {
+  if (n_push < 0 || n_pop < 0 || top < 0 || top > num_blocks) return SPECDEC_EINVAL;
+  if (n_push + n_pop == 0) return SPECDEC_OK;
+  if (!tables || !free_stack || !used || !entries) return SPECDEC_EINVAL;
+  block_plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, as_stream(stream)>>>(
+      tables, table_stride, free_stack, used, top, entries, n_push, n_pop, popped);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_block_free_checked(int32_t *free_stack, uint8_t *used, int64_t num_blocks,
+                                           int32_t top, int32_t block, int32_t *status,
+                                           void *stream) {
+  if (block < 0 || block >= num_blocks || top < 0 || top >= num_blocks) return SPECDEC_EINVAL;
+  if (!free_stack || !used || !status) return SPECDEC_EINVAL;
+  block_free_checked_kernel<<<dim3(1), dim3(64), 0, as_stream(stream)>>>(free_stack, used, top,
+                                                                         block, status);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_block_slots(const int32_t *table_row, int64_t start, int64_t stop,
+                                    int32_t block_size, int64_t *out, void *stream) {
+  if (start < 0 || stop < start || block_size <= 0) return SPECDEC_EINVAL;
+  const int64_t n = stop - start;
+  if (n == 0) return SPECDEC_OK;
+  if (!table_row || !out) return SPECDEC_EINVAL;
+  block_slots_kernel<<<dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream)>>>(
+      table_row, start, n, block_size, out);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_slot_map(const int32_t *tables, int64_t table_stride, const int32_t *meta,
+                                 int32_t batch, int32_t block_size, int32_t width,
+                                 int32_t read_width, const int32_t *write_offsets, int64_t *write,
+                                 int64_t *write_index, int64_t *read, void *stream) {
+  if (batch < 0 || block_size <= 0 || width < 0 || read_width < 0) return SPECDEC_EINVAL;
+  if (batch == 0 || read_width == 0) return SPECDEC_OK;
+  if (!tables || !meta || !write_offsets || !read) return SPECDEC_EINVAL;
+  dim3 grid(grid_for(read_width, 256) > 64 ? 64 : grid_for(read_width, 256), (unsigned)batch);
+  slot_map_kernel<<<grid, dim3(256), 0, as_stream(stream)>>>(tables, table_stride, meta, batch,
+                                                             block_size, width, read_width,
+                                                             write_offsets, write, write_index,
+                                                             read);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t n_heads,
+                                    int32_t n_kv_heads, int32_t head_dim, const float *cos_table,
+                                    const float *sin_table, int64_t max_positions,
+                                    const int32_t *meta, int32_t batch, int32_t width,
+                                    const int32_t *tables, int64_t table_stride,
+                                    int32_t block_size, void *k_pool, void *v_pool,
+                                    void *stream) {
+  (void)max_positions;  // positions are range-checked by the caller against the table size
+  if (batch < 0 || width < 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 ||
+      head_dim % 2 || block_size <= 0)
+    return SPECDEC_EINVAL;
+  if (batch == 0 || width == 0) return SPECDEC_OK;
+  if (!qkv || !cos_table || !sin_table || !meta || !tables || !k_pool || !v_pool)
+    return SPECDEC_EINVAL;
+  const int64_t n = (int64_t)batch * width * (n_heads + 2 * n_kv_heads) * (head_dim / 2);
+  dim3 grid(grid_for(n, 256)), block(256);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_BF16) {
+    rope_append_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
+        (__hip_bfloat16 *)qkv, token_stride, n_heads, n_kv_heads, head_dim, cos_table, sin_table,
+        meta, batch, width, tables, table_stride, block_size, (__hip_bfloat16 *)k_pool,
+        (__hip_bfloat16 *)v_pool);
+  } else if (dtype == SPECDEC_F32) {
+    rope_append_kernel<float><<<grid, block, 0, s>>>(
+        (float *)qkv, token_stride, n_heads, n_kv_heads, head_dim, cos_table, sin_table, meta,
+        batch, width, tables, table_stride, block_size, (float *)k_pool, (float *)v_pool);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_kv_write(const void *k, const void *v, int dtype, int32_t n_kv_heads,
+                                 int32_t head_dim, const int32_t *meta, int32_t batch,
+                                 int32_t width, const int32_t *tables, int64_t table_stride,
+                                 int32_t block_size, void *k_pool, void *v_pool, void *stream) {
+  if (batch < 0 || width < 0 || n_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
+    return SPECDEC_EINVAL;
+  if (batch == 0 || width == 0) return SPECDEC_OK;
+  if (!k || !v || !meta || !tables || !k_pool || !v_pool) return SPECDEC_EINVAL;
+  const int64_t n = (int64_t)batch * n_kv_heads * width * head_dim;
+  dim3 grid(grid_for(n, 256)), block(256);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_BF16) {
+    kv_write_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
+        (const __hip_bfloat16 *)k, (const __hip_bfloat16 *)v, n_kv_heads, head_dim, meta, batch,
+        width, tables, table_stride, block_size, (__hip_bfloat16 *)k_pool,
+        (__hip_bfloat16 *)v_pool);
+  } else if (dtype == SPECDEC_F32) {
+    kv_write_kernel<float><<<grid, block, 0, s>>>((const float *)k, (const float *)v, n_kv_heads,
+                                                 head_dim, meta, batch, width, tables,
+                                                 table_stride, block_size, (float *)k_pool,
+                                                 (float *)v_pool);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_kv_gather(const void *k_pool, const void *v_pool, int dtype,
+                                  int32_t n_kv_heads, int32_t head_dim, const int32_t *meta,
+                                  int32_t batch, const int32_t *tables, int64_t table_stride,
+                                  int32_t block_size, int32_t read_width, void *k_out,
+                                  void *v_out, void *stream) {
+  if (batch < 0 || read_width < 0 || n_kv_heads <= 0 || head_dim <= 0 || block_size <= 0)
+    return SPECDEC_EINVAL;
+  if (batch == 0 || read_width == 0) return SPECDEC_OK;
+  if (!k_pool || !v_pool || !meta || !tables || !k_out || !v_out) return SPECDEC_EINVAL;
+  const int64_t n = (int64_t)batch * n_kv_heads * read_width * head_dim;
+  dim3 grid(grid_for(n, 256)), block(256);
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_BF16) {
+    kv_gather_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
+        (const __hip_bfloat16 *)k_pool, (const __hip_bfloat16 *)v_pool, n_kv_heads, head_dim,
+        meta, batch, tables, table_stride, block_size, read_width, (__hip_bfloat16 *)k_out,
+        (__hip_bfloat16 *)v_out);
+  } else if (dtype == SPECDEC_F32) {
+    kv_gather_kernel<float><<<grid, block, 0, s>>>(
+        (const float *)k_pool, (const float *)v_pool, n_kv_heads, head_dim, meta, batch, tables,
+        table_stride, block_size, read_width, (float *)k_out, (float *)v_out);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}

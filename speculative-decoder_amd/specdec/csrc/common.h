@@ -1,0 +1,104 @@
+// Shared helpers for the gfx950 kernels of libspecdec.so: status codes,
+// stream casts, wavefront (64-lane) and workgroup reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../../include/specdec.h"
+
+#define SPECDEC_API extern "C" __attribute__((visibility("default")))
+
+namespace specdec {
+
+constexpr int kWave = 64;
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPECDEC_OK : SPECDEC_EHIP;
+}
+
+// ---- element conversion -------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(double x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 x) { return __bfloat162float(x); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ double from_f32<double>(float x) { return x; }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float x) {
+  return __float2bfloat16(x);  // round to nearest even
+}
+
+// ---- wavefront reductions (all 64 lanes participate) --------------------
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+template <typename T> __device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Workgroup-wide sum with a fixed reduction order (lane tree, then waves in
+// index order), so repeated launches give identical bits.
+// `scratch` holds at least blockDim.x / 64 elements.
+template <typename T> __device__ T block_sum(T v, T *scratch) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  T total = T(0);
+  for (int w = 0; w < nw; ++w) total += scratch[w];
+  return total;
+}
+
+template <typename T> __device__ T block_max(T v, T *scratch) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  T m = scratch[0];
+  for (int w = 1; w < nw; ++w) m = fmax(m, scratch[w]);
+  return m;
+}
+
+// Exclusive scan of one value per thread across the workgroup, fixed order.
+// Returns the exclusive prefix; *total receives the sum of all values.
+// `scratch` holds at least blockDim.x / 64 + 1 elements.
+template <typename T> __device__ T block_exclusive_scan(T v, T *scratch, T *total) {
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  // inclusive scan inside the wave (Hillis-Steele over shuffles)
+  T x = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    T y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == kWave - 1) scratch[wid] = x;
+  __syncthreads();
+  T wave_prefix = T(0), all = T(0);
+  for (int w = 0; w < nw; ++w) {
+    if (w < wid) wave_prefix += scratch[w];
+    all += scratch[w];
+  }
+  *total = all;
+  // exclusive prefix taken from the neighbour's inclusive value rather than
+  // x - v, which would round differently from a true prefix sum
+  T excl = __shfl_up(x, 1, kWave);
+  if (lane == 0) excl = T(0);
+  return wave_prefix + excl;
+}
+
+}  // namespace specdec

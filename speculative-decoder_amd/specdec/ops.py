@@ -1,0 +1,241 @@
+"""Tensor-level wrappers of the libspecdec.so entry points.
+
+Each wrapper checks devices, dtypes and contiguity on the host, launches on
+torch's current HIP stream and raises on a non-zero status.  Nothing here
+computes on the CPU: inputs that are not on a GPU are an error.
+"""
+from __future__ import annotations
+
+import torch
+
+from specdec._lib import lib
+
+OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
+F32, F64, BF16 = 0, 1, 2
+
+_DTYPES = {torch.float32: F32, torch.float64: F64, torch.bfloat16: BF16}
+
+
+class KernelError(RuntimeError):
+    pass
+
+
+def _check(status: int, name: str) -> None:
+    if status == OK:
+        return
+    what = {EINVAL: "invalid argument", EHIP: "HIP launch failed", EUNSUPPORTED: "unsupported shape"}
+    err = NotImplementedError if status == EUNSUPPORTED else KernelError
+    raise err(f"{name}: {what.get(status, 'error')} (status {status})")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def gpu(t: torch.Tensor, name: str = "tensor") -> torch.Tensor:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a GPU (got {t.device}); the hot path has no CPU fallback")
+    return t
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------ accept --
+def probabilities(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """[..., V] logits -> fp32 probabilities (one-hot argmax at temperature 0)."""
+    gpu(logits, "logits")
+    shape = logits.shape
+    x = logits.reshape(-1, shape[-1])
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    st = lib().specdec_probabilities(x.data_ptr(), dtype_code(x), x.shape[0], x.shape[1], x.stride(0),
+                                     float(temperature), out.data_ptr(), out.stride(0), stream())
+    _check(st, "probabilities")
+    return out.view(shape)
+
+
+def _rows3(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def accept_reject(p, q, draft, u_accept, u_residual) -> torch.Tensor:
+    """Fused accept + residual + inverse CDF; returns int64 [3, B] on the GPU:
+    n_accepted, next_token, zero-q flag."""
+    p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
+    b, k = draft.shape
+    out = torch.empty(3, b, dtype=torch.int64, device=p.device)
+    st = lib().specdec_accept_reject(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
+                                     q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(),
+                                     u_residual.data_ptr(), b, k, p.shape[-1], out.data_ptr(), stream())
+    _check(st, "accept_reject")
+    return out
+
+
+def accept_count(p, q, draft, u_accept) -> torch.Tensor:
+    """Accept stage alone; int64 [2, B]: n_accepted, zero-q flag."""
+    p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
+    b, k = draft.shape
+    out = torch.empty(2, b, dtype=torch.int64, device=p.device)
+    st = lib().specdec_accept_count(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
+                                    q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(), b, k,
+                                    out.data_ptr(), stream())
+    _check(st, "accept_count")
+    return out
+
+
+def sample_inverse_cdf(probs: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    gpu(probs, "probs")
+    if probs.stride(-1) != 1:
+        probs = probs.contiguous()
+    b, v = probs.shape
+    out = torch.empty(b, dtype=torch.int64, device=probs.device)
+    st = lib().specdec_sample_inverse_cdf(probs.data_ptr(), dtype_code(probs), b, v, probs.stride(0),
+                                          u.data_ptr(), out.data_ptr(), stream())
+    _check(st, "sample_inverse_cdf")
+    return out
+
+
+def one_hot(ids: torch.Tensor, vocab: int) -> torch.Tensor:
+    gpu(ids, "ids")
+    flat = ids.reshape(-1).to(torch.int64).contiguous()
+    out = torch.empty(flat.numel(), vocab, dtype=torch.float32, device=ids.device)
+    _check(lib().specdec_one_hot(flat.data_ptr(), flat.numel(), vocab, out.data_ptr(), stream()), "one_hot")
+    return out.view(*ids.shape, vocab)
+
+
+# ------------------------------------------------------------------ n-gram --
+def ngram_lookup(history: torch.Tensor, lengths: torch.Tensor, k: int, max_n: int):
+    """history int32 [B, cap], lengths int32 [B] -> (draft int64 [B, k], match int32 [B, 2])."""
+    gpu(history, "history")
+    b = history.shape[0]
+    draft = torch.empty(b, k, dtype=torch.int64, device=history.device)
+    match = torch.empty(b, 2, dtype=torch.int32, device=history.device)
+    st = lib().specdec_ngram_lookup(history.data_ptr(), history.stride(0), lengths.data_ptr(), b, k, max_n,
+                                    draft.data_ptr(), match.data_ptr(), stream())
+    _check(st, "ngram_lookup")
+    return draft, match
+
+
+# ------------------------------------------------------------------- cache --
+def block_plan(tables, free_stack, used, top: int, entries, n_push: int, n_pop: int, popped=None) -> None:
+    st = lib().specdec_block_plan(tables.data_ptr(), tables.stride(0), free_stack.data_ptr(), used.data_ptr(),
+                                  free_stack.numel(), top, entries.data_ptr(), n_push, n_pop, ptr(popped),
+                                  stream())
+    _check(st, "block_plan")
+
+
+def block_free_checked(free_stack, used, top: int, block: int, status) -> None:
+    st = lib().specdec_block_free_checked(free_stack.data_ptr(), used.data_ptr(), free_stack.numel(), top,
+                                          block, status.data_ptr(), stream())
+    _check(st, "block_free_checked")
+
+
+def block_slots(row: torch.Tensor, start: int, stop: int, block_size: int) -> torch.Tensor:
+    out = torch.empty(max(stop - start, 0), dtype=torch.int64, device=row.device)
+    st = lib().specdec_block_slots(row.data_ptr(), start, stop, block_size, out.data_ptr(), stream())
+    _check(st, "block_slots")
+    return out
+
+
+def slot_map(tables, meta, batch: int, block_size: int, width: int, read_width: int, write_offsets,
+             n_write: int):
+    dev = tables.device
+    write = torch.empty(n_write, dtype=torch.int64, device=dev)
+    write_index = torch.empty(n_write, dtype=torch.int64, device=dev)
+    read = torch.empty(batch, read_width, dtype=torch.int64, device=dev)
+    st = lib().specdec_slot_map(tables.data_ptr(), tables.stride(0), meta.data_ptr(), batch, block_size, width,
+                                read_width, write_offsets.data_ptr(), write.data_ptr(), write_index.data_ptr(),
+                                read.data_ptr(), stream())
+    _check(st, "slot_map")
+    return write, write_index, read
+
+
+def rope_append(qkv, n_heads, n_kv_heads, head_dim, cos, sin, meta, batch, width, tables, block_size,
+                k_pool, v_pool) -> None:
+    st = lib().specdec_rope_append(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), n_heads, n_kv_heads, head_dim,
+                                   cos.data_ptr(), sin.data_ptr(), cos.shape[0], meta.data_ptr(), batch, width,
+                                   tables.data_ptr(), tables.stride(0), block_size, k_pool.data_ptr(),
+                                   v_pool.data_ptr(), stream())
+    _check(st, "rope_append")
+
+
+def kv_write(k, v, meta, batch, width, tables, block_size, k_pool, v_pool) -> None:
+    k, v = k.contiguous(), v.contiguous()
+    st = lib().specdec_kv_write(k.data_ptr(), v.data_ptr(), dtype_code(k), k.shape[1], k.shape[3], meta.data_ptr(),
+                                batch, width, tables.data_ptr(), tables.stride(0), block_size, k_pool.data_ptr(),
+                                v_pool.data_ptr(), stream())
+    _check(st, "kv_write")
+
+
+def kv_gather(k_pool, v_pool, meta, batch, tables, block_size, read_width):
+    n_kv, d = k_pool.shape[1], k_pool.shape[3]
+    k_out = torch.empty(batch, n_kv, read_width, d, dtype=k_pool.dtype, device=k_pool.device)
+    v_out = torch.empty_like(k_out)
+    st = lib().specdec_kv_gather(k_pool.data_ptr(), v_pool.data_ptr(), dtype_code(k_pool), n_kv, d, meta.data_ptr(),
+                                 batch, tables.data_ptr(), tables.stride(0), block_size, read_width,
+                                 k_out.data_ptr(), v_out.data_ptr(), stream())
+    _check(st, "kv_gather")
+    return k_out, v_out
+
+
+# --------------------------------------------------------------- attention --
+class AttentionWorkspace:
+    """Grow-only split-KV partials and arrival counters for one device.
+    Calls that share a workspace must be ordered on one stream."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.floats = torch.empty(0, dtype=torch.float32, device=device)
+        self.counters = torch.zeros(0, dtype=torch.int32, device=device)
+
+    def reserve(self, floats: int, counters: int) -> None:
+        if floats > self.floats.numel():
+            self.floats = torch.empty(max(floats, 2 * self.floats.numel()), dtype=torch.float32, device=self.device)
+        if counters > self.counters.numel():
+            self.counters = torch.zeros(max(counters, 2 * self.counters.numel()), dtype=torch.int32,
+                                        device=self.device)
+
+
+_workspaces: dict[torch.device, AttentionWorkspace] = {}
+
+
+def workspace_for(device: torch.device) -> AttentionWorkspace:
+    ws = _workspaces.get(device)
+    if ws is None:
+        ws = _workspaces[device] = AttentionWorkspace(device)
+    return ws
+
+
+def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_kv_len: int) -> int:
+    return lib().specdec_attention_split(batch, width, n_heads, n_kv_heads, max_kv_len)
+
+
+def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
+                    block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None):
+    import ctypes
+
+    ws = workspace or workspace_for(q.device)
+    floats, counters = ctypes.c_int64(), ctypes.c_int64()
+    st = lib().specdec_attention_workspace(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, 0,
+                                           ctypes.byref(floats), ctypes.byref(counters))
+    _check(st, "attention_workspace")
+    ws.reserve(floats.value, counters.value)
+    st = lib().specdec_paged_attention(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
+                                       v_pool.data_ptr(), tables.data_ptr(), tables.stride(0), meta.data_ptr(), batch,
+                                       width, n_heads, n_kv_heads, head_dim, block_size, float(scale), max_kv_len,
+                                       ws.floats.data_ptr(), ws.floats.numel(), ws.counters.data_ptr(),
+                                       ws.counters.numel(), out.data_ptr(), out_token_stride, stream())
+    _check(st, "paged_attention")
+    return out

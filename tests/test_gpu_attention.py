@@ -1,0 +1,125 @@
+"""Paged verify attention kernel vs SDPA on the gathered cache (the
+reference's attention step), plus the cache write/gather and rollback."""
+import random
+
+import pytest
+import torch
+
+import oracle.forward as of
+from cache.kv import KVCache
+from specdec import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def make_cache(layers, hkv, d, num_blocks, bs, dtype, seed):
+    """A cache whose blocks are handed out in a seeded random order: a
+    permutation of the pool is allocated and freed once so the LIFO stack
+    yields shuffled block ids."""
+    cache = KVCache(layers, hkv, d, num_blocks, bs, dtype, "cuda")
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(seed)).tolist()
+    cache.add(-1)
+    cache.append([-1], [num_blocks * bs])
+    # free in permuted order by rewriting the table before releasing it
+    table = cache.tables[-1]
+    cache.table_tensor[table.row, :num_blocks] = torch.tensor(perm, dtype=torch.int32, device="cuda")
+    cache.free(-1)
+    cache.flush()
+    return cache
+
+
+def run_case(batch, lengths, h, hkv, bs, dtype, t_new, seed, rollback=True):
+    d = 64
+    g = torch.Generator().manual_seed(seed)
+    nb = sum((L + 2 * t_new + 2 * bs) // bs + 1 for L in lengths) + 8
+    cache = make_cache(1, hkv, d, nb, bs, dtype, seed)
+    ids = list(range(batch))
+    for s in ids:
+        cache.add(s)
+    # history: prefill each row to its length with random K/V
+    step = cache.append(ids, lengths)
+    kh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(dtype)
+    vh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(dtype)
+    cache.write(0, step, kh.cuda(), vh.cuda())
+    outs = []
+    for rnd in range(2):
+        step = cache.append(ids, [t_new] * batch)
+        q = torch.randn(batch, t_new, h, d, generator=g).to(dtype)
+        kn = torch.randn(batch, hkv, t_new, d, generator=g).to(dtype)
+        vn = torch.randn(batch, hkv, t_new, d, generator=g).to(dtype)
+        cache.write(0, step, kn.cuda(), vn.cuda())
+        out = torch.zeros(batch, t_new, h * d, dtype=dtype, device="cuda")
+        qd = q.reshape(batch, t_new, h * d).cuda()
+        ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch,
+                            t_new, h, hkv, d, bs, d ** -0.5, step.max_total, out, out.stride(1))
+        k_all, v_all = cache.gather(0, step)
+        want = of.attention(q.transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
+                            torch.tensor(step.past), torch.tensor(step.total), d ** -0.5)
+        got = out.view(batch, t_new, h, d).transpose(1, 2).float().cpu()
+        outs.append((got, want))
+        if rollback:
+            rng = random.Random(seed * 7 + rnd)
+            for s in ids:
+                a = rng.randint(0, t_new - 1)
+                cache.truncate(s, step.past[ids.index(s)] + 1 + a)
+    return outs
+
+
+@pytest.mark.parametrize("length", [512, 1024, 2048, 4096])
+@pytest.mark.parametrize("batch", [1, 4, 8])
+def test_config2_bf16_matches_sdpa(batch, length):
+    """32/32 heads, d=64, bs=16, bf16, k+1=5 queries, shuffled pool, rollback."""
+    lengths = [length - 3 * b for b in range(batch)]
+    for got, want in run_case(batch, lengths, 32, 32, 16, torch.bfloat16, 5, seed=batch * 10000 + length):
+        err = (got - want).abs().max().item()
+        assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("bs", [1, 3, 4, 16, 32])
+@pytest.mark.parametrize("heads", [(4, 2), (9, 3), (8, 8)])
+def test_fp32_any_block_size_and_gqa(bs, heads):
+    h, hkv = heads
+    for got, want in run_case(3, [37, 5, 70], h, hkv, bs, torch.float32, 5, seed=bs * 100 + h):
+        assert torch.allclose(got, want, atol=2e-5, rtol=1e-5), (got - want).abs().max()
+
+
+@pytest.mark.parametrize("bs", [4, 16])
+def test_bf16_gqa_small_blocks(bs):
+    for got, want in run_case(2, [300, 45], 9, 3, bs, torch.bfloat16, 1, seed=bs):
+        assert (got - want).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_verify_rows_equal_decode_rows_bitwise(dtype):
+    """The same query at the same position gives identical bits whether it is
+    verified among k+1 tokens or decoded alone: the reduction order depends
+    only on key positions (the property the greedy identity relies on)."""
+    d, h, hkv, bs = 64, 32, 32, 16
+    L = 1000
+    g = torch.Generator().manual_seed(5)
+    cache = make_cache(1, hkv, d, 128, bs, dtype, 1)
+    cache.add(0)
+    step = cache.append([0], [L + 5])
+    kh = torch.randn(1, hkv, L + 5, d, generator=g).to(dtype).cuda()
+    vh = torch.randn(1, hkv, L + 5, d, generator=g).to(dtype).cuda()
+    cache.write(0, step, kh, vh)
+    q = torch.randn(1, 5, h * d, generator=g).to(dtype).cuda()
+    cache.truncate(0, L)
+    step5 = cache.append([0], [5])
+    out5 = torch.zeros(1, 5, h * d, dtype=dtype, device="cuda")
+    ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step5.meta, 1, 5, h, hkv, d,
+                        bs, 0.125, step5.max_total, out5, out5.stride(1))
+    for t in range(5):
+        cache.truncate(0, L + t)
+        step1 = cache.append([0], [1])
+        out1 = torch.zeros(1, 1, h * d, dtype=dtype, device="cuda")
+        q1 = q[:, t:t + 1].contiguous()
+        ops.paged_attention(q1, q1.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step1.meta, 1, 1, h, hkv,
+                            d, bs, 0.125, step1.max_total, out1, out1.stride(1))
+        assert torch.equal(out1[0, 0], out5[0, t]), t
+
+
+def test_prefill_many_query_tiles():
+    """A 200-token prefill (13 query tiles per head) against SDPA."""
+    for got, want in run_case(2, [0, 17], 4, 2, 16, torch.float32, 200, seed=3, rollback=False):
+        assert torch.allclose(got, want, atol=2e-5, rtol=1e-5)

@@ -1,0 +1,78 @@
+"""N-gram lookup kernel vs the oracle, the reference's literals and golden rows."""
+import hashlib
+import json
+
+import pytest
+import torch
+
+import oracle.ngram as on
+from helpers import golden
+from make_golden import planted_rows
+from spec.ngram import NGramDraft, lookup, lookup_batch
+
+pytestmark = pytest.mark.gpu
+
+
+def test_reference_literals():
+    assert lookup([1, 2, 3, 4, 1, 2], k=2, max_n=3) == [3, 4]
+    assert lookup([1, 2, 3, 1, 2], k=5, max_n=2) == [3, 1, 2, 3, 1]
+    ctx = [7, 8, 9, 1, 8, 5, 7, 8]
+    assert lookup(ctx, k=1, max_n=2) == [9]
+    assert lookup(ctx, k=1, max_n=1) == [5]
+    assert lookup([1, 4, 2, 4, 3, 4], k=1, max_n=1) == [3]
+    assert lookup([1, 2, 3], k=3, max_n=3) == [3, 3, 3]
+
+
+def test_golden_rows():
+    for case in golden("ngram.json")["cases"]:
+        rows = case["rows"]
+        if rows is None:
+            rows = planted_rows(*case["gen"])
+            assert hashlib.sha256(json.dumps(rows).encode()).hexdigest() == case["rows_sha"]
+        got, _ = lookup_batch(rows, case["k"], case["max_n"])
+        assert got == case["out"], (case["gen"], case["k"], case["max_n"])
+
+
+@pytest.mark.parametrize("length", [2048, 4096, 8192])
+def test_config3_batch16_matches_oracle_with_positions(length):
+    rows = planted_rows(16, length, 49152, seed=length)
+    got, match = lookup_batch(rows, 4, 3)
+    for row, g, m in zip(rows, got, match):
+        want, start, n = on.lookup_match(row, 4, 3)
+        assert g == want
+        assert tuple(m) == (start, n)
+
+
+@pytest.mark.parametrize("vocab", [2, 3, 7])
+def test_small_vocab_random_rows_all_n(vocab):
+    g = torch.Generator().manual_seed(vocab)
+    rows = [torch.randint(0, vocab, (int(n),), generator=g).tolist()
+            for n in torch.randint(1, 40, (64,), generator=g)]
+    for k in (0, 1, 4, 9):
+        for max_n in (0, 1, 2, 3, 5, 8):
+            got, match = lookup_batch(rows, k, max_n)
+            for row, gt, m in zip(rows, got, match):
+                want, start, n = on.lookup_match(row, k, max_n)
+                assert gt == want and tuple(m) == (start, n), (row, k, max_n)
+
+
+def test_drafter_incremental_history_matches_full_lookup():
+    """NGramDraft uploads only appended tokens; proposals equal lookup on the
+    whole context every round, and q is the one-hot of the proposal."""
+    rows = planted_rows(4, 600, 50, seed=3)
+    drafter = NGramDraft(64)
+    ctxs = [r[:200] for r in rows]
+    for step in range(0, 300, 37):
+        ctxs = [r[: 200 + step] for r in rows]
+        draft, q = drafter.propose([0, 1, 2, 3], ctxs, 4, 0.0, None)
+        want = [on.lookup(c, 4, 3) for c in ctxs]
+        assert draft.cpu().tolist() == want
+        assert torch.equal(q.cpu(), torch.nn.functional.one_hot(torch.tensor(want), 64).float())
+    drafter.release(1)
+    draft, _ = drafter.propose([1], [rows[1][:50]], 4, 0.0, None)
+    assert draft.cpu().tolist() == [on.lookup(rows[1][:50], 4, 3)]
+
+
+def test_empty_context_raises():
+    with pytest.raises(IndexError):
+        lookup([], 3, 3)

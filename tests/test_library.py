@@ -1,0 +1,45 @@
+"""The C-ABI library loads and exports every symbol include/specdec.h declares
+(no GPU needed: nothing is launched)."""
+import re
+from pathlib import Path
+
+from specdec import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "specdec.h"
+
+
+def declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^int (specdec_\w+)\(", text, flags=re.M))
+
+
+def test_header_and_binding_agree():
+    assert declared() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_symbol():
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.specdec_abi_version() == _lib.ABI_VERSION
+
+
+def test_attention_workspace_query_needs_no_gpu():
+    import ctypes
+
+    lib = _lib.load()
+    floats, counters = ctypes.c_int64(), ctypes.c_int64()
+    # B=1, T=5, 32/32 heads, d=64, 4101 keys: one tile per head, 17 splits of 256
+    assert lib.specdec_attention_workspace(1, 5, 32, 32, 64, 4101, 0, ctypes.byref(floats), ctypes.byref(counters)) == 0
+    assert counters.value == 32
+    assert floats.value == 32 * 17 * 16 * 66
+    assert lib.specdec_attention_split(1, 5, 32, 32, 4101) == 256
+    assert lib.specdec_attention_workspace(1, 5, 32, 32, 128, 10, 0, ctypes.byref(floats), ctypes.byref(counters)) == 3
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _lib.load()
+    # negative sizes and null pointers return SPECDEC_EINVAL without touching a device
+    assert lib.specdec_probabilities(None, 0, -1, 10, 10, 1.0, None, 10, None) == 1
+    assert lib.specdec_ngram_lookup(None, 0, None, 1, 4, 9, None, None, None) == 3  # max_n > 8
+    assert lib.specdec_block_plan(None, 1, None, None, 4, 5, None, 1, 0, None, None) == 1  # top > num_blocks
