@@ -1,0 +1,356 @@
+"""Benchmark of the speculative-decoding hot path on one MI355X.
+
+Headline (`value`): emitted tokens/s of greedy speculative decoding at batch 1
+with k = 4 and paged KV (block size 16), target with SmolLM2-1.7B shapes and
+draft with SmolLM2-135M shapes, random-init bf16 weights, a 256-token seeded
+prompt and 128 new tokens.  One step = one `generate` call.
+
+`roofline`: the verify paged-attention kernel at B = 1, context 4096, 32/32
+heads of 64, 5 query tokens, shuffled block table: algorithmic bytes per
+launch (K+V of 4101 positions + Q in + O out + block table) over the mean
+launch time measured with HIP events on the stream it runs on.
+
+`cpu_baseline`: the oracle's CPU restatement of the reference loop
+(gather + SDPA forward, host accept-reject) on the same weights, timed on a
+bounded sample of the same request.
+
+`kernels`: per-kernel times for the other workloads (accept-reject at
+V = 49152, n-gram lookup at batch 16, cache append/rollback, attention over
+the batch x context grid), each with its algorithmic bytes and GB/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only e2e|attention|kernels]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "speculative-decoder_amd"))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+V = 49152
+PROMPT = 256
+NEW_TOKENS = 128
+K = 4
+BLOCK = 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------- models ---
+def build_models(dtype=torch.bfloat16, seed=0):
+    from lm.model import SMOLLM2_135M, SMOLLM2_1_7B, Llama, random_state_dict
+
+    dev = torch.device("cuda", 0)
+    t_state = random_state_dict(SMOLLM2_1_7B, seed, dev, dtype)
+    d_state = random_state_dict(SMOLLM2_135M, seed + 1, dev, dtype)
+    return (Llama.from_state_dict(SMOLLM2_1_7B, t_state), Llama.from_state_dict(SMOLLM2_135M, d_state),
+            t_state, d_state)
+
+
+def prompt_ids(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, V, (PROMPT,), generator=g).tolist()
+
+
+def run_e2e(target, draft, prompt, new_tokens=NEW_TOKENS):
+    from cache.kv import KVCache
+    from spec.draft import ModelDraft
+    from spec.loop import generate
+
+    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
+    tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda")
+    dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda")
+    out, stats = generate(target, tc, ModelDraft(draft, dc), [prompt], new_tokens, k=K,
+                          generator=torch.Generator().manual_seed(0))
+    return out[0], stats
+
+
+def bench_e2e(steps, warmup):
+    target, draft, t_state, d_state = build_models()
+    prompt = prompt_ids()
+    log("e2e warmup")
+    for _ in range(warmup):
+        run_e2e(target, draft, prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = []
+    for _ in range(steps):
+        out, stats = run_e2e(target, draft, prompt)
+        outs.append(out)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    emitted = sum(len(o) for o in outs)
+    result = {"tokens_per_s": emitted / dt, "ms_per_step": 1000 * dt / steps, "emitted_per_step": len(outs[0]),
+              "rounds": stats.rounds, "mean_accept_len": stats.accepted / max(stats.rounds, 1),
+              "acceptance": stats.accepted / max(stats.drafted, 1)}
+    # identity check of this output against plain greedy decoding of the target
+    from baselines.cached_autoregressive import generate as plain
+    from cache.kv import KVCache
+
+    blocks = (PROMPT + NEW_TOKENS + 2 * BLOCK) // BLOCK + 4
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    want = plain(target, KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda"), prompt, NEW_TOKENS)
+    torch.cuda.synchronize()
+    result["plain_greedy_tokens_per_s"] = NEW_TOKENS / (time.perf_counter() - t1)
+    result["identical_to_plain_greedy"] = want == outs[0]
+    result["first_divergence"] = next((i for i, (a, b) in enumerate(zip(want, outs[0])) if a != b), None)
+    return result, (target, draft, t_state, d_state, prompt, outs[0])
+
+
+# ------------------------------------------------------------ attention -----
+def attention_bytes(batch, lengths, t_new=5, h=32, hkv=32, d=64, bs=BLOCK):
+    kv = sum((L + t_new) * hkv * d * 2 * 2 for L in lengths)
+    qo = batch * t_new * h * d * 2 * 2
+    tables = sum(-(-(L + t_new) // bs) * 4 for L in lengths)
+    return kv + qo + tables
+
+
+def setup_attention(batch, length, seed=0, h=32, hkv=32, d=64, t_new=5, num_blocks=4096):
+    """Config 2: pool of 4096 blocks handed out in a seeded random order,
+    `length` cached positions per row, then an append of t_new tokens."""
+    from cache.kv import KVCache
+
+    need = batch * (-(-(length + t_new) // BLOCK))
+    num_blocks = max(num_blocks, need + 8)
+    cache = KVCache(1, hkv, d, num_blocks, BLOCK, torch.bfloat16, "cuda", max_seqs=batch + 2)
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(seed))
+    cache.add(-1)
+    cache.append([-1], [num_blocks * BLOCK])
+    cache.table_tensor[cache.tables[-1].row, :num_blocks] = perm.to(torch.int32).cuda()
+    cache.free(-1)
+    cache.flush()
+    ids = list(range(batch))
+    for s in ids:
+        cache.add(s)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    step = cache.append(ids, [length] * batch)
+    cache.k.normal_(generator=g)
+    cache.v.normal_(generator=g)
+    step = cache.append(ids, [t_new] * batch)
+    q = torch.randn(batch, t_new, h * d, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    return cache, step, q, out
+
+
+def time_attention(batch, length, iters=200):
+    from specdec import ops
+
+    cache, step, q, out = setup_attention(batch, length)
+    h, hkv, d = 32, 32, 64
+
+    def launch():
+        ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, 5, h,
+                            hkv, d, BLOCK, 0.125, step.max_total, out, out.stride(1))
+
+    for _ in range(10):
+        launch()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        launch()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1000 / iters
+    nbytes = attention_bytes(batch, [length] * batch)
+    return {"batch": batch, "context": length, "us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+            "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
+
+
+# ------------------------------------------------------- other kernels ------
+def time_fn(fn, iters=100):
+    for _ in range(5):
+        fn()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000 / iters
+
+
+def bench_kernels():
+    from make_golden import planted_rows
+    from specdec import ops
+
+    res = {}
+    # config 1: accept-reject, B=1, k=4, V=49152, fp32, T=1
+    for b, k in [(1, 4), (8, 4), (32, 8)]:
+        g = torch.Generator(device="cuda").manual_seed(1)
+        tl = torch.randn(b, k + 1, V, generator=g, device="cuda") * 2
+        dl = tl[:, :k] + torch.randn(b, k, V, generator=g, device="cuda") * 0.5
+        p = ops.probabilities(tl, 1.0)
+        q = ops.probabilities(dl, 1.0)
+        draft = torch.randint(0, V, (b, k), device="cuda")
+        q.view(-1, V)[torch.arange(b * k, device="cuda"), draft.view(-1)] += 1e-3
+        ua = torch.rand(b, k, generator=g, device="cuda")
+        ur = torch.rand(b, generator=g, device="cuda")
+        us_soft = time_fn(lambda: ops.probabilities(torch.cat([tl.view(-1, V), dl.view(-1, V)]), 1.0))
+        us_acc = time_fn(lambda: ops.accept_reject(p, q, draft, ua, ur))
+        logit_bytes = (2 * k + 1) * V * 4 * b
+        res[f"accept_b{b}_k{k}"] = {"softmax_us": us_soft, "accept_us": us_acc, "logit_bytes": logit_bytes,
+                                    "softmax_gbs": 2 * logit_bytes / us_soft / 1e3}
+    # config 3: n-gram, B=16
+    for length in (2048, 4096, 8192):
+        rows = planted_rows(16, length, V, seed=length)
+        hist = torch.tensor(rows, dtype=torch.int32, device="cuda")
+        lens = torch.full((16,), length, dtype=torch.int32, device="cuda")
+        us = time_fn(lambda: ops.ngram_lookup(hist, lens, 4, 3))
+        nbytes = 16 * length * 4
+        res[f"ngram_b16_L{length}"] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3}
+    # config 2': cache append (rope + scatter of 5 tokens) and rollback plan
+    cache, step, q, out = setup_attention(1, 4096)
+    qkv = torch.randn(1, 5, 96 * 64, device="cuda").to(torch.bfloat16)
+    from lm.model import SMOLLM2_1_7B, rope_tables
+
+    cos, sin = (t.cuda() for t in rope_tables(SMOLLM2_1_7B, 8192))
+    us_app = time_fn(lambda: ops.rope_append(qkv, 32, 32, 64, cos, sin, step.meta, 1, 5, cache.table_tensor, BLOCK,
+                                             cache.k[0], cache.v[0]))
+    res["append_b1_t5"] = {"us": us_app, "bytes": 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2}
+    # attention over the config-2 grid
+    for b in (1, 4, 8):
+        for L in (512, 1024, 2048, 4096):
+            res[f"attention_b{b}_L{L}"] = time_attention(b, L, iters=50)
+    return res
+
+
+# ------------------------------------------------------------ CPU side ------
+def cpu_baseline(t_state, d_state, prompt, new_tokens=16):
+    """Oracle loop on the host cores: same weights (bf16), same prompt, a
+    bounded number of new tokens."""
+    import oracle.forward as of
+    import oracle.kv as okv
+    from lm.model import SMOLLM2_135M, SMOLLM2_1_7B
+    from oracle.draft import ModelDraft
+    from oracle.loop import generate
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+
+    def cfg(s):
+        return of.Config(s.vocab_size, s.hidden_size, s.num_hidden_layers, s.num_attention_heads,
+                         s.num_key_value_heads, s.intermediate_size, s.head_dim, s.rms_norm_eps, s.rope_theta, True)
+
+    tm = of.Model(cfg(SMOLLM2_1_7B), {k: v.cpu() for k, v in t_state.items()})
+    dm = of.Model(cfg(SMOLLM2_135M), {k: v.cpu() for k, v in d_state.items()})
+    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
+    t0 = time.perf_counter()
+    out, stats = generate(tm, okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16),
+                          ModelDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16)),
+                          [prompt], new_tokens, K, generator=torch.Generator().manual_seed(0))
+    dt = time.perf_counter() - t0
+    return {"value": len(out[0]) / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle loop (gather+SDPA forward, CPU accept-reject), 256-token prompt, "
+                      f"{new_tokens} new tokens, bf16, torch threads={threads}",
+            "seconds": dt, "tokens": out[0]}
+
+
+def cpu_attention_baseline(length=4096):
+    """Oracle attention step (gather copy + masked SDPA) at B=1, L=4096 on the CPU."""
+    import oracle.forward as of
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    pool = torch.randn(4096 * BLOCK, 32, 64, generator=g).to(torch.bfloat16)
+    read = (torch.randperm(4096, generator=g)[: -(-(length + 5) // BLOCK)][:, None] * BLOCK
+            + torch.arange(BLOCK)).flatten()[: length + 5][None]
+    q = torch.randn(1, 32, 5, 64, generator=g).to(torch.bfloat16)
+    past, total = torch.tensor([length]), torch.tensor([length + 5])
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 3.0:
+        k_all = pool[read].transpose(1, 2)
+        v_all = pool[read].transpose(1, 2)
+        of.attention(q, k_all, v_all, past, total, 0.125)
+        n += 1
+    us = (time.perf_counter() - t0) / n * 1e6
+    return {"us": us, "gbs": attention_bytes(1, [length]) / us / 1e3, "cores": threads}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (sharding is described in "
+              "DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, str(ROOT))
+    sys.path.insert(0, str(ROOT / "tests" / "golden"))
+
+    if args.only == "attention":
+        r = time_attention(1, 4096, iters=max(args.steps, 1) * 100)
+        print(json.dumps({"attention_b1_L4096": r}))
+        return
+    if args.only == "kernels":
+        print(json.dumps(bench_kernels()))
+        return
+
+    e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
+    log(f"e2e {e2e}")
+    attn = time_attention(1, 4096, iters=300)
+    log(f"attention {attn}")
+    kernels = {} if args.only == "e2e" else bench_kernels()
+    cpu = None
+    if not args.no_cpu:
+        del target, draft
+        torch.cuda.empty_cache()
+        log("cpu baseline")
+        cpu = cpu_baseline(t_state, d_state, prompt)
+        cpu_tokens = cpu.pop("tokens")
+        cpu["matches_gpu_prefix"] = cpu_tokens == gpu_tokens[: len(cpu_tokens)]
+        cpu["attention_b1_L4096"] = cpu_attention_baseline()
+    line = {
+        "metric": "spec-decode accepted tokens/s, 1.7B/135M k=4 b=1; verify-attn HBM GB/s",
+        "value": e2e["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": e2e["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0, 0.02), seeded uniform prompt ids)",
+        "config": {"workload": "greedy speculative decode, target SmolLM2-1.7B shapes / draft SmolLM2-135M shapes, "
+                               "batch 1, k=4, paged KV block 16, prompt 256, 128 new tokens",
+                   "batch": 1, "k": K, "prompt": PROMPT, "new_tokens": NEW_TOKENS, "block_size": BLOCK},
+        "roofline": {"bound": "hbm", "achieved": attn["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "attention_bf16_kernel (verify, B=1, context 4096, 32/32 heads, 5 queries)",
+                     "us_per_launch": attn["us"], "bytes_per_launch": attn["bytes"]},
+        "cpu_baseline": cpu,
+        "e2e": e2e,
+        "kernels": kernels,
+    }
+    if cpu:
+        line["cpu_baseline"]["speedup"] = e2e["tokens_per_s"] / cpu["value"]
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -33,7 +33,7 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
 
     The same call serves prefill (T = prompt length), decode (T = 1) and
     speculative verification (T = k + 1)."""
-    llama = as_llama(model)
+    llama = as_llama(model, cache.device)
     cfg = llama.config
     step = cache.append(seq_ids, n_new)
     ids = input_ids.to(cache.device, non_blocking=True)

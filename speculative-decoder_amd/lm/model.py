@@ -1,6 +1,6 @@
 """Llama-architecture weights held as plain device tensors.
 
-The forward of lm/forward.py runs on this container: the q/k/v projections
+lm/forward.py runs on this container of weights: the q/k/v projections
 are fused into one [(H + 2*Hkv)*d, hidden] weight and gate/up into one
 [2*I, hidden] weight, so each layer is four GEMMs.  Weights use the
 Hugging Face state-dict names on the way in (`from_state_dict`, `from_hf`),
@@ -196,16 +196,21 @@ def shape_from_hf_config(config) -> LlamaShape:
         max_position_embeddings=config.max_position_embeddings)
 
 
-def as_llama(model) -> Llama:
-    """Our Llama, or a transformers LlamaForCausalLM converted once and cached on it."""
+def as_llama(model, device=None) -> Llama:
+    """Our Llama, or a transformers LlamaForCausalLM converted once (onto
+    `device`, default the model's own) and cached on it."""
     if isinstance(model, Llama):
         return model
     cached = getattr(model, "_specdec_llama", None)
+    if cached is not None and (
+            (device is not None and cached.device != torch.device(device))
+            or len(cached.layers) != model.config.num_hidden_layers):
+        cached = None
     if cached is None:
         shape = shape_from_hf_config(model.config)
         state = {k: v.detach() for k, v in model.state_dict().items()}
         if shape.tie_word_embeddings is False and "lm_head.weight" not in state:
             shape = shape.replace(tie_word_embeddings=True)
-        cached = Llama.from_state_dict(shape, state)
+        cached = Llama.from_state_dict(shape, state, device=device)
         model._specdec_llama = cached
     return cached

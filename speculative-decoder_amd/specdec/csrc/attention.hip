@@ -91,12 +91,27 @@ __device__ __forceinline__ int64_t block_of(const AttnArgs &a, const TileInfo &t
 
 template <typename T> __device__ __forceinline__ float elem_f32(const T *p) { return to_f32(*p); }
 
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Combine the 4 waves of this workgroup, then the splits (last arriving
 // workgroup), and write the normalised output rows.
+//
+// Split partials cross workgroups (and XCDs) through device-coherent
+// stores and loads (agent-scope relaxed atomics: write-through / L2-bypass),
+// a wait for the stores to complete, and a relaxed arrival counter, which
+// avoids a full L2 writeback per workgroup.  The last workgroup loads every
+// split's (m, l) into LDS in parallel, reduces them per query across a wave,
+// then streams the O partials with the loads unrolled.
 template <typename T>
 __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
   __shared__ float s_m[4][kRows], s_l[4][kRows];
-  __shared__ float s_o[4][kRows][kD + 1];
+  __shared__ float s_o[4][kRows][kD + 1];  // wave partials; later the split (w, l) table
+  __shared__ float s_L[kRows];
   __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -110,14 +125,13 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
     for (int i = 0; i < 4; ++i) s_o[wave][c][16 * t + 4 * g + i] = o[t][i];
   __syncthreads();
 
+  const int r0 = ti.qt * kRows;
+  const int nq = min(kRows, ti.nrows - r0);  // real query rows in this tile
   float wm[4], wl[4], wo[4];
-  int qs[4], ds[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = tid + kAttnThreads * j;
     const int qq = idx >> 6, d = idx & 63;
-    qs[j] = qq;
-    ds[j] = d;
     float M = s_m[0][qq];
     for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
     float L = 0.0f, O = 0.0f;
@@ -133,53 +147,89 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
   }
 
   T *out = reinterpret_cast<T *>(a.out);
-  const int r0 = ti.qt * kRows;
   auto store = [&](int qq, int d, float val) {
     const int r = r0 + qq;
-    if (r >= ti.nrows) return;
     const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
     out[((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d] = from_f32<T>(val);
   };
 
   if (ti.nsplit == 1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) store(qs[j], ds[j], wo[j] / wl[j]);
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + kAttnThreads * j;
+      if ((idx >> 6) < nq) store(idx >> 6, idx & 63, wo[j] / wl[j]);
+    }
     return;
   }
 
-  // split partial: O[16][64] then (m, l)[16]
-  const int64_t base = ((int64_t)ti.unit * a.max_splits + blockIdx.y) * (kRows * (kD + 2));
-  float *ws = a.ws + base;
+  constexpr int kPart = kRows * (kD + 2);  // floats per split partial
+  float *ws = a.ws + ((int64_t)ti.unit * a.max_splits + blockIdx.y) * kPart;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    ws[qs[j] * kD + ds[j]] = wo[j];
-    if (ds[j] == 0) {
-      ws[kRows * kD + 2 * qs[j]] = wm[j];
-      ws[kRows * kD + 2 * qs[j] + 1] = wl[j];
+    const int idx = tid + kAttnThreads * j;
+    const int qq = idx >> 6, d = idx & 63;
+    if (qq >= nq) continue;
+    st_agent(ws + qq * kD + d, wo[j]);
+    if (d == 0) {
+      st_agent(ws + kRows * kD + 2 * qq, wm[j]);
+      st_agent(ws + kRows * kD + 2 * qq + 1, wl[j]);
     }
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
   __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&a.counters[ti.unit], 1) == ti.nsplit - 1);
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&a.counters[ti.unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             ti.nsplit - 1;
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * (kRows * (kD + 2));
+
+  const int ns = ti.nsplit;  // <= kMaxSplits, guaranteed by the split choice
+  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * kPart;
+  float *s_wl = &s_o[0][0][0];  // [ns][nq] pairs (weight-to-be, l)
+  for (int i = tid; i < ns * nq; i += kAttnThreads) {
+    const int sp = i / nq, qq = i - sp * nq;
+    s_wl[2 * i] = ld_agent(ws0 + sp * kPart + kRows * kD + 2 * qq);
+    s_wl[2 * i + 1] = ld_agent(ws0 + sp * kPart + kRows * kD + 2 * qq + 1);
+  }
+  __syncthreads();
+  // wave w reduces queries w, w+4, ...; lane handles splits lane, lane+64
+  for (int qq = wave; qq < nq; qq += 4) {
+    float mv[2], lv[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int sp = lane + 64 * h2;
+      mv[h2] = sp < ns ? s_wl[2 * (sp * nq + qq)] : -INFINITY;
+      lv[h2] = sp < ns ? s_wl[2 * (sp * nq + qq) + 1] : 0.0f;
+    }
+    const float M = wave_max(fmaxf(mv[0], mv[1]));
+    float part = 0.0f;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const float f = (mv[h2] == -INFINITY) ? 0.0f : expf(mv[h2] - M);
+      part += f * lv[h2];
+      const int sp = lane + 64 * h2;
+      if (sp < ns) s_wl[2 * (sp * nq + qq)] = f;
+    }
+    const float L = wave_sum(part);
+    if (lane == 0) s_L[qq] = L;
+  }
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int qq = qs[j], d = ds[j];
-    float M = -INFINITY;
-    for (int s = 0; s < ti.nsplit; ++s)
-      M = fmaxf(M, __builtin_nontemporal_load(ws0 + s * (kRows * (kD + 2)) + kRows * kD + 2 * qq));
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < ti.nsplit; ++s) {
-      const float *p = ws0 + s * (kRows * (kD + 2));
-      const float ms = __builtin_nontemporal_load(p + kRows * kD + 2 * qq);
-      const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
-      L += f * __builtin_nontemporal_load(p + kRows * kD + 2 * qq + 1);
-      O += f * __builtin_nontemporal_load(p + qq * kD + d);
+    const int idx = tid + kAttnThreads * j;
+    const int qq = idx >> 6, d = idx & 63;
+    if (qq >= nq) continue;
+    float O = 0.0f;
+    int sp = 0;
+    for (; sp + 8 <= ns; sp += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = ld_agent(ws0 + (sp + u) * kPart + qq * kD + d);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) O += s_wl[2 * ((sp + u) * nq + qq)] * v[u];
     }
-    store(qq, d, O / L);
+    for (; sp < ns; ++sp) O += s_wl[2 * (sp * nq + qq)] * ld_agent(ws0 + sp * kPart + qq * kD + d);
+    store(qq, d, O / s_L[qq]);
   }
   if (tid == 0) a.counters[ti.unit] = 0;
 }
@@ -210,7 +260,15 @@ __device__ __forceinline__ float online_update(float (&sv)[8], float &m, float &
 }
 
 // ---------------------------------------------------------------- bf16 ----
-template <bool BS16>
+// MODE 1: block_size == 16 (constant arithmetic); MODE 2: block_size % 16 == 0;
+// MODE 0: any block size (per-token addressing).
+//
+// Within a 32-token chunk starting at cs, MFMA half hf (0, 1) gives lane c
+// the K row of token cs + 8*(c/4) + 4*hf + c%4.  The S^T accumulator row
+// 4g+i of half hf is then token cs + 8g + 4hf + i, so lane group g holds the
+// scores of the 8 consecutive tokens cs+8g .. cs+8g+7 and reads their V^T
+// as one 16-byte run per dim.
+template <int MODE>
 __global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a) {
   TileInfo ti;
   if (!tile_info(a, ti)) return;
@@ -241,86 +299,85 @@ __global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  const int Hkv = a.Hkv, bs = a.bs;
+  const int Hkv = a.Hkv;
+  const int bs = (MODE == 1) ? 16 : a.bs;
+  const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
+  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
+  const int kv_len = ti.kv_len;
   const int wave_tokens = a.split / 4;
   const int w_lo = blockIdx.y * a.split + wave * wave_tokens;
-  const int w_hi = min(w_lo + wave_tokens, ti.kv_len);
+  const int w_hi = min(w_lo + wave_tokens, kv_len);
 
-  for (int c0 = w_lo; c0 < w_hi; c0 += 32) {
-    u32x4 kraw[2][2];
-    u32x2 vraw[2][4];
+  // element offset of the (block, head) tile holding token pos
+  auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
+
+  for (int c0 = w_lo; c0 < w_hi; c0 += 64) {
+    u32x4 kraw[2][2][2];  // [chunk][half][kk]
+    u32x4 vraw[2][4];     // [chunk][dim tile]
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      const int gs = c0 + 16 * gi;
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cs = c0 + 32 * ch;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) kraw[gi][kk] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) vraw[gi][tt] = u32x2{0u, 0u};
-      if (gs >= ti.kv_len) continue;
-      if (BS16) {
-        // the 16-token group lies inside one block
-        const int64_t blk = block_of(a, ti, gs);
-        const int off = gs % bs;
-        const u16 *kb = kp + ((blk * Hkv + ti.h) * bs + off + c) * kD;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) kraw[gi][kk] = *reinterpret_cast<const u32x4 *>(kb + 32 * kk + 8 * g);
-        const u16 *vb = vp + (blk * Hkv + ti.h) * (int64_t)kD * bs + off + 4 * g;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          vraw[gi][tt] = *reinterpret_cast<const u32x2 *>(vb + (int64_t)(16 * tt + c) * bs);
-      } else {
-        const int pos = gs + c;
-        if (pos < ti.kv_len) {
-          const int64_t blk = block_of(a, ti, pos);
-          const u16 *kb = kp + ((blk * Hkv + ti.h) * bs + pos % bs) * kD;
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            const u16 *src = kb + 32 * kk + 8 * g;
-            unsigned int w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = (unsigned)src[2 * e] | ((unsigned)src[2 * e + 1] << 16);
-            kraw[gi][kk] = u32x4{w[0], w[1], w[2], w[3]};
-          }
+      for (int hf = 0; hf < 2; ++hf) {
+        const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
+        const bool ok = (MODE == 0) ? tok < kv_len : (tok / bs) * bs < kv_len;
+        kraw[ch][hf][0] = kraw[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) {
+          const u16 *kb = kp + tile_of(tok) + (int64_t)(tok % bs) * kD + 8 * g;
+          kraw[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
+          kraw[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
         }
-        u16 vv[4][4];
+      }
+      const int vt = cs + 8 * g;  // first of this lane group's 8 tokens
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{0u, 0u, 0u, 0u};
+      if (MODE != 0) {
+        if ((vt / bs) * bs < kv_len) {
+          const u16 *vb = vp + tile_of(vt) + vt % bs;
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            vraw[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
+        }
+      } else {
+        unsigned int w[4][4] = {};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int pos = vt + i;
+          if (pos >= kv_len) continue;
+          const u16 *vb = vp + tile_of(pos) + pos % bs;
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            w[tt][i >> 1] |= (unsigned)vb[(int64_t)(16 * tt + c) * bs] << (16 * (i & 1));
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
+      }
+    }
+
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cs = c0 + 32 * ch;
+      if (cs >= w_hi) break;
+      float sv[8];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][0]), qop[0], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][1]), qop[1], s, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int vpos = gs + 4 * g + i;
-          const bool ok = vpos < ti.kv_len;
-          const int64_t blk = ok ? block_of(a, ti, vpos) : 0;
-          const u16 *vb = vp + (blk * Hkv + ti.h) * (int64_t)kD * bs + vpos % bs;
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) vv[tt][i] = ok ? vb[(int64_t)(16 * tt + c) * bs] : (u16)0;
+          const int pos = cs + 8 * g + 4 * hf + i;
+          const bool ok = row_ok && pos <= qpos && pos < kv_len;
+          sv[4 * hf + i] = ok ? s[i] * a.scale : -INFINITY;
         }
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          vraw[gi][tt] = u32x2{(unsigned)vv[tt][0] | ((unsigned)vv[tt][1] << 16),
-                               (unsigned)vv[tt][2] | ((unsigned)vv[tt][3] << 16)};
       }
-    }
-
-    float sv[8];
+      online_update(sv, m, l, o);
+      bf16x8 pop;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[gi][0]), qop[0], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[gi][1]), qop[1], s, 0, 0, 0);
+      for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos = c0 + 16 * gi + 4 * g + i;
-        const bool ok = row_ok && pos <= qpos && pos < ti.kv_len;
-        sv[4 * gi + i] = ok ? s[i] * a.scale : -INFINITY;
-      }
-    }
-    online_update(sv, m, l, o);
-
-    bf16x8 pop;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[j];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      u32x4 vr = u32x4{vraw[0][tt][0], vraw[0][tt][1], vraw[1][tt][0], vraw[1][tt][1]};
-      o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr), pop, o[tt], 0, 0, 0);
+      for (int tt = 0; tt < 4; ++tt)
+        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vraw[ch][tt]), pop, o[tt], 0, 0, 0);
     }
   }
   finish<__hip_bfloat16>(a, ti, m, l, o);
@@ -414,15 +471,24 @@ __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a)
 
 inline int qtiles(int width, int H, int Hkv) { return (width * (H / Hkv) + kRows - 1) / kRows; }
 
+constexpr int kMaxSplits = 128;  // (w, l) pairs of <= 128 splits x 16 rows fit the combine's LDS table
+
 inline int choose_split(int batch, int width, int H, int Hkv, int max_kv_len) {
   const int nqt = qtiles(width, H, Hkv);
-  if (nqt == 1) return kDefaultSplit;
+  if (nqt == 1) {
+    // fixed 256 up to 32768 keys, so a query's reduction order does not
+    // depend on how many queries share the call
+    const int mult = (max_kv_len + kDefaultSplit * kMaxSplits - 1) / (kDefaultSplit * kMaxSplits);
+    return kDefaultSplit * (mult > 1 ? mult : 1);
+  }
   // many query tiles (prefill): fewer, longer splits keep the workspace small
   const int64_t units = (int64_t)batch * Hkv * nqt;
   const int want = units >= 1024 ? 1 : (int)((2048 + units - 1) / units);
   int split = (max_kv_len + want - 1) / want;
   split = ((split + 127) / 128) * 128;
-  return split < kDefaultSplit ? kDefaultSplit : split;
+  if (split < kDefaultSplit) split = kDefaultSplit;
+  const int min_split = ((max_kv_len + kMaxSplits - 1) / kMaxSplits + 127) / 128 * 128;
+  return split < min_split ? min_split : split;
 }
 
 }  // namespace specdec
@@ -500,8 +566,9 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
   hipStream_t s = as_stream(stream);
   const bool bs16 = (block_size % 16) == 0;
   if (dtype == SPECDEC_BF16) {
-    if (bs16) attention_bf16_kernel<true><<<grid, block, 0, s>>>(a);
-    else attention_bf16_kernel<false><<<grid, block, 0, s>>>(a);
+    if (block_size == 16) attention_bf16_kernel<1><<<grid, block, 0, s>>>(a);
+    else if (bs16) attention_bf16_kernel<2><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<0><<<grid, block, 0, s>>>(a);
   } else if (dtype == SPECDEC_F32) {
     if (bs16) attention_f32_kernel<true><<<grid, block, 0, s>>>(a);
     else attention_f32_kernel<false><<<grid, block, 0, s>>>(a);

@@ -123,3 +123,34 @@ def test_prefill_many_query_tiles():
     """A 200-token prefill (13 query tiles per head) against SDPA."""
     for got, want in run_case(2, [0, 17], 4, 2, 16, torch.float32, 200, seed=3, rollback=False):
         assert torch.allclose(got, want, atol=2e-5, rtol=1e-5)
+
+
+def test_repeated_split_combines_stay_exact():
+    """Many back-to-back launches over the same workspace and counters (every
+    call splits 17 ways and combines in its last workgroup): each result is
+    compared with SDPA, so a stale partial or a counter left non-zero shows."""
+    d, h, hkv, bs, L = 64, 32, 32, 16, 4096
+    g = torch.Generator().manual_seed(11)
+    cache = make_cache(1, hkv, d, 300, bs, torch.bfloat16, 4)
+    cache.add(0)
+    step = cache.append([0], [L])
+    cache.write(0, step, torch.randn(1, hkv, L, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(1, hkv, L, d, generator=g).to(torch.bfloat16).cuda())
+    step = cache.append([0], [5])
+    cache.write(0, step, torch.randn(1, hkv, 5, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(1, hkv, 5, d, generator=g).to(torch.bfloat16).cuda())
+    k_all, v_all = cache.gather(0, step)
+    outs, qs = [], []
+    for i in range(40):
+        q = torch.randn(1, 5, h * d, generator=g).to(torch.bfloat16)
+        qd = q.cuda()
+        out = torch.empty(1, 5, h * d, dtype=torch.bfloat16, device="cuda")
+        ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 1, 5, h, hkv,
+                            d, bs, 0.125, step.max_total, out, out.stride(1))
+        outs.append(out)
+        qs.append(q)
+    for q, out in zip(qs, outs):
+        want = of.attention(q.view(1, 5, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
+                            torch.tensor([L]), torch.tensor([L + 5]), 0.125)
+        assert (out.view(1, 5, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
+    assert int(ops.workspace_for(torch.device("cuda", 0)).counters.abs().sum()) == 0
