@@ -62,14 +62,21 @@ def prompt_ids(seed=0):
     return torch.randint(0, V, (PROMPT,), generator=g).tolist()
 
 
-def run_e2e(target, draft, prompt, new_tokens=NEW_TOKENS):
+def make_caches(target, draft, new_tokens=NEW_TOKENS):
+    """Target and draft caches sized for one request; reused across requests
+    (sequences are freed at the end of each), as a server would."""
     from cache.kv import KVCache
+
+    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
+    return (KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda"),
+            KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda"))
+
+
+def run_e2e(target, draft, prompt, caches, new_tokens=NEW_TOKENS):
     from spec.draft import ModelDraft
     from spec.loop import generate
 
-    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
-    tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda")
-    dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda")
+    tc, dc = caches
     out, stats = generate(target, tc, ModelDraft(draft, dc), [prompt], new_tokens, k=K,
                           generator=torch.Generator().manual_seed(0))
     return out[0], stats
@@ -78,14 +85,15 @@ def run_e2e(target, draft, prompt, new_tokens=NEW_TOKENS):
 def bench_e2e(steps, warmup):
     target, draft, t_state, d_state = build_models()
     prompt = prompt_ids()
+    caches = make_caches(target, draft)
     log("e2e warmup")
     for _ in range(warmup):
-        run_e2e(target, draft, prompt)
+        run_e2e(target, draft, prompt, caches)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     outs = []
     for _ in range(steps):
-        out, stats = run_e2e(target, draft, prompt)
+        out, stats = run_e2e(target, draft, prompt, caches)
         outs.append(out)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
@@ -143,34 +151,55 @@ def setup_attention(batch, length, seed=0, h=32, hkv=32, d=64, t_new=5, num_bloc
     return cache, step, q, out
 
 
+def graph_time_us(launch, per_graph=20, replays=10):
+    """Mean GPU time of `launch` (one kernel) from HIP events around replays of
+    a graph holding `per_graph` back-to-back launches, so host launch cost
+    is not in the measurement."""
+    for _ in range(3):
+        launch()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            launch()
+    graph.replay()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000 / (per_graph * replays)
+
+
 def time_attention(batch, length, iters=200):
     from specdec import ops
 
     cache, step, q, out = setup_attention(batch, length)
     h, hkv, d = 32, 32, 64
+    ws = ops.AttentionWorkspace(q.device)
 
     def launch():
         ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, 5, h,
-                            hkv, d, BLOCK, 0.125, step.max_total, out, out.stride(1))
+                            hkv, d, BLOCK, 0.125, step.max_total, out, out.stride(1), ws)
 
-    for _ in range(10):
-        launch()
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    stream.synchronize()
-    start.record(stream)
-    for _ in range(iters):
-        launch()
-    end.record(stream)
-    end.synchronize()
-    us = start.elapsed_time(end) * 1000 / iters
+    launch()
+    us = graph_time_us(launch, per_graph=20, replays=max(iters // 20, 1))
     nbytes = attention_bytes(batch, [length] * batch)
     return {"batch": batch, "context": length, "us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
             "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
 
 
 # ------------------------------------------------------- other kernels ------
-def time_fn(fn, iters=100):
+def time_fn(fn, iters=100, graph=False):
+    if graph:
+        return graph_time_us(fn, per_graph=10, replays=max(iters // 10, 1))
     for _ in range(5):
         fn()
     stream = torch.cuda.current_stream()
@@ -200,8 +229,9 @@ def bench_kernels():
         q.view(-1, V)[torch.arange(b * k, device="cuda"), draft.view(-1)] += 1e-3
         ua = torch.rand(b, k, generator=g, device="cuda")
         ur = torch.rand(b, generator=g, device="cuda")
-        us_soft = time_fn(lambda: ops.probabilities(torch.cat([tl.view(-1, V), dl.view(-1, V)]), 1.0))
-        us_acc = time_fn(lambda: ops.accept_reject(p, q, draft, ua, ur))
+        both = torch.cat([tl.view(-1, V), dl.view(-1, V)])
+        us_soft = time_fn(lambda: ops.probabilities(both, 1.0), graph=True)
+        us_acc = time_fn(lambda: ops.accept_reject(p, q, draft, ua, ur), graph=True)
         logit_bytes = (2 * k + 1) * V * 4 * b
         res[f"accept_b{b}_k{k}"] = {"softmax_us": us_soft, "accept_us": us_acc, "logit_bytes": logit_bytes,
                                     "softmax_gbs": 2 * logit_bytes / us_soft / 1e3}
@@ -210,7 +240,7 @@ def bench_kernels():
         rows = planted_rows(16, length, V, seed=length)
         hist = torch.tensor(rows, dtype=torch.int32, device="cuda")
         lens = torch.full((16,), length, dtype=torch.int32, device="cuda")
-        us = time_fn(lambda: ops.ngram_lookup(hist, lens, 4, 3))
+        us = time_fn(lambda: ops.ngram_lookup(hist, lens, 4, 3), graph=True)
         nbytes = 16 * length * 4
         res[f"ngram_b16_L{length}"] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3}
     # config 2': cache append (rope + scatter of 5 tokens) and rollback plan
@@ -220,7 +250,7 @@ def bench_kernels():
 
     cos, sin = (t.cuda() for t in rope_tables(SMOLLM2_1_7B, 8192))
     us_app = time_fn(lambda: ops.rope_append(qkv, 32, 32, 64, cos, sin, step.meta, 1, 5, cache.table_tensor, BLOCK,
-                                             cache.k[0], cache.v[0]))
+                                             cache.k[0], cache.v[0]), graph=True)
     res["append_b1_t5"] = {"us": us_app, "bytes": 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2}
     # attention over the config-2 grid
     for b in (1, 4, 8):
@@ -230,7 +260,7 @@ def bench_kernels():
 
 
 # ------------------------------------------------------------ CPU side ------
-def cpu_baseline(t_state, d_state, prompt, new_tokens=16):
+def cpu_baseline(t_state, d_state, prompt, new_tokens=64):
     """Oracle loop on the host cores: same weights (bf16), same prompt, a
     bounded number of new tokens."""
     import oracle.forward as of

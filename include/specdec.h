@@ -188,6 +188,21 @@ int specdec_kv_gather(const void *k_pool, const void *v_pool, int dtype,
                       int32_t block_size, int32_t read_width, void *k_out,
                       void *v_out, void *stream);
 
+/* ------------------------------------------------------------ layer glue --- */
+
+/* Residual add + RMSNorm over rows of `dim` (BF16 or F32).  If delta is not
+ * null, hidden <- hidden + delta (rounded to the element type) first; then
+ * out <- weight * round(hidden * rsqrt(mean(hidden^2) + eps)).  The norm and
+ * the add follow transformers' LlamaRMSNorm and the residual adds of the
+ * decoder layer that lm/forward.py:56,64-66 runs. */
+int specdec_add_rmsnorm(void *hidden, const void *delta, const void *weight, void *out, int dtype,
+                        int64_t rows, int64_t dim, float eps, void *stream);
+
+/* out [rows, inter] = round(silu(gate)) * up, with gate_up [rows, 2*inter]
+ * holding gate then up per row (the Llama MLP activation, lm/forward.py:65). */
+int specdec_silu_mul(const void *gate_up, void *out, int dtype, int64_t rows, int64_t inter,
+                     void *stream);
+
 /* -------------------------------------------------------------- attention --- */
 
 /* Workspace needed by specdec_paged_attention for a call shape: `floats`

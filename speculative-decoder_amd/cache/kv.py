@@ -85,6 +85,7 @@ class KVCache:
         self.tables: dict[int, BlockTable] = {}
         self._store = _TableStore(max_seqs, num_blocks, self.device)
         self.bytes_per_slot = 2 * n_layers * n_kv_heads * head_dim * self.k.element_size()
+        self.graphs: dict = {}  # captured forwards over this cache (lm/graphs.py)
 
     @property
     def dtype(self) -> torch.dtype:
@@ -151,8 +152,45 @@ class KVCache:
             raise failure
         rows = [self.tables[s].row for s in seq_ids]
         meta = torch.tensor(rows + past + list(n_new), dtype=torch.int32).pin_memory()
-        meta = meta.to(self.device, non_blocking=True)
+        meta = meta.to(self.device, non_blocking=True).view(3, len(seq_ids))
         return PagedStep(self, meta, rows, past, list(n_new), width)
+
+    def append_steps(self, seq_ids: list[int], steps: list[list[int]]) -> tuple[torch.Tensor, list[PagedStep]]:
+        """Reserve slots for several consecutive appends at once, as if
+        `append(seq_ids, steps[i])` were called for i = 0, 1, ... in order (same
+        block ids, same OutOfBlocks point).  One block-plan launch and one
+        metadata upload: returns the int32 [len(steps), 3, B] device metadata
+        and a host PagedStep per step (whose `meta` is a view into it)."""
+        alloc = self.allocator
+        pops: list[tuple[int, int, int]] = []
+        host: list[int] = []
+        infos = []
+        failure = None
+        rows = [self.tables[s].row for s in seq_ids]
+        for n_new in steps:
+            past = [self.tables[s].length for s in seq_ids]
+            for seq_id, n in zip(seq_ids, n_new):
+                table = self.tables[seq_id]
+                needed = table._need(table.length + n, self.block_size)
+                if needed > alloc.num_free:
+                    failure = OutOfBlocks(f"need {needed} blocks, {alloc.num_free} free")
+                    break
+                if needed > 0:
+                    pops.append((table.row, len(table), needed))
+                    alloc._take(needed)
+                    table._n += needed
+                table.length += n
+            if failure is not None:
+                break
+            host += rows + past + list(n_new)
+            infos.append((past, list(n_new)))
+        alloc._plan(self._store, pops)
+        if failure is not None:
+            raise failure
+        metas = torch.tensor(host, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
+        metas = metas.view(len(steps), 3, len(seq_ids))
+        out = [PagedStep(self, metas[i], rows, past, n_new, max(n_new)) for i, (past, n_new) in enumerate(infos)]
+        return metas, out
 
     # -- per-layer data movement ---------------------------------------------
     def write(self, layer: int, step: PagedStep, k: torch.Tensor, v: torch.Tensor) -> None:

@@ -1,10 +1,17 @@
 """Cached Llama forward over the paged cache (reference: lm/forward.py:21-84).
 
-Per layer: RMSNorm, one fused QKV GEMM (torch/hipBLASLt), the fused RoPE +
-paged append kernel, the paged verify-attention kernel reading K/V blocks in
-place (no gather copy, no materialised mask), o_proj, RMSNorm and the SwiGLU
-MLP as two GEMMs.  The output projection runs in at least fp32, as in the
-reference (lm/forward.py:71-84).
+A forward is split in two:
+  * host part: `cache.append` decides block growth (one block-plan launch)
+    and uploads the per-row metadata (table row, past length, new tokens);
+  * device part, `forward_core`: nine launches per layer -- fused residual
+    add + RMSNorm, one fused QKV GEMM (torch/hipBLASLt), the fused RoPE +
+    paged append kernel, the paged verify-attention kernel reading K/V
+    blocks in place (no gather copy, no materialised mask), o_proj, add +
+    RMSNorm, the gate/up GEMM, SiLU*up, the down GEMM -- then the fp32
+    output projection (lm/forward.py:71-84).
+The device part reads everything it needs from device memory, so a fixed
+(batch, width) shape can be captured once in a HIP graph and replayed
+(lm/graphs.py).
 """
 from __future__ import annotations
 
@@ -17,10 +24,43 @@ from specdec import ops
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """transformers' LlamaRMSNorm: normalise in fp32, cast back, then scale."""
-    h = x.float()
-    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
-    return weight * h.to(x.dtype)
+    """transformers' LlamaRMSNorm on the GPU (fused kernel)."""
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    return ops.add_rmsnorm(x.clone(), None, weight, out, eps)
+
+
+def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Tensor, max_kv_len: int,
+                 last: torch.Tensor | None = None,
+                 workspace: ops.AttentionWorkspace | None = None) -> torch.Tensor:
+    """Device-only forward of ids [B, T] whose rows were appended with `meta`
+    (int32 [3, B] on the device).  `max_kv_len` bounds every row's cached
+    length after the append; `last` (int64 [B]) selects one row per batch
+    entry before the output projection."""
+    cfg = llama.config
+    b, t = ids.shape
+    h, hk, d, inter, eps = (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size,
+                            cfg.rms_norm_eps)
+    tables = cache.table_tensor
+    layers = llama.layers
+    hidden = F.embedding(ids, llama.embed)
+    x = torch.empty_like(hidden)
+    ops.add_rmsnorm(hidden, None, layers[0].ln1, x, eps)
+    attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
+    act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
+    for i, layer in enumerate(layers):
+        qkv = F.linear(x, layer.wqkv)
+        ops.rope_append(qkv, h, hk, d, llama.rope_cos, llama.rope_sin, meta, b, t, tables, cache.block_size,
+                        cache.k[i], cache.v[i])
+        ops.paged_attention(qkv, qkv.stride(1), cache.k[i], cache.v[i], tables, meta, b, t, h, hk, d,
+                            cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace)
+        ops.add_rmsnorm(hidden, F.linear(attn, layer.wo), layer.ln2, x, eps)
+        ops.silu_mul(F.linear(x, layer.wgu), act)
+        nxt = layers[i + 1].ln1 if i + 1 < len(layers) else llama.norm
+        ops.add_rmsnorm(hidden, F.linear(act, layer.wd), nxt, x, eps)
+    if last is not None:
+        x = x[torch.arange(b, device=x.device), last]
+    return logits(llama, x)
 
 
 @torch.no_grad()
@@ -34,31 +74,14 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
     The same call serves prefill (T = prompt length), decode (T = 1) and
     speculative verification (T = k + 1)."""
     llama = as_llama(model, cache.device)
-    cfg = llama.config
     step = cache.append(seq_ids, n_new)
     ids = input_ids.to(cache.device, non_blocking=True)
-    b, t = ids.shape
     llama.ensure_positions(step.max_total)
-    h, hk, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    hidden = F.embedding(ids, llama.embed)
-    attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
-    tables = cache.table_tensor
-    inter = cfg.intermediate_size
-    for i, layer in enumerate(llama.layers):
-        x = rms_norm(hidden, layer.ln1, cfg.rms_norm_eps)
-        qkv = F.linear(x, layer.wqkv)
-        ops.rope_append(qkv, h, hk, d, llama.rope_cos, llama.rope_sin, step.meta, b, t, tables,
-                        cache.block_size, cache.k[i], cache.v[i])
-        ops.paged_attention(qkv, qkv.stride(1), cache.k[i], cache.v[i], tables, step.meta, b, t, h, hk, d,
-                            cache.block_size, llama.scaling, step.max_total, attn, attn.stride(1))
-        hidden = hidden + F.linear(attn, layer.wo)
-        x = rms_norm(hidden, layer.ln2, cfg.rms_norm_eps)
-        gu = F.linear(x, layer.wgu)
-        hidden = hidden + F.linear(F.silu(gu[..., :inter]) * gu[..., inter:], layer.wd)
+    last = None
     if last_only:
-        last = torch.tensor([n - 1 for n in n_new], device=hidden.device)
-        hidden = hidden[torch.arange(b, device=hidden.device), last]
-    return logits(llama, rms_norm(hidden, llama.norm, cfg.rms_norm_eps))
+        last = torch.tensor([n - 1 for n in n_new], dtype=torch.int64).pin_memory().to(cache.device,
+                                                                                          non_blocking=True)
+    return forward_core(llama, cache, step.meta, ids, step.max_total, last)
 
 
 def logits(model, hidden: torch.Tensor) -> torch.Tensor:
@@ -68,6 +91,3 @@ def logits(model, hidden: torch.Tensor) -> torch.Tensor:
     llama = as_llama(model)
     wide = llama.head_wide
     return F.linear(hidden.to(wide.dtype), wide)
-
-
-__all__ = ["forward", "logits", "rms_norm", "Llama"]

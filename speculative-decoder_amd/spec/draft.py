@@ -13,7 +13,9 @@ from typing import Protocol
 import torch
 
 from cache.kv import KVCache
+from lm import graphs
 from lm.forward import forward
+from lm.model import as_llama
 from lm.sampling import probabilities
 from spec.accept import sample_inverse_cdf
 
@@ -57,6 +59,8 @@ class ModelDraft:
         # after a round that accepted every draft (d_k was sampled but never
         # fed); feeding every uncached token in the first step closes either gap.
         pending: list[list[int]] | torch.Tensor = [ctx[self.cache.length(s):] for s, ctx in zip(seq_ids, contexts)]
+        if graphs.enabled() and k > 0:
+            return self._propose_graphs(seq_ids, pending, k, temperature, generator)
         tokens, qs = [], []
         for _ in range(k):
             q = probabilities(run(self.model, self.cache, seq_ids, pending), temperature)
@@ -65,6 +69,32 @@ class ModelDraft:
             qs.append(q)
             pending = token[:, None]
         return torch.stack(tokens, dim=1), torch.stack(qs, dim=1)
+
+    def _propose_graphs(self, seq_ids, pending, k, temperature, generator):
+        """The same k steps as one block plan + one metadata upload, then two
+        graph replays: the first step (right-padded pending tokens) and the
+        chain of k-1 one-token steps, tokens staying on the device."""
+        cache = self.cache
+        b = len(seq_ids)
+        llama = as_llama(self.model, cache.device)
+        n_first = [len(p) for p in pending]
+        width = max(n_first)
+        metas, steps = cache.append_steps(seq_ids, [n_first] + [[1] * b] * (k - 1))
+        max_total = steps[-1].max_total
+        llama.ensure_positions(max_total)
+        bucket = graphs.bucket_for(max_total)
+        # the reference draws one uniform per row per step, in step order
+        dev = generator.device if generator is not None else torch.device("cpu")
+        u = torch.stack([torch.rand(b, generator=generator, dtype=torch.float32, device=dev) for _ in range(k)])
+        u = u.to(cache.device, non_blocking=True)
+        ids = torch.tensor([p + [0] * (width - len(p)) for p in pending], dtype=torch.int64)
+        first = graphs.get(cache, graphs.DraftStepGraph, llama, b, width, float(temperature), bucket)
+        q0, t0 = first.run(ids, metas[0], u[0])
+        if k == 1:
+            return t0.clone().view(b, 1), q0.clone().view(b, 1, -1)
+        chain = graphs.get(cache, graphs.DraftChainGraph, llama, b, k - 1, float(temperature), bucket)
+        qs, toks = chain.run(t0, metas[1:], u[1:])
+        return torch.cat([t0.view(b, 1), toks], dim=1), torch.cat([q0.view(b, 1, -1), qs], dim=1)
 
     def rollback(self, seq_id: int, keep: int) -> None:
         self.cache.truncate(seq_id, min(self.cache.length(seq_id), keep))

@@ -4,7 +4,9 @@ from __future__ import annotations
 import torch
 
 from cache.kv import KVCache
+from lm import graphs
 from lm.forward import forward
+from lm.model import as_llama
 from lm.sampling import probabilities
 
 
@@ -22,6 +24,13 @@ def verify(target, cache: KVCache, seq_ids: list[int], contexts: list[list[int]]
             raise RuntimeError(f"seq {seq_id}: target cache holds {cache.length(seq_id)}, expected {len(ctx) - 1}")
     last = torch.tensor([[ctx[-1]] for ctx in contexts], dtype=torch.int64).to(cache.device, non_blocking=True)
     input_ids = torch.cat([last, draft.to(cache.device, torch.int64)], dim=1)
-    k1 = input_ids.shape[1]
-    logits = forward(target, cache, seq_ids, input_ids, [k1] * len(seq_ids))
-    return probabilities(logits, temperature)
+    b, k1 = input_ids.shape
+    if not graphs.enabled():
+        return probabilities(forward(target, cache, seq_ids, input_ids, [k1] * b), temperature)
+    llama = as_llama(target, cache.device)
+    step = cache.append(seq_ids, [k1] * b)
+    llama.ensure_positions(step.max_total)
+    runner = graphs.get(cache, graphs.VerifyGraph, llama, b, k1, float(temperature),
+                        graphs.bucket_for(step.max_total))
+    # a copy: the runner's output buffer is overwritten by its next replay
+    return runner.run(input_ids, step.meta).clone()

@@ -190,6 +190,26 @@ def kv_gather(k_pool, v_pool, meta, batch, tables, block_size, read_width):
     return k_out, v_out
 
 
+# -------------------------------------------------------------- layer glue --
+def add_rmsnorm(hidden: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor, out: torch.Tensor,
+                eps: float) -> torch.Tensor:
+    """hidden += delta (if given), out = RMSNorm(hidden) * weight; rows are the
+    leading dims.  hidden and out must be contiguous."""
+    dim = hidden.shape[-1]
+    st = lib().specdec_add_rmsnorm(hidden.data_ptr(), ptr(delta), weight.data_ptr(), out.data_ptr(),
+                                   dtype_code(hidden), hidden.numel() // dim, dim, float(eps), stream())
+    _check(st, "add_rmsnorm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    inter = gate_up.shape[-1] // 2
+    st = lib().specdec_silu_mul(gate_up.data_ptr(), out.data_ptr(), dtype_code(gate_up), gate_up.numel() // (2 * inter),
+                                inter, stream())
+    _check(st, "silu_mul")
+    return out
+
+
 # --------------------------------------------------------------- attention --
 class AttentionWorkspace:
     """Grow-only split-KV partials and arrival counters for one device.

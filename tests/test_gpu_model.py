@@ -232,3 +232,28 @@ def test_sampled_loop_matches_oracle_loop(tiny, tiny_draft, temperature):
     assert got_out == want_out
     assert (got.rounds, got.accepted, got.attempts, got.accepts) == (want.rounds, want.accepted, want.attempts,
                                                                      want.accepts)
+
+
+@pytest.mark.parametrize("temperature", [0.0, 1.0])
+def test_graph_replay_equals_eager_launches(tiny, tiny_draft, monkeypatch, temperature):
+    """The captured verify and draft graphs produce the same tokens and
+    statistics as the same kernels launched one by one."""
+    prompts = random_prompts(5, 256, seed=12)
+    runs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("SPECDEC_GRAPHS", flag)
+        out, stats = generate(tiny, new_cache(tiny), ModelDraft(tiny_draft, new_cache(tiny_draft)), prompts, 30, 4,
+                              temperature=temperature, generator=torch.Generator().manual_seed(3))
+        runs.append((out, stats.rounds, stats.accepted, stats.emitted_per_round))
+    assert runs[0] == runs[1]
+
+
+def test_graphs_are_reused_across_requests(tiny, tiny_draft, prompts, expected):
+    """One cache pair serving several requests in turn: graphs captured for the
+    first are replayed for the next, and outputs stay exact."""
+    tc, dc = new_cache(tiny), new_cache(tiny_draft)
+    for p, want in zip(prompts[:6], expected[:6]):
+        out, _ = generate(tiny, tc, ModelDraft(tiny_draft, dc), [p], MAX_NEW, k=4)
+        assert out[0] == want
+    assert len(tc.graphs) >= 1 and len(dc.graphs) >= 1
+    assert tc.allocator.num_used == 0 and dc.allocator.num_used == 0
