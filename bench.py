@@ -318,7 +318,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels"], default="all")
+    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -337,6 +337,19 @@ def main():
         return
     if args.only == "kernels":
         print(json.dumps(bench_kernels()))
+        return
+    if args.only == "copy":
+        # reference copy of a known size for scaling the FETCH_SIZE / WRITE_SIZE counters
+        x = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(max(args.steps, 1)):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": x.numel() * 4, "launches": max(args.steps, 1)}))
+        return
+    if args.only == "e2e":
+        e2e, _ = bench_e2e(args.steps, args.warmup)
+        print(json.dumps({"e2e": e2e}))
         return
 
     e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
