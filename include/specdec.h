@@ -206,12 +206,11 @@ int specdec_silu_mul(const void *gate_up, void *out, int dtype, int64_t rows, in
 /* -------------------------------------------------------------- attention --- */
 
 /* Workspace needed by specdec_paged_attention for a call shape: `floats`
- * fp32 elements of split partials and `counters` int32 arrival counters (the
- * counters must be zero before the first call; the kernel leaves them zero). */
+ * fp32 elements of split partials (no initialisation needed). */
 int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
                                 int32_t n_kv_heads, int32_t head_dim,
                                 int32_t max_kv_len, int32_t split_tokens,
-                                int64_t *floats, int64_t *counters);
+                                int64_t *floats);
 
 /* Split-KV size the attention kernel uses for a call shape (tokens per
  * workgroup; a fixed 256 whenever all queries of a kv head fit one 16-row
@@ -225,7 +224,9 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * place).  q token (b, t), head h at q + (b*width + t)*q_token_stride +
  * h*head_dim; out likewise with out_token_stride.  Softmax in fp32 with
  * `scale`; QK^T and PV on MFMA (bf16) or fp32 MFMA (F32).  Query rows with
- * t >= n_new[b] are not written.  head_dim must be 64.
+ * t >= n_new[b] are not written.  head_dim must be 64.  When a row needs
+ * more than one split, a second kernel combining the split partials is
+ * launched on the same stream; calls sharing a workspace must be ordered.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
  * cache/kv.py:108-112. */
 int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
@@ -234,8 +235,7 @@ int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
                             const int32_t *meta, int32_t batch, int32_t width,
                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                             int32_t block_size, float scale, int32_t max_kv_len,
-                            float *workspace, int64_t workspace_floats,
-                            int32_t *counters, int64_t n_counters, void *out,
+                            float *workspace, int64_t workspace_floats, void *out,
                             int64_t out_token_stride, void *stream);
 
 #ifdef __cplusplus

@@ -74,15 +74,8 @@ class _Captured:
         dev = cache.device
         self.ws = ops.AttentionWorkspace(dev)
         cfg = llama.config
-        import ctypes
-
-        from specdec._lib import lib
-
-        floats, counters = ctypes.c_int64(), ctypes.c_int64()
-        ops._check(lib().specdec_attention_workspace(batch, width, cfg.num_attention_heads, cfg.num_key_value_heads,
-                                                     cfg.head_dim, bucket, 0, ctypes.byref(floats),
-                                                     ctypes.byref(counters)), "attention_workspace")
-        self.ws.reserve(floats.value, counters.value)
+        self.ws.reserve(ops.attention_workspace_floats(batch, width, cfg.num_attention_heads, cfg.num_key_value_heads,
+                                                       cfg.head_dim, bucket))
         self.graph = None
         self.outs = None
         self._ptrs = None

@@ -5,11 +5,13 @@
 // Reference semantics: lm/sampling.py:13-18 (probabilities),
 // spec/accept.py:18-26 (residual), :29-35 (inverse CDF), :44-79 (accept).
 //
-// Layout: one workgroup per row (softmax) or per batch entry (accept), the
-// vocab split into contiguous per-thread chunks so the inverse-CDF scan is a
-// chunk sum, a workgroup exclusive scan of the chunk sums, and a re-walk of
-// each chunk.  The vocab rows are streamed from HBM; re-reads of the same
-// row within one workgroup hit L2.
+// Layout: one workgroup per row (softmax) or per batch entry (accept).  Rows
+// are walked in tiles of 4 elements per thread, so every load instruction
+// is a coalesced 16-byte-per-lane read.  The inverse-CDF search accumulates
+// the CDF in fp64 tile by tile (a fixed-order workgroup reduction per tile
+// and a running carry), finds the tile whose end prefix passes the target,
+// and scans only that tile element by element.  Re-reads of a row within
+// one workgroup hit L2.
 #include "common.h"
 
 #include <float.h>
@@ -72,14 +74,22 @@ __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
     return;
   }
 
-  // logits.float() / T, then a max-shifted softmax with fp32 exp and sum
-  float m = -INFINITY;
-  for (int64_t i = tid; i < vocab; i += blockDim.x) m = fmaxf(m, to_f32(x[i]) / temperature);
-  m = block_max(m, red_f);
-  float s = 0.0f;
-  for (int64_t i = tid; i < vocab; i += blockDim.x) s += expf(to_f32(x[i]) / temperature - m);
+  // logits.float() / T, then a max-shifted softmax: one pass keeps a running
+  // (max, sum) per thread, merged across the workgroup; a second pass writes
+  float m = -INFINITY, s = 0.0f;
+  for (int64_t i = tid; i < vocab; i += blockDim.x) {
+    const float v = to_f32(x[i]) / temperature;
+    if (v > m) {
+      s = (m == -INFINITY) ? 0.0f : s * expf(m - v);
+      m = v;
+    }
+    s += expf(v - m);
+  }
+  const float mg = block_max(m, red_f);
+  s = (m == -INFINITY) ? 0.0f : s * expf(m - mg);
   s = block_sum(s, red_f);
-  for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = expf(to_f32(x[i]) / temperature - m) / s;
+  const float inv = 1.0f / s;
+  for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = expf(to_f32(x[i]) / temperature - mg) * inv;
 }
 
 // ------------------------------------------- accept stage (per batch) ----
@@ -105,32 +115,65 @@ __device__ __forceinline__ void accept_stage(const T *p, const T *q, int64_t p_b
   *bad_out = bad;
 }
 
-// Inverse-CDF sample of one row whose element i is produced by `elem(i)`.
-// Thread chunks are contiguous so the scan order is: fp64 chunk sums, an
-// fp64 workgroup scan over chunks, then a sequential fp64 walk per chunk,
-// each prefix rounded to T and compared against target = T(u * cdf[-1]).
+// Inverse-CDF sample of one row whose element i is produced by `elem(i)`:
+// the index of the first prefix sum (accumulated in fp64, rounded to T)
+// that exceeds target = T(u * T(total)), clamped to vocab-1.
+// Tile j covers elements [j*TILE, (j+1)*TILE), 4 consecutive per thread.
+// Every prefix is computed one way only: the carry into the tile, plus a
+// fixed-order workgroup exclusive scan of the per-thread sums, plus the
+// thread's own elements in order.  Pass 1 runs that over every tile and
+// keeps the prefix at each tile's end; pass 2 recomputes the one tile whose
+// end prefix first exceeds the target -- the same arithmetic, so the same
+// bits -- and counts its prefixes that do not.
+constexpr int kCdfPerThread = 4;
+constexpr int kMaxTiles = 64;  // vocab <= 64 * 4 * blockDim.x
+
 template <typename T, typename Elem>
-__device__ int64_t inverse_cdf_row(Elem elem, int64_t vocab, T u, double *scratch) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int64_t chunk = (vocab + nt - 1) / nt;
-  const int64_t lo = min<int64_t>((int64_t)tid * chunk, vocab);
-  const int64_t hi = min<int64_t>(lo + chunk, vocab);
+__device__ double cdf_tile(Elem elem, int64_t vocab, int64_t tile, int j, double carry, T target, double *scratch,
+                           double *s_end, int *count) {
+  const int tid = threadIdx.x;
+  const int64_t base = j * tile + (int64_t)tid * kCdfPerThread;
+  T v[kCdfPerThread];
   double local = 0.0;
-  for (int64_t i = lo; i < hi; ++i) local += (double)elem(i);
-  double total;
-  const double prefix = block_exclusive_scan(local, scratch, &total);
-  const T last = round_to(total, T());
-  const T target = u * last;
-  // count prefixes <= target; cdf is monotone, so this is searchsorted(right)
-  int64_t count = 0;
-  double acc = prefix;
-  for (int64_t i = lo; i < hi; ++i) {
-    acc += (double)elem(i);
-    if (round_to(acc, T()) <= target) ++count;
+#pragma unroll
+  for (int e = 0; e < kCdfPerThread; ++e) {
+    v[e] = base + e < vocab ? elem(base + e) : T(0);
+    local += (double)v[e];
   }
+  double unused;
+  double run = carry + block_exclusive_scan(local, scratch, &unused);
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < kCdfPerThread; ++e) {
+    if (base + e >= vocab) break;
+    run += (double)v[e];
+    if (round_to(run, T()) <= target) ++c;
+    if (base + e == min(vocab, (j + 1) * tile) - 1) *s_end = run;  // the tile's last element
+  }
+  *count = c;
   __syncthreads();
-  const double all = block_sum((double)count, scratch);
-  int64_t idx = (int64_t)all;
+  return *s_end;
+}
+
+template <typename T, typename Elem>
+__device__ int64_t inverse_cdf_row(Elem elem, int64_t vocab, T u, double *scratch, double *carry) {
+  __shared__ double s_end;
+  const int64_t tile = (int64_t)blockDim.x * kCdfPerThread;
+  const int ntiles = (int)((vocab + tile - 1) / tile);
+  double acc = 0.0;
+  int count;
+  for (int j = 0; j < ntiles; ++j) {
+    acc = cdf_tile<T>(elem, vocab, tile, j, acc, T(0), scratch, &s_end, &count);
+    if (threadIdx.x == 0) carry[j] = acc;  // prefix at the end of tile j
+    __syncthreads();
+  }
+  const T target = u * round_to(acc, T());
+  int jt = ntiles;
+  for (int j = 0; j < ntiles; ++j)
+    if (round_to(carry[j], T()) > target) { jt = j; break; }
+  if (jt == ntiles) return vocab - 1;
+  cdf_tile<T>(elem, vocab, tile, jt, jt == 0 ? 0.0 : carry[jt - 1], target, scratch, &s_end, &count);
+  const int64_t idx = jt * tile + (int64_t)block_sum((double)count, scratch);
   return idx > vocab - 1 ? vocab - 1 : idx;
 }
 
@@ -141,6 +184,7 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_kernel(
     const T *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab,
     int64_t *__restrict__ out) {
   __shared__ double scratch[kAcceptThreads / kWave + 1];
+  __shared__ double carry[kMaxTiles];
   __shared__ int64_t s_n;
   const int64_t b = blockIdx.x;
   if (threadIdx.x == 0) {
@@ -173,7 +217,7 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_kernel(
     r = r > T(0) ? r : T(0);
     return r / denom;
   };
-  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u_residual[b], scratch);
+  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u_residual[b], scratch, carry);
   if (threadIdx.x == 0) out[batch + b] = idx;
 }
 
@@ -196,10 +240,11 @@ __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_kernel(
     const T *__restrict__ probs, int64_t vocab, int64_t row_stride, const T *__restrict__ u,
     int64_t *__restrict__ out) {
   __shared__ double scratch[kAcceptThreads / kWave + 1];
+  __shared__ double carry[kMaxTiles];
   const int64_t b = blockIdx.x;
   const T *row = probs + b * row_stride;
   auto elem = [=](int64_t i) -> T { return row[i]; };
-  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u[b], scratch);
+  const int64_t idx = inverse_cdf_row<T>(elem, vocab, u[b], scratch, carry);
   if (threadIdx.x == 0) out[b] = idx;
 }
 
@@ -217,7 +262,7 @@ __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64
 
 using namespace specdec;
 
-SPECDEC_API int specdec_abi_version(void) { return 1; }
+SPECDEC_API int specdec_abi_version(void) { return 2; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,
@@ -252,6 +297,7 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
                                       const void *u_residual, int64_t batch, int64_t k,
                                       int64_t vocab, int64_t *out, void *stream) {
   if (batch < 0 || k < 0 || vocab <= 0) return SPECDEC_EINVAL;
+  if (vocab > (int64_t)kMaxTiles * kCdfPerThread * kAcceptThreads) return SPECDEC_EUNSUPPORTED;
   if (batch == 0) return SPECDEC_OK;
   if (!p || !out || !u_residual || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
   dim3 grid((unsigned)batch), block(kAcceptThreads);
@@ -302,6 +348,7 @@ SPECDEC_API int specdec_sample_inverse_cdf(const void *probs, int dtype, int64_t
                                            int64_t vocab, int64_t row_stride, const void *u,
                                            int64_t *out, void *stream) {
   if (batch < 0 || vocab <= 0) return SPECDEC_EINVAL;
+  if (vocab > (int64_t)kMaxTiles * kCdfPerThread * kAcceptThreads) return SPECDEC_EUNSUPPORTED;
   if (batch == 0) return SPECDEC_OK;
   if (!probs || !u || !out) return SPECDEC_EINVAL;
   dim3 grid((unsigned)batch), block(kAcceptThreads);

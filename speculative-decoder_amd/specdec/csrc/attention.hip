@@ -22,8 +22,9 @@
 // tile.  All per-query statistics live in lane column c, so the running
 // rescale is lane-local.
 //
-// Splits are combined through a workspace by the last workgroup of each
-// (batch, head, tile) to arrive (atomic counter, reset by that workgroup).
+// Splits write (O / l, lse) partials to a workspace; a second small kernel
+// (attention_combine_kernel), launched right after on the same stream,
+// folds them per (batch, head, tile).
 // Every query's reduction order depends only on the absolute key positions,
 // never on how many queries share the call, so a token verified among k+1
 // gets the same bits as the same token decoded alone.
@@ -42,6 +43,7 @@ constexpr int kD = 64;            // head dim
 constexpr int kAttnThreads = 256;  // 4 waves
 constexpr int kRows = 16;          // query rows per tile
 constexpr int kDefaultSplit = 256;
+constexpr int kPart = kRows * (kD + 1);  // floats per split partial: O/l [16][64], lse [16]
 
 struct AttnArgs {
   const void *q;
@@ -55,7 +57,6 @@ struct AttnArgs {
   float scale;
   int split, max_splits, n_qtiles;
   float *ws;
-  int32_t *counters;
   void *out;
   int64_t out_stride;
 };
@@ -64,7 +65,7 @@ struct TileInfo {
   int b, h, qt, group, row, past, nrows, kv_len, nsplit, unit;
 };
 
-__device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti) {
+__device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
   const int unit = blockIdx.x;
   ti.unit = unit;
   ti.qt = unit % a.n_qtiles;
@@ -81,7 +82,8 @@ __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti) {
   const int t_hi = min(r0 + kRows - 1, ti.nrows - 1) / ti.group;
   ti.kv_len = ti.past + t_hi + 1;
   ti.nsplit = (ti.kv_len + a.split - 1) / a.split;
-  if ((int)blockIdx.y >= ti.nsplit || ti.nsplit > a.max_splits) return false;
+  if (ti.nsplit > a.max_splits) return false;
+  if (!any_split && (int)blockIdx.y >= ti.nsplit) return false;
   return true;
 }
 
@@ -99,20 +101,21 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 }
 
 // Combine the 4 waves of this workgroup, then the splits (last arriving
-// workgroup), and write the normalised output rows.
+// workgroup), and write the normalised output rows.  Statistics are in the
+// log2 domain: a wave's (m, l, o) mean o / l = sum_j 2^(t_j - m) v_j / sum_j 2^(t_j - m)
+// with t_j the score times scale * log2(e).
 //
-// Split partials cross workgroups (and XCDs) through device-coherent
-// stores and loads (agent-scope relaxed atomics: write-through / L2-bypass),
-// a wait for the stores to complete, and a relaxed arrival counter, which
-// avoids a full L2 writeback per workgroup.  The last workgroup loads every
-// split's (m, l) into LDS in parallel, reduces them per query across a wave,
-// then streams the O partials with the loads unrolled.
+// Split partials cross workgroups (and XCDs) as (O / l, lse = m + log2 l)
+// through device-coherent stores and loads (agent-scope relaxed atomics:
+// write-through / L2-bypass), a wait for the stores to complete, and a
+// relaxed arrival counter -- no full L2 writeback per workgroup.  The last
+// workgroup reads every split in one pass: thread (q, 4 dims) loads the
+// split lse values and float4 rows in groups of 16 splits and folds them
+// with a running maximum, in split order.
 template <typename T>
 __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
   __shared__ float s_m[4][kRows], s_l[4][kRows];
-  __shared__ float s_o[4][kRows][kD + 1];  // wave partials; later the split (w, l) table
-  __shared__ float s_L[kRows];
-  __shared__ int s_last;
+  __shared__ float s_o[4][kRows][kD + 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   if (g == 0) {
@@ -127,127 +130,124 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
 
   const int r0 = ti.qt * kRows;
   const int nq = min(kRows, ti.nrows - r0);  // real query rows in this tile
-  float wm[4], wl[4], wo[4];
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;  // this thread: row qq, dims d0..d0+3
+  float M = s_m[0][qq];
+  for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
+  float L = 0.0f, O[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < 4; ++w) {
+    const float mw = s_m[w][qq];
+    const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+    L += f * s_l[w][qq];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kAttnThreads * j;
-    const int qq = idx >> 6, d = idx & 63;
-    float M = s_m[0][qq];
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
-    float L = 0.0f, O = 0.0f;
-    for (int w = 0; w < 4; ++w) {
-      const float mw = s_m[w][qq];
-      const float f = (mw == -INFINITY) ? 0.0f : expf(mw - M);
-      L += f * s_l[w][qq];
-      O += f * s_o[w][qq][d];
-    }
-    wm[j] = M;
-    wl[j] = L;
-    wo[j] = O;
+    for (int i = 0; i < 4; ++i) O[i] += f * s_o[w][qq][d0 + i];
   }
 
   T *out = reinterpret_cast<T *>(a.out);
-  auto store = [&](int qq, int d, float val) {
+  auto store4 = [&](const float (&val)[4]) {
     const int r = r0 + qq;
     const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
-    out[((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d] = from_f32<T>(val);
+    T *dst = out + ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(val[i]);
   };
 
   if (ti.nsplit == 1) {
+    if (qq < nq) {
+      float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = tid + kAttnThreads * j;
-      if ((idx >> 6) < nq) store(idx >> 6, idx & 63, wo[j] / wl[j]);
+      for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
+      store4(v);
     }
     return;
   }
 
-  constexpr int kPart = kRows * (kD + 2);  // floats per split partial
+  // split partial for the combine kernel: O / l [16][64] and lse [16]
   float *ws = a.ws + ((int64_t)ti.unit * a.max_splits + blockIdx.y) * kPart;
+  if (qq < nq) {
+    const bool any = L > 0.0f;
+    f32x4 v;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kAttnThreads * j;
-    const int qq = idx >> 6, d = idx & 63;
-    if (qq >= nq) continue;
-    st_agent(ws + qq * kD + d, wo[j]);
-    if (d == 0) {
-      st_agent(ws + kRows * kD + 2 * qq, wm[j]);
-      st_agent(ws + kRows * kD + 2 * qq + 1, wl[j]);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = any ? O[i] / L : 0.0f;
+    *reinterpret_cast<f32x4 *>(ws + qq * kD + d0) = v;
+    if (d0 == 0) ws[kRows * kD + qq] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
   }
-  __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
-  __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&a.counters[ti.unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             ti.nsplit - 1;
-  __syncthreads();
-  if (!s_last) return;
-
-  const int ns = ti.nsplit;  // <= kMaxSplits, guaranteed by the split choice
-  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * kPart;
-  float *s_wl = &s_o[0][0][0];  // [ns][nq] pairs (weight-to-be, l)
-  for (int i = tid; i < ns * nq; i += kAttnThreads) {
-    const int sp = i / nq, qq = i - sp * nq;
-    s_wl[2 * i] = ld_agent(ws0 + sp * kPart + kRows * kD + 2 * qq);
-    s_wl[2 * i + 1] = ld_agent(ws0 + sp * kPart + kRows * kD + 2 * qq + 1);
-  }
-  __syncthreads();
-  // wave w reduces queries w, w+4, ...; lane handles splits lane, lane+64
-  for (int qq = wave; qq < nq; qq += 4) {
-    float mv[2], lv[2];
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int sp = lane + 64 * h2;
-      mv[h2] = sp < ns ? s_wl[2 * (sp * nq + qq)] : -INFINITY;
-      lv[h2] = sp < ns ? s_wl[2 * (sp * nq + qq) + 1] : 0.0f;
-    }
-    const float M = wave_max(fmaxf(mv[0], mv[1]));
-    float part = 0.0f;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const float f = (mv[h2] == -INFINITY) ? 0.0f : expf(mv[h2] - M);
-      part += f * lv[h2];
-      const int sp = lane + 64 * h2;
-      if (sp < ns) s_wl[2 * (sp * nq + qq)] = f;
-    }
-    const float L = wave_sum(part);
-    if (lane == 0) s_L[qq] = L;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + kAttnThreads * j;
-    const int qq = idx >> 6, d = idx & 63;
-    if (qq >= nq) continue;
-    float O = 0.0f;
-    int sp = 0;
-    for (; sp + 8 <= ns; sp += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = ld_agent(ws0 + (sp + u) * kPart + qq * kD + d);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) O += s_wl[2 * ((sp + u) * nq + qq)] * v[u];
-    }
-    for (; sp < ns; ++sp) O += s_wl[2 * (sp * nq + qq)] * ld_agent(ws0 + sp * kPart + qq * kD + d);
-    store(qq, d, O / s_L[qq]);
-  }
-  if (tid == 0) a.counters[ti.unit] = 0;
 }
 
-// Online-softmax update shared by both element types.  sv[8]: scaled,
-// masked scores of this lane's 8 tokens (-inf where not visible).
-__device__ __forceinline__ float online_update(float (&sv)[8], float &m, float &l, f32x4 (&o)[4]) {
+// Final combine of the split partials, one workgroup per (row, head, tile)
+// with more than one split: thread (q, 4 dims) folds every split in split
+// order; loads go out 32 splits at a time, each group rescaled once to its
+// maximum.
+__global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArgs a, int dtype) {
+  TileInfo ti;
+  if (!tile_info(a, ti, /*any_split=*/true) || ti.nsplit == 1) return;
+  const int tid = threadIdx.x;
+  const int r0 = ti.qt * kRows;
+  const int nq = min(kRows, ti.nrows - r0);
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  if (qq >= nq) return;
+  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * kPart;
+  const int ns = ti.nsplit;
+  float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < ns; s0 += 32) {
+    // every load is issued before any is used: addresses past the last
+    // split are clamped to it and their weight forced to zero
+    float lse[32];
+    f32x4 ov[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const float *p = ws0 + (int64_t)min(s0 + u, ns - 1) * kPart;
+      lse[u] = p[kRows * kD + qq];
+      ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
+    }
+    float Mg = Mx;
+#pragma unroll
+    for (int u = 0; u < 32; ++u)
+      if (s0 + u < ns) Mg = fmaxf(Mg, lse[u]);
+    if (Mg > Mx) {  // rescale what is accumulated to the new maximum
+      const float r = (Mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(Mx - Mg);
+      den *= r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) num[i] *= r;
+      Mx = Mg;
+    }
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const float w = (s0 + u >= ns || lse[u] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(lse[u] - Mx);
+      den += w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) num[i] += w * ov[u][i];
+    }
+  }
+  const int r = r0 + qq;
+  const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
+  const int64_t off = ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
+  if (dtype == SPECDEC_BF16) {
+    __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) + off;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = __float2bfloat16(num[i] / den);
+  } else {
+    float *dst = reinterpret_cast<float *>(a.out) + off;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = num[i] / den;
+  }
+}
+
+// Online-softmax update over N scores per lane (t = score * scale * log2 e,
+// -inf where not visible), replaced by their weights 2^(t - m).
+template <int N>
+__device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l, f32x4 (&o)[4]) {
   float cm = sv[0];
 #pragma unroll
-  for (int j = 1; j < 8; ++j) cm = fmaxf(cm, sv[j]);
+  for (int j = 1; j < N; ++j) cm = fmaxf(cm, sv[j]);
   cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
   cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
   const float m_new = fmaxf(m, cm);
-  const float alpha = (m == -INFINITY) ? 0.0f : expf(m - m_new);
+  const float alpha = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+  const float mu = (m_new == -INFINITY) ? 0.0f : m_new;
   float ps = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    sv[j] = (sv[j] == -INFINITY) ? 0.0f : expf(sv[j] - m_new);
+  for (int j = 0; j < N; ++j) {
+    sv[j] = __builtin_amdgcn_exp2f(sv[j] - mu);
     ps += sv[j];
   }
   ps += __shfl_xor(ps, 16, 64);
@@ -256,7 +256,6 @@ __device__ __forceinline__ float online_update(float (&sv)[8], float &m, float &
 #pragma unroll
   for (int t = 0; t < 4; ++t) o[t] *= alpha;
   m = m_new;
-  return alpha;
 }
 
 // ---------------------------------------------------------------- bf16 ----
@@ -300,6 +299,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a
   float m = -INFINITY, l = 0.0f;
 
   const int Hkv = a.Hkv;
+  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
   const int bs = (MODE == 1) ? 16 : a.bs;
   const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
   const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
@@ -354,27 +354,36 @@ __global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a
       }
     }
 
+    // scores of both chunks (S^T = K Q^T), in log2 units
+    float sv[16];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      const int cs = c0 + 32 * ch;
-      if (cs >= w_hi) break;
-      float sv[8];
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
         s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][0]), qop[0], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][1]), qop[1], s, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int pos = cs + 8 * g + 4 * hf + i;
-          const bool ok = row_ok && pos <= qpos && pos < kv_len;
-          sv[4 * hf + i] = ok ? s[i] * a.scale : -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = s[i] * c2;
       }
-      online_update(sv, m, l, o);
+    }
+    // keys past a query's position (or past kv_len) only occur in chunks
+    // reaching beyond `past`; elsewhere every score is visible
+    if (c0 + 64 > ti.past) {
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int pos = c0 + 32 * ch + 8 * g + j;
+          if (!(row_ok && pos <= qpos && pos < kv_len)) sv[8 * ch + j] = -INFINITY;
+        }
+    }
+    online_update<16>(sv, m, l, o);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
       bf16x8 pop;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[j];
+      for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[8 * ch + j];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
         o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vraw[ch][tt]), pop, o[tt], 0, 0, 0);
@@ -454,7 +463,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a)
       for (int i = 0; i < 4; ++i) {
         const int pos = gs + 4 * g + i;
         const bool ok = row_ok && pos <= qpos && pos < ti.kv_len;
-        sv[4 * gi + i] = ok ? s4[i] * a.scale : -INFINITY;
+        sv[4 * gi + i] = ok ? s4[i] * (a.scale * 1.4426950408889634f) : -INFINITY;
       }
     }
     online_update(sv, m, l, o);
@@ -471,7 +480,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a)
 
 inline int qtiles(int width, int H, int Hkv) { return (width * (H / Hkv) + kRows - 1) / kRows; }
 
-constexpr int kMaxSplits = 128;  // (w, l) pairs of <= 128 splits x 16 rows fit the combine's LDS table
+constexpr int kMaxSplits = 128;  // bounds the split workspace of one (row, head, tile)
 
 inline int choose_split(int batch, int width, int H, int Hkv, int max_kv_len) {
   const int nqt = qtiles(width, H, Hkv);
@@ -485,9 +494,9 @@ inline int choose_split(int batch, int width, int H, int Hkv, int max_kv_len) {
   const int64_t units = (int64_t)batch * Hkv * nqt;
   const int want = units >= 1024 ? 1 : (int)((2048 + units - 1) / units);
   int split = (max_kv_len + want - 1) / want;
-  split = ((split + 127) / 128) * 128;
+  split = ((split + 255) / 256) * 256;  // waves take 64-token steps
   if (split < kDefaultSplit) split = kDefaultSplit;
-  const int min_split = ((max_kv_len + kMaxSplits - 1) / kMaxSplits + 127) / 128 * 128;
+  const int min_split = ((max_kv_len + kMaxSplits - 1) / kMaxSplits + 255) / 256 * 256;
   return split < min_split ? min_split : split;
 }
 
@@ -504,8 +513,8 @@ SPECDEC_API int specdec_attention_split(int32_t batch, int32_t width, int32_t n_
 SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
                                             int32_t n_kv_heads, int32_t head_dim,
                                             int32_t max_kv_len, int32_t split_tokens,
-                                            int64_t *floats, int64_t *counters) {
-  if (!floats || !counters || batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 ||
+                                            int64_t *floats) {
+  if (!floats || batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 ||
       n_heads % n_kv_heads || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
@@ -514,8 +523,7 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
                                 max_kv_len);
   const int64_t units = (int64_t)batch * n_kv_heads * qtiles(width, n_heads, n_kv_heads);
   const int64_t splits = (max_kv_len + split_tokens - 1) / split_tokens;
-  *floats = units * splits * kRows * (kD + 2);
-  *counters = units;
+  *floats = units * splits * kPart;
   return SPECDEC_OK;
 }
 
@@ -525,8 +533,7 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
                                         const int32_t *meta, int32_t batch, int32_t width,
                                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                         int32_t block_size, float scale, int32_t max_kv_len,
-                                        float *workspace, int64_t workspace_floats,
-                                        int32_t *counters, int64_t n_counters, void *out,
+                                        float *workspace, int64_t workspace_floats, void *out,
                                         int64_t out_token_stride, void *stream) {
   if (batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads ||
       block_size <= 0 || max_kv_len < 0)
@@ -552,14 +559,12 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;
-  a.counters = counters;
   a.out = out;
   a.out_stride = out_token_stride;
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
   if (a.max_splits > 1) {
-    if (!workspace || !counters) return SPECDEC_EINVAL;
-    if (workspace_floats < units * a.max_splits * kRows * (kD + 2) || n_counters < units)
-      return SPECDEC_EINVAL;
+    if (!workspace) return SPECDEC_EINVAL;
+    if (workspace_floats < units * a.max_splits * kPart) return SPECDEC_EINVAL;
   }
   if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
   dim3 grid((unsigned)units, (unsigned)a.max_splits), block(kAttnThreads);
@@ -575,5 +580,7 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
   } else {
     return SPECDEC_EINVAL;
   }
+  if (a.max_splits > 1)
+    attention_combine_kernel<<<dim3((unsigned)units), block, 0, s>>>(a, dtype);
   return launch_status();
 }

@@ -212,20 +212,27 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
 
 # --------------------------------------------------------------- attention --
 class AttentionWorkspace:
-    """Grow-only split-KV partials and arrival counters for one device.
-    Calls that share a workspace must be ordered on one stream."""
+    """Grow-only buffer of split-KV partials for one device.  Calls that
+    share a workspace must be ordered on one stream."""
 
     def __init__(self, device: torch.device) -> None:
         self.device = device
         self.floats = torch.empty(0, dtype=torch.float32, device=device)
-        self.counters = torch.zeros(0, dtype=torch.int32, device=device)
 
-    def reserve(self, floats: int, counters: int) -> None:
+    def reserve(self, floats: int) -> None:
         if floats > self.floats.numel():
             self.floats = torch.empty(max(floats, 2 * self.floats.numel()), dtype=torch.float32, device=self.device)
-        if counters > self.counters.numel():
-            self.counters = torch.zeros(max(counters, 2 * self.counters.numel()), dtype=torch.int32,
-                                        device=self.device)
+
+
+def attention_workspace_floats(batch: int, width: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                               max_kv_len: int) -> int:
+    import ctypes
+
+    floats = ctypes.c_int64()
+    st = lib().specdec_attention_workspace(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, 0,
+                                           ctypes.byref(floats))
+    _check(st, "attention_workspace")
+    return floats.value
 
 
 _workspaces: dict[torch.device, AttentionWorkspace] = {}
@@ -244,18 +251,12 @@ def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_k
 
 def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
                     block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None):
-    import ctypes
-
     ws = workspace or workspace_for(q.device)
-    floats, counters = ctypes.c_int64(), ctypes.c_int64()
-    st = lib().specdec_attention_workspace(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, 0,
-                                           ctypes.byref(floats), ctypes.byref(counters))
-    _check(st, "attention_workspace")
-    ws.reserve(floats.value, counters.value)
+    ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len))
     st = lib().specdec_paged_attention(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
                                        v_pool.data_ptr(), tables.data_ptr(), tables.stride(0), meta.data_ptr(), batch,
                                        width, n_heads, n_kv_heads, head_dim, block_size, float(scale), max_kv_len,
-                                       ws.floats.data_ptr(), ws.floats.numel(), ws.counters.data_ptr(),
-                                       ws.counters.numel(), out.data_ptr(), out_token_stride, stream())
+                                       ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(), out_token_stride,
+                                       stream())
     _check(st, "paged_attention")
     return out
