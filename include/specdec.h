@@ -49,7 +49,7 @@ extern "C" {
 #define SPECDEC_F64 1
 #define SPECDEC_BF16 2
 
-/* ABI version; bumped whenever a signature below changes. */
+/* ABI version; bumped whenever a signature below changes (currently 3). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -190,7 +190,7 @@ int specdec_kv_gather(const void *k_pool, const void *v_pool, int dtype,
 
 /* ------------------------------------------------------------ layer glue --- */
 
-/* Residual add + RMSNorm over rows of `dim` (BF16 or F32).  If delta is not
+/* Residual add + RMSNorm over rows of `dim` <= 8192 (BF16 or F32).  If delta is not
  * null, hidden <- hidden + delta (rounded to the element type) first; then
  * out <- weight * round(hidden * rsqrt(mean(hidden^2) + eps)).  The norm and
  * the add follow transformers' LlamaRMSNorm and the residual adds of the
@@ -212,10 +212,10 @@ int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
                                 int32_t max_kv_len, int32_t split_tokens,
                                 int64_t *floats);
 
-/* Split-KV size the attention kernel uses for a call shape (tokens per
- * workgroup; a fixed 256 whenever all queries of a kv head fit one 16-row
- * tile, so that a query's reduction order does not depend on how many
- * tokens are verified with it). */
+/* Split-KV size the attention kernel uses by default for a call shape
+ * (tokens per workgroup; a fixed 256 whenever all queries of a kv head fit
+ * one 16-row tile and the context is at most 32768, so that a query's
+ * reduction order does not depend on how many tokens are verified with it). */
 int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
                             int32_t n_kv_heads, int32_t max_kv_len);
 
@@ -224,7 +224,11 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * place).  q token (b, t), head h at q + (b*width + t)*q_token_stride +
  * h*head_dim; out likewise with out_token_stride.  Softmax in fp32 with
  * `scale`; QK^T and PV on MFMA (bf16) or fp32 MFMA (F32).  Query rows with
- * t >= n_new[b] are not written.  head_dim must be 64.  When a row needs
+ * t >= n_new[b] are not written.  head_dim must be 64.  split_tokens = 0
+ * selects the fixed split of specdec_attention_split (a query's bits then
+ * do not depend on the other queries of the call); a positive value is
+ * rounded up to a multiple of 256 (e.g. one split for a short draft
+ * context, saving the combine launch).  When a row needs
  * more than one split, a second kernel combining the split partials is
  * launched on the same stream; calls sharing a workspace must be ordered.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
@@ -235,7 +239,8 @@ int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
                             const int32_t *meta, int32_t batch, int32_t width,
                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                             int32_t block_size, float scale, int32_t max_kv_len,
-                            float *workspace, int64_t workspace_floats, void *out,
+                            int32_t split_tokens, float *workspace,
+                            int64_t workspace_floats, void *out,
                             int64_t out_token_stride, void *stream);
 
 #ifdef __cplusplus

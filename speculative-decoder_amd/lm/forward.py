@@ -31,12 +31,14 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 
 
 def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Tensor, max_kv_len: int,
-                 last: torch.Tensor | None = None,
-                 workspace: ops.AttentionWorkspace | None = None) -> torch.Tensor:
+                 last: torch.Tensor | None = None, workspace: ops.AttentionWorkspace | None = None,
+                 split_tokens: int = 0) -> torch.Tensor:
     """Device-only forward of ids [B, T] whose rows were appended with `meta`
     (int32 [3, B] on the device).  `max_kv_len` bounds every row's cached
     length after the append; `last` (int64 [B]) selects one row per batch
-    entry before the output projection."""
+    entry before the output projection.  `split_tokens` is the attention
+    split (0: the fixed default whose results do not depend on the other
+    queries of the call)."""
     cfg = llama.config
     b, t = ids.shape
     h, hk, d, inter, eps = (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size,
@@ -53,7 +55,8 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
         ops.rope_append(qkv, h, hk, d, llama.rope_cos, llama.rope_sin, meta, b, t, tables, cache.block_size,
                         cache.k[i], cache.v[i])
         ops.paged_attention(qkv, qkv.stride(1), cache.k[i], cache.v[i], tables, meta, b, t, h, hk, d,
-                            cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace)
+                            cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
+                            split_tokens)
         ops.add_rmsnorm(hidden, F.linear(attn, layer.wo), layer.ln2, x, eps)
         ops.silu_mul(F.linear(x, layer.wgu), act)
         nxt = layers[i + 1].ln1 if i + 1 < len(layers) else llama.norm
@@ -65,14 +68,15 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
 
 @torch.no_grad()
 def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, n_new: list[int],
-            last_only: bool = False) -> torch.Tensor:
+            last_only: bool = False, latency_split: bool = False) -> torch.Tensor:
     """Run `input_ids` [B, T] (right-padded; row b has n_new[b] real tokens)
     through the model, appending to each sequence's cache.  Returns logits
     [B, T, V]; rows past n_new[b] are padding.  With `last_only`, only each
     row's last real token is projected and the result is [B, V].
 
     The same call serves prefill (T = prompt length), decode (T = 1) and
-    speculative verification (T = k + 1)."""
+    speculative verification (T = k + 1).  `latency_split` lets attention
+    pick a split for latency (the draft) instead of the fixed default."""
     llama = as_llama(model, cache.device)
     step = cache.append(seq_ids, n_new)
     ids = input_ids.to(cache.device, non_blocking=True)
@@ -81,7 +85,10 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
     if last_only:
         last = torch.tensor([n - 1 for n in n_new], dtype=torch.int64).pin_memory().to(cache.device,
                                                                                           non_blocking=True)
-    return forward_core(llama, cache, step.meta, ids, step.max_total, last)
+    cfg = llama.config
+    split = (ops.latency_split(ids.shape[0], ids.shape[1], cfg.num_attention_heads, cfg.num_key_value_heads,
+                               step.max_total) if latency_split else 0)
+    return forward_core(llama, cache, step.meta, ids, step.max_total, last, split_tokens=split)
 
 
 def logits(model, hidden: torch.Tensor) -> torch.Tensor:

@@ -66,7 +66,8 @@ def _capture(run):
 
 
 class _Captured:
-    def __init__(self, llama: Llama, cache: KVCache, batch: int, bucket: int, width: int) -> None:
+    def __init__(self, llama: Llama, cache: KVCache, batch: int, bucket: int, width: int,
+                 latency: bool = False) -> None:
         # the cache owns its runners (cache.graphs); a weak reference back keeps
         # that from being a cycle, so dropping a cache frees its graphs at once
         self._cache = weakref.ref(cache)
@@ -74,8 +75,10 @@ class _Captured:
         dev = cache.device
         self.ws = ops.AttentionWorkspace(dev)
         cfg = llama.config
+        self.split = (ops.latency_split(batch, width, cfg.num_attention_heads, cfg.num_key_value_heads, bucket)
+                      if latency else 0)
         self.ws.reserve(ops.attention_workspace_floats(batch, width, cfg.num_attention_heads, cfg.num_key_value_heads,
-                                                       cfg.head_dim, bucket))
+                                                       cfg.head_dim, bucket, self.split))
         self.graph = None
         self.outs = None
         self._ptrs = None
@@ -129,7 +132,7 @@ class DraftStepGraph(_Captured):
     last real token, probabilities, and an inverse-CDF sample with u[B]."""
 
     def __init__(self, llama, cache, batch, width, temperature, bucket):
-        super().__init__(llama, cache, batch, bucket, width)
+        super().__init__(llama, cache, batch, bucket, width, latency=True)
         dev = cache.device
         self.temperature = temperature
         self.ids = torch.zeros(batch, width, dtype=torch.int64, device=dev)
@@ -144,7 +147,7 @@ class DraftStepGraph(_Captured):
 
         def work():
             last = self.meta[2].long() - 1
-            lg = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws)
+            lg = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split)
             q = ops.probabilities(lg, self.temperature)
             return q, ops.sample_inverse_cdf(q, self.u)
 
@@ -156,7 +159,7 @@ class DraftChainGraph(_Captured):
     the next step on the device.  Outputs q [B, steps, V] and tokens [B, steps]."""
 
     def __init__(self, llama, cache, batch, steps, temperature, bucket):
-        super().__init__(llama, cache, batch, bucket, 1)
+        super().__init__(llama, cache, batch, bucket, 1, latency=True)
         dev = cache.device
         self.temperature, self.steps = temperature, steps
         v = llama.config.vocab_size
@@ -176,7 +179,8 @@ class DraftChainGraph(_Captured):
         def work():
             self.ids.copy_(self.first)
             for i in range(self.steps):
-                lg = forward_core(self.llama, self.cache, self.metas[i], self.ids, self.bucket, None, self.ws)
+                lg = forward_core(self.llama, self.cache, self.metas[i], self.ids, self.bucket, None, self.ws,
+                                  self.split)
                 q = ops.probabilities(lg.view(self.batch, -1), self.temperature)
                 tok = ops.sample_inverse_cdf(q, self.u[i])
                 self.q[:, i].copy_(q)

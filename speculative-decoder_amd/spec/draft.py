@@ -63,7 +63,7 @@ class ModelDraft:
             return self._propose_graphs(seq_ids, pending, k, temperature, generator)
         tokens, qs = [], []
         for _ in range(k):
-            q = probabilities(run(self.model, self.cache, seq_ids, pending), temperature)
+            q = probabilities(run(self.model, self.cache, seq_ids, pending, latency_split=True), temperature)
             token = sample(q, generator)
             tokens.append(token)
             qs.append(q)
@@ -127,13 +127,15 @@ class UniformDraft:
         pass
 
 
-def run(model, cache: KVCache, seq_ids: list[int], chunks: list[list[int]] | torch.Tensor) -> torch.Tensor:
+def run(model, cache: KVCache, seq_ids: list[int], chunks: list[list[int]] | torch.Tensor,
+        latency_split: bool = False) -> torch.Tensor:
     """Forward right-padded chunks; returns the logits after each row's last
     real token, [B, V].  `chunks` may also be a [B, w] id tensor already on
     the device (every row w tokens long)."""
     if isinstance(chunks, torch.Tensor):
-        return forward(model, cache, seq_ids, chunks, [chunks.shape[1]] * chunks.shape[0], last_only=True)
+        return forward(model, cache, seq_ids, chunks, [chunks.shape[1]] * chunks.shape[0], last_only=True,
+                       latency_split=latency_split)
     n_new = [len(c) for c in chunks]
     width = max(n_new)
     input_ids = torch.tensor([c + [0] * (width - len(c)) for c in chunks], dtype=torch.int64)
-    return forward(model, cache, seq_ids, input_ids, n_new, last_only=True)
+    return forward(model, cache, seq_ids, input_ids, n_new, last_only=True, latency_split=latency_split)

@@ -267,8 +267,11 @@ __device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l
 // 4g+i of half hf is then token cs + 8g + 4hf + i, so lane group g holds the
 // scores of the 8 consecutive tokens cs+8g .. cs+8g+7 and reads their V^T
 // as one 16-byte run per dim.
+// Four waves per SIMD (<= 128 VGPRs): enough resident waves to keep HBM
+// busy at batch 8 and beyond.
 template <int MODE>
-__global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
+    AttnArgs a) {
   TileInfo ti;
   if (!tile_info(a, ti)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -304,14 +307,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_bf16_kernel(AttnArgs a
   const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
   const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
   const int kv_len = ti.kv_len;
-  const int wave_tokens = a.split / 4;
-  const int w_lo = blockIdx.y * a.split + wave * wave_tokens;
-  const int w_hi = min(w_lo + wave_tokens, kv_len);
+  // wave w takes the 64-token steps w, w+4, w+8, ... of this split
+  const int s_lo = blockIdx.y * a.split;
+  const int s_hi = min(s_lo + a.split, kv_len);
 
   // element offset of the (block, head) tile holding token pos
   auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
 
-  for (int c0 = w_lo; c0 < w_hi; c0 += 64) {
+  for (int c0 = s_lo + 64 * wave; c0 < s_hi; c0 += 256) {
     u32x4 kraw[2][2][2];  // [chunk][half][kk]
     u32x4 vraw[2][4];     // [chunk][dim tile]
 #pragma unroll
@@ -421,11 +424,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a)
   float m = -INFINITY, l = 0.0f;
 
   const int Hkv = a.Hkv, bs = a.bs;
-  const int wave_tokens = a.split / 4;
-  const int w_lo = blockIdx.y * a.split + wave * wave_tokens;
-  const int w_hi = min(w_lo + wave_tokens, ti.kv_len);
+  const int s_lo = blockIdx.y * a.split;
+  const int s_hi = min(s_lo + a.split, ti.kv_len);
 
-  for (int c0 = w_lo; c0 < w_hi; c0 += 32) {
+  // wave w takes the 32-token chunks 2w, 2w+1, 2w+8, 2w+9, ... of this split
+  for (int step = s_lo + 64 * wave; step < s_hi; step += 256)
+  for (int c0 = step; c0 < min(step + 64, s_hi); c0 += 32) {
     float sv[8];
     float vv[2][4][4];  // [group][tile][token i]
 #pragma unroll
@@ -500,6 +504,14 @@ inline int choose_split(int batch, int width, int H, int Hkv, int max_kv_len) {
   return split < min_split ? min_split : split;
 }
 
+// A caller-chosen split, rounded up to whole 256-token steps of the four
+// waves and raised if it would need more than kMaxSplits splits.
+inline int round_split(int split, int max_kv_len) {
+  split = ((split + 255) / 256) * 256;
+  const int min_split = ((max_kv_len + kMaxSplits - 1) / kMaxSplits + 255) / 256 * 256;
+  return split < min_split ? min_split : split;
+}
+
 }  // namespace specdec
 
 using namespace specdec;
@@ -518,9 +530,9 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
       n_heads % n_kv_heads || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
-  if (split_tokens <= 0)
-    split_tokens = choose_split(batch > 0 ? batch : 1, width > 0 ? width : 1, n_heads, n_kv_heads,
-                                max_kv_len);
+  split_tokens = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
+                                  : choose_split(batch > 0 ? batch : 1, width > 0 ? width : 1, n_heads,
+                                                 n_kv_heads, max_kv_len);
   const int64_t units = (int64_t)batch * n_kv_heads * qtiles(width, n_heads, n_kv_heads);
   const int64_t splits = (max_kv_len + split_tokens - 1) / split_tokens;
   *floats = units * splits * kPart;
@@ -533,7 +545,8 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
                                         const int32_t *meta, int32_t batch, int32_t width,
                                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                         int32_t block_size, float scale, int32_t max_kv_len,
-                                        float *workspace, int64_t workspace_floats, void *out,
+                                        int32_t split_tokens, float *workspace,
+                                        int64_t workspace_floats, void *out,
                                         int64_t out_token_stride, void *stream) {
   if (batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads ||
       block_size <= 0 || max_kv_len < 0)
@@ -555,7 +568,8 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
   a.Hkv = n_kv_heads;
   a.bs = block_size;
   a.scale = scale;
-  a.split = choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
+  a.split = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
+                             : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;

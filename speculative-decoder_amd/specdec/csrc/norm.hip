@@ -14,8 +14,12 @@ namespace specdec {
 
 constexpr int kNormThreads = 256;
 
-// One workgroup per row.  If delta is non-null: hidden <- hidden + delta
-// (rounded to T) first.  Then out <- weight * T(hidden * rsqrt(mean + eps)).
+// One workgroup per row, the row held in registers (kNormPer values per
+// thread, dim <= kNormThreads * kNormPer).  If delta is non-null:
+// hidden <- hidden + delta (rounded to T) first.  Then
+// out <- weight * T(hidden * rsqrt(mean + eps)).
+constexpr int kNormPer = 32;
+
 template <typename T>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(T *__restrict__ hidden, const T *__restrict__ delta,
                                                                    const T *__restrict__ weight, T *__restrict__ out,
@@ -25,21 +29,32 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(T *__restrict
   T *h = hidden + row * dim;
   const T *dl = delta ? delta + row * dim : nullptr;
   T *y = out + row * dim;
+  const int tid = threadIdx.x;
+  float v[kNormPer], w[kNormPer];
   float ss = 0.0f;
-  for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
-    float v = to_f32(h[i]);
-    if (dl) {
-      const T s = from_f32<T>(v + to_f32(dl[i]));
-      h[i] = s;
-      v = to_f32(s);
+#pragma unroll
+  for (int k = 0; k < kNormPer; ++k) {
+    const int64_t i = tid + (int64_t)k * kNormThreads;
+    v[k] = 0.0f;
+    w[k] = 0.0f;
+    if (i < dim) {
+      float x = to_f32(h[i]);
+      if (dl) {
+        const T s = from_f32<T>(x + to_f32(dl[i]));
+        h[i] = s;
+        x = to_f32(s);
+      }
+      v[k] = x;
+      w[k] = to_f32(weight[i]);
     }
-    ss += v * v;
+    ss += v[k] * v[k];
   }
   ss = block_sum(ss, red);
   const float inv = rsqrtf(ss / (float)dim + eps);
-  for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
-    const T n = from_f32<T>(to_f32(h[i]) * inv);
-    y[i] = from_f32<T>(to_f32(weight[i]) * to_f32(n));
+#pragma unroll
+  for (int k = 0; k < kNormPer; ++k) {
+    const int64_t i = tid + (int64_t)k * kNormThreads;
+    if (i < dim) y[i] = from_f32<T>(w[k] * to_f32(from_f32<T>(v[k] * inv)));
   }
 }
 
@@ -61,6 +76,7 @@ using namespace specdec;
 SPECDEC_API int specdec_add_rmsnorm(void *hidden, const void *delta, const void *weight, void *out, int dtype,
                                     int64_t rows, int64_t dim, float eps, void *stream) {
   if (rows < 0 || dim <= 0) return SPECDEC_EINVAL;
+  if (dim > (int64_t)kNormThreads * kNormPer) return SPECDEC_EUNSUPPORTED;
   if (rows == 0) return SPECDEC_OK;
   if (!hidden || !weight || !out) return SPECDEC_EINVAL;
   dim3 grid((unsigned)rows), block(kNormThreads);

@@ -225,11 +225,11 @@ class AttentionWorkspace:
 
 
 def attention_workspace_floats(batch: int, width: int, n_heads: int, n_kv_heads: int, head_dim: int,
-                               max_kv_len: int) -> int:
+                               max_kv_len: int, split_tokens: int = 0) -> int:
     import ctypes
 
     floats = ctypes.c_int64()
-    st = lib().specdec_attention_workspace(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, 0,
+    st = lib().specdec_attention_workspace(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens,
                                            ctypes.byref(floats))
     _check(st, "attention_workspace")
     return floats.value
@@ -249,14 +249,25 @@ def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_k
     return lib().specdec_attention_split(batch, width, n_heads, n_kv_heads, max_kv_len)
 
 
+def latency_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_kv_len: int) -> int:
+    """A split for calls whose bits need not match any other call (the draft
+    model): with few (row, head) units, one split of up to 2048 tokens, so
+    no combine kernel runs; otherwise the default."""
+    units = batch * n_kv_heads * -(-(width * (n_heads // n_kv_heads)) // 16)
+    if units >= 64:
+        return 0
+    return min(max(256, -(-max_kv_len // 256) * 256), 2048)
+
+
 def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
-                    block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None):
+                    block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None,
+                    split_tokens: int = 0):
     ws = workspace or workspace_for(q.device)
-    ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len))
+    ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
     st = lib().specdec_paged_attention(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
                                        v_pool.data_ptr(), tables.data_ptr(), tables.stride(0), meta.data_ptr(), batch,
                                        width, n_heads, n_kv_heads, head_dim, block_size, float(scale), max_kv_len,
-                                       ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(), out_token_stride,
-                                       stream())
+                                       split_tokens, ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(),
+                                       out_token_stride, stream())
     _check(st, "paged_attention")
     return out

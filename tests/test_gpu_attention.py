@@ -153,3 +153,32 @@ def test_repeated_split_combines_stay_exact():
         want = of.attention(q.view(1, 5, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
                             torch.tensor([L]), torch.tensor([L + 5]), 0.125)
         assert (out.view(1, 5, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("split", [256, 512, 2048])
+@pytest.mark.parametrize("heads", [(32, 32), (9, 3)])
+def test_explicit_split_sizes(split, heads):
+    """Caller-chosen splits (the draft's single-split policy) against SDPA."""
+    h, hkv = heads
+    d, bs = 64, 16
+    g = torch.Generator().manual_seed(split + h)
+    cache = make_cache(1, hkv, d, 400, bs, torch.bfloat16, 9)
+    ids = [0, 1]
+    for s in ids:
+        cache.add(s)
+    lengths = [1500, 333]
+    step = cache.append(ids, lengths)
+    cache.write(0, step, torch.randn(2, hkv, 1500, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(2, hkv, 1500, d, generator=g).to(torch.bfloat16).cuda())
+    step = cache.append(ids, [1, 1])
+    cache.write(0, step, torch.randn(2, hkv, 1, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(2, hkv, 1, d, generator=g).to(torch.bfloat16).cuda())
+    q = torch.randn(2, 1, h * d, generator=g).to(torch.bfloat16)
+    qd = q.cuda()
+    out = torch.zeros(2, 1, h * d, dtype=torch.bfloat16, device="cuda")
+    ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, 1, h, hkv, d, bs,
+                        0.125, step.max_total, out, out.stride(1), ops.AttentionWorkspace(qd.device), split)
+    k_all, v_all = cache.gather(0, step)
+    want = of.attention(q.view(2, 1, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
+                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
+    assert (out.view(2, 1, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
