@@ -57,6 +57,11 @@ def build_models(dtype=torch.bfloat16, seed=0):
             t_state, d_state)
 
 
+def mean_accept_len(stats):
+    """Accepted draft tokens per (sequence, round)."""
+    return stats.accepted / max(len(stats.emitted_per_round), 1)
+
+
 def prompt_ids(seed=0):
     g = torch.Generator().manual_seed(seed)
     return torch.randint(0, V, (PROMPT,), generator=g).tolist()
@@ -99,7 +104,7 @@ def bench_e2e(steps, warmup):
     dt = time.perf_counter() - t0
     emitted = sum(len(o) for o in outs)
     result = {"tokens_per_s": emitted / dt, "ms_per_step": 1000 * dt / steps, "emitted_per_step": len(outs[0]),
-              "rounds": stats.rounds, "mean_accept_len": stats.accepted / max(stats.rounds, 1),
+              "rounds": stats.rounds, "mean_accept_len": mean_accept_len(stats),
               "acceptance": stats.accepted / max(stats.drafted, 1)}
     # identity check of this output against plain greedy decoding of the target
     from baselines.cached_autoregressive import generate as plain
@@ -114,6 +119,94 @@ def bench_e2e(steps, warmup):
     result["identical_to_plain_greedy"] = want == outs[0]
     result["first_divergence"] = next((i for i, (a, b) in enumerate(zip(want, outs[0])) if a != b), None)
     return result, (target, draft, t_state, d_state, prompt, outs[0])
+
+
+def bench_variant_b(target, t_state, prompt, steps=1, n_layers=4, noise=0.002):
+    """Config 4, second variant: the draft is the target's first `n_layers`
+    layers (embeddings, final norm and head shared) plus N(0, noise^2) on
+    every matrix of those layers."""
+    from cache.kv import KVCache
+    from lm.model import SMOLLM2_1_7B, Llama, perturbed_truncation
+    from spec.draft import ModelDraft
+    from spec.loop import generate
+
+    state, shape = perturbed_truncation(t_state, SMOLLM2_1_7B, n_layers, noise, seed=7)
+    draft = Llama.from_state_dict(shape, state)
+    blocks = (PROMPT + NEW_TOKENS + 2 * K + 2 * BLOCK) // BLOCK + 4
+    tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda")
+    dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda")
+    generate(target, tc, ModelDraft(draft, dc), [prompt], NEW_TOKENS, k=K, generator=torch.Generator().manual_seed(0))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out, stats = generate(target, tc, ModelDraft(draft, dc), [prompt], NEW_TOKENS, k=K,
+                              generator=torch.Generator().manual_seed(0))
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"draft": f"target layers 0..{n_layers - 1} + N(0, {noise}^2)", "tokens_per_s": len(out[0]) / dt,
+            "acceptance": stats.accepted / max(stats.drafted, 1),
+            "mean_accept_len": mean_accept_len(stats), "rounds": stats.rounds}
+
+
+def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 8, "model"), (32, 8, "ngram")),
+                  prompt_len=1024, new_tokens=32, temperature=0.8):
+    """Config 5, bounded: batched sampled speculative decoding on seeded
+    1024-token prompts with ~30% planted repetition, `new_tokens` per row.
+    Reports emitted tokens/s, mean accept length, and per round the accept
+    kernel time (HIP events around the call the loop makes) and the verify
+    attention kernel time at that batch and context (graph-replayed)."""
+    import spec.loop as loop_mod
+    from cache.kv import KVCache
+    from make_golden import planted_rows
+    from spec.draft import ModelDraft
+    from spec.loop import generate
+    from spec.ngram import NGramDraft
+
+    results = {}
+    for batch, k, kind in combos:
+        prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
+        blocks = batch * ((prompt_len + new_tokens + 2 * k + 2 * BLOCK) // BLOCK + 2) + 8
+        tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda", )
+        dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda") if kind == "model" else None
+        accept_us = []
+        real_accept = loop_mod.accept_reject
+
+        def timed_accept(*a, **kw):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record()
+            v = real_accept(*a, **kw)
+            en.record()
+            en.synchronize()
+            accept_us.append(st.elapsed_time(en) * 1000)
+            return v
+
+        def run():
+            drafter = ModelDraft(draft, dc) if kind == "model" else NGramDraft(V)
+            return generate(target, tc, drafter, prompts, new_tokens, k=k, temperature=temperature,
+                            generator=torch.Generator().manual_seed(5))
+
+        run()  # warm-up: captures the graphs of this shape
+        loop_mod.accept_reject = timed_accept
+        try:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            outs, stats = run()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        finally:
+            loop_mod.accept_reject = real_accept
+        attn = time_attention(batch, prompt_len + new_tokens // 2, iters=40, t_new=k + 1)
+        results[f"b{batch}_k{k}_{kind}"] = {
+            "tokens_per_s": sum(len(o) for o in outs) / dt, "mean_accept_len": mean_accept_len(stats),
+            "acceptance": stats.accepted / max(stats.drafted, 1),
+            "rounds": stats.rounds, "accept_call_us_per_round": sum(accept_us) / max(len(accept_us), 1),
+            "verify_attention_us_per_layer": attn["us"], "verify_attention_gbs": attn["gbs"],
+            "sample": f"{batch} rows, {prompt_len}-token prompts (~30% planted repetition), {new_tokens} new tokens, "
+                      f"T={temperature}, k={k}"}
+        log(f"batched {batch} {k} {kind}: {results[f'b{batch}_k{k}_{kind}']}")
+        del tc, dc
+        torch.cuda.empty_cache()
+    return results
 
 
 # ------------------------------------------------------------ attention -----
@@ -178,20 +271,20 @@ def graph_time_us(launch, per_graph=20, replays=10):
     return start.elapsed_time(end) * 1000 / (per_graph * replays)
 
 
-def time_attention(batch, length, iters=200):
+def time_attention(batch, length, iters=200, t_new=5):
     from specdec import ops
 
-    cache, step, q, out = setup_attention(batch, length)
+    cache, step, q, out = setup_attention(batch, length, t_new=t_new)
     h, hkv, d = 32, 32, 64
     ws = ops.AttentionWorkspace(q.device)
 
     def launch():
-        ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, 5, h,
+        ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, t_new, h,
                             hkv, d, BLOCK, 0.125, step.max_total, out, out.stride(1), ws)
 
     launch()
     us = graph_time_us(launch, per_graph=20, replays=max(iters // 20, 1))
-    nbytes = attention_bytes(batch, [length] * batch)
+    nbytes = attention_bytes(batch, [length] * batch, t_new=t_new)
     return {"batch": batch, "context": length, "us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
             "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
 
@@ -320,6 +413,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batched", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (sharding is described in "
@@ -356,7 +450,12 @@ def main():
     log(f"e2e {e2e}")
     attn = time_attention(1, 4096, iters=300)
     log(f"attention {attn}")
+    attn8 = time_attention(8, 4096, iters=100)
+    log(f"attention b8 {attn8}")
     kernels = {} if args.only == "e2e" else bench_kernels()
+    variant_b = bench_variant_b(target, t_state, prompt)
+    log(f"variant B {variant_b}")
+    batched = {} if args.no_batched else bench_batched(target, draft)
     cpu = None
     if not args.no_cpu:
         del target, draft
@@ -388,6 +487,9 @@ def main():
                      "us_per_launch": attn["us"], "bytes_per_launch": attn["bytes"]},
         "cpu_baseline": cpu,
         "e2e": e2e,
+        "e2e_variant_b": variant_b,
+        "attention_b8_ctx4096": attn8,
+        "batched_sampled": batched,
         "kernels": kernels,
     }
     if cpu:
