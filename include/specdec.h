@@ -49,7 +49,7 @@ extern "C" {
 #define SPECDEC_F64 1
 #define SPECDEC_BF16 2
 
-/* ABI version; bumped whenever a signature below changes (currently 3). */
+/* ABI version; bumped whenever a signature below changes (currently 4). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -242,6 +242,23 @@ int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
                             int32_t split_tokens, float *workspace,
                             int64_t workspace_floats, void *out,
                             int64_t out_token_stride, void *stream);
+
+/* specdec_paged_attention fused with specdec_rope_append: qkv [batch,
+ * width, (H + 2*Hkv) * head_dim] holds the projections before RoPE.  The q
+ * heads are rotated in registers, and each workgroup first writes the new
+ * tokens' rotated k and their v for its kv head and split into the paged
+ * pools (identical values where workgroups overlap), so one launch per layer
+ * replaces two.  Same rounding as the two separate kernels.
+ * Replaces lm/forward.py:53,60-63 + cache/kv.py:101-112. */
+int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
+                                 const float *cos_table, const float *sin_table,
+                                 void *k_pool, void *v_pool, const int32_t *tables,
+                                 int64_t table_stride, const int32_t *meta, int32_t batch,
+                                 int32_t width, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, int32_t block_size, float scale,
+                                 int32_t max_kv_len, int32_t split_tokens,
+                                 float *workspace, int64_t workspace_floats, void *out,
+                                 int64_t out_token_stride, void *stream);
 
 #ifdef __cplusplus
 }

@@ -3,11 +3,12 @@
 A forward is split in two:
   * host part: `cache.append` decides block growth (one block-plan launch)
     and uploads the per-row metadata (table row, past length, new tokens);
-  * device part, `forward_core`: nine launches per layer -- fused residual
-    add + RMSNorm, one fused QKV GEMM (torch/hipBLASLt), the fused RoPE +
-    paged append kernel, the paged verify-attention kernel reading K/V
-    blocks in place (no gather copy, no materialised mask), o_proj, add +
-    RMSNorm, the gate/up GEMM, SiLU*up, the down GEMM -- then the fp32
+  * device part, `forward_core`: eight launches per layer (nine when the
+    attention needs its split combine) -- fused residual add + RMSNorm, one
+    fused QKV GEMM (torch/hipBLASLt), the paged verify-attention kernel that
+    also applies RoPE and appends the new K/V to the paged pools and reads
+    K/V blocks in place (no gather copy, no materialised mask), o_proj, add
+    + RMSNorm, the gate/up GEMM, SiLU*up, the down GEMM -- then the fp32
     output projection (lm/forward.py:71-84).
 The device part reads everything it needs from device memory, so a fixed
 (batch, width) shape can be captured once in a HIP graph and replayed
@@ -52,11 +53,9 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
     for i, layer in enumerate(layers):
         qkv = F.linear(x, layer.wqkv)
-        ops.rope_append(qkv, h, hk, d, llama.rope_cos, llama.rope_sin, meta, b, t, tables, cache.block_size,
-                        cache.k[i], cache.v[i])
-        ops.paged_attention(qkv, qkv.stride(1), cache.k[i], cache.v[i], tables, meta, b, t, h, hk, d,
-                            cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
-                            split_tokens)
+        ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t, h,
+                                 hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
+                                 split_tokens)
         ops.add_rmsnorm(hidden, F.linear(attn, layer.wo), layer.ln2, x, eps)
         ops.silu_mul(F.linear(x, layer.wgu), act)
         nxt = layers[i + 1].ln1 if i + 1 < len(layers) else llama.norm

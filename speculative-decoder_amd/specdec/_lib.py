@@ -34,9 +34,11 @@ SIGNATURES: dict[str, list] = {
     "specdec_attention_split": [I32, I32, I32, I32, I32],
     "specdec_paged_attention": [P, c_int, I64, P, P, P, I64, P, I32, I32, I32, I32, I32, I32, c_float,
                                 I32, I32, P, I64, P, I64, P],
+    "specdec_rope_paged_attention": [P, c_int, I64, P, P, P, P, P, I64, P, I32, I32, I32, I32, I32, I32, c_float,
+                                     I32, I32, P, I64, P, I64, P],
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _lib: ctypes.CDLL | None = None
 
 

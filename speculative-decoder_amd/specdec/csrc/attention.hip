@@ -48,6 +48,11 @@ constexpr int kPart = kRows * (kD + 1);  // floats per split partial: O/l [16][6
 struct AttnArgs {
   const void *q;
   int64_t q_stride;
+  // fused RoPE + append (rope != 0): q points at qkv; q heads are rotated in
+  // registers and the new tokens' k (rotated) and v are written to k/v
+  int rope;
+  const float *cos_t;
+  const float *sin_t;
   const void *k;
   const void *v;
   const int32_t *tables;
@@ -91,7 +96,46 @@ __device__ __forceinline__ int64_t block_of(const AttnArgs &a, const TileInfo &t
   return a.tables[(int64_t)ti.row * a.table_stride + pos / a.bs];
 }
 
-template <typename T> __device__ __forceinline__ float elem_f32(const T *p) { return to_f32(*p); }
+// RoPE of one (x1, x2) pair exactly as the append kernel computes it: each
+// product and the sum rounded on their own (no fused multiply-add).
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &y1, float &y2) {
+  y1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+  y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+}
+
+// Fused append: this workgroup writes kv head h of every new token whose
+// position lies in [lo, hi) -- its own split -- rotated k and plain v, into
+// the paged pools, before it reads any key.  Workgroups whose ranges
+// overlap write identical values.
+template <typename T>
+__device__ void append_new_kv(const AttnArgs &a, const TileInfo &ti, int lo, int hi) {
+  const int nnew = a.meta[2 * a.batch + ti.b];
+  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + nnew);
+  if (p0 >= p1) return;
+  const int half = kD / 2;
+  const T *qkv = reinterpret_cast<const T *>(a.q);
+  T *kp = reinterpret_cast<T *>(const_cast<void *>(a.k));
+  T *vp = reinterpret_cast<T *>(const_cast<void *>(a.v));
+  const int n = (p1 - p0) * half;
+  for (int task = threadIdx.x; task < n; task += blockDim.x) {
+    const int pos = p0 + task / half, i = task % half;
+    const int t = pos - ti.past;
+    const T *x = qkv + ((int64_t)ti.b * a.width + t) * a.q_stride;
+    const T *kx = x + (int64_t)(a.H + ti.h) * kD;
+    const T *vx = x + (int64_t)(a.H + a.Hkv + ti.h) * kD;
+    float y1, y2;
+    rope_pair(to_f32(kx[i]), to_f32(kx[i + half]), a.cos_t[(int64_t)pos * half + i], a.sin_t[(int64_t)pos * half + i],
+              y1, y2);
+    const int64_t blk = a.tables[(int64_t)ti.row * a.table_stride + pos / a.bs];
+    const int off = pos % a.bs;
+    T *kd = kp + ((blk * a.Hkv + ti.h) * a.bs + off) * kD;
+    kd[i] = from_f32<T>(y1);
+    kd[i + half] = from_f32<T>(y2);
+    T *vd = vp + (blk * a.Hkv + ti.h) * (int64_t)kD * a.bs + off;
+    vd[(int64_t)i * a.bs] = vx[i];
+    vd[(int64_t)(i + half) * a.bs] = vx[i + half];
+  }
+}
 
 __device__ __forceinline__ void st_agent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -288,12 +332,34 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
   const u16 *qrow =
       reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
 
+  if (a.rope) {
+    append_new_kv<__hip_bfloat16>(a, ti, blockIdx.y * a.split, (blockIdx.y + 1) * a.split);
+    __threadfence_block();
+    __syncthreads();
+  }
+
+  // Q operand: lane (query c, group g) holds dims 8g..8g+7 (kk = 0) and
+  // 32+8g..32+8g+7 (kk = 1) -- the two halves of 8 RoPE pairs
   bf16x8 qop[2];
+  {
+    u32x4 raw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (row_ok) {
+      raw[0] = *reinterpret_cast<const u32x4 *>(qrow + 8 * g);
+      raw[1] = *reinterpret_cast<const u32x4 *>(qrow + 32 + 8 * g);
+    }
+    qop[0] = __builtin_bit_cast(bf16x8, raw[0]);
+    qop[1] = __builtin_bit_cast(bf16x8, raw[1]);
+    if (a.rope && row_ok) {
+      const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
+      const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (row_ok) raw = *reinterpret_cast<const u32x4 *>(qrow + 32 * kk + 8 * g);
-    qop[kk] = __builtin_bit_cast(bf16x8, raw);
+      for (int j = 0; j < 8; ++j) {
+        float y1, y2;
+        rope_pair((float)qop[0][j], (float)qop[1][j], cs[j], sn[j], y1, y2);
+        qop[0][j] = (__bf16)y1;
+        qop[1][j] = (__bf16)y2;
+      }
+    }
   }
 
   f32x4 o[4];
@@ -414,9 +480,27 @@ __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a)
   const float *vp = reinterpret_cast<const float *>(a.v);
   const float *qrow =
       reinterpret_cast<const float *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
+  if (a.rope) {
+    append_new_kv<float>(a, ti, blockIdx.y * a.split, (blockIdx.y + 1) * a.split);
+    __threadfence_block();
+    __syncthreads();
+  }
+  // lane group g holds dims 16g..16g+15; its RoPE partners are 32 dims away
   float qv[16];
 #pragma unroll
   for (int s = 0; s < 16; ++s) qv[s] = row_ok ? qrow[16 * g + s] : 0.0f;
+  if (a.rope && row_ok) {
+    const int lo = (16 * g) % 32;  // index into the cos/sin half-table
+    const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + lo;
+    const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + lo;
+    const float *partner = qrow + (16 * g + 32) % 64;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      float y1, y2;
+      if (g < 2) rope_pair(qv[s], partner[s], cs[s], sn[s], y1, y2), qv[s] = y1;
+      else rope_pair(partner[s], qv[s], cs[s], sn[s], y1, y2), qv[s] = y2;
+    }
+  }
 
   f32x4 o[4];
 #pragma unroll
@@ -539,42 +623,25 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
   return SPECDEC_OK;
 }
 
-SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
-                                        const void *k_pool, const void *v_pool,
-                                        const int32_t *tables, int64_t table_stride,
-                                        const int32_t *meta, int32_t batch, int32_t width,
-                                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
-                                        int32_t block_size, float scale, int32_t max_kv_len,
-                                        int32_t split_tokens, float *workspace,
-                                        int64_t workspace_floats, void *out,
-                                        int64_t out_token_stride, void *stream) {
+static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width, int32_t n_heads,
+                            int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_kv_len,
+                            int32_t split_tokens, float *workspace, int64_t workspace_floats, void *stream) {
   if (batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads ||
       block_size <= 0 || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
   if (batch == 0 || width == 0 || max_kv_len == 0) return SPECDEC_OK;
-  if (!q || !k_pool || !v_pool || !tables || !meta || !out) return SPECDEC_EINVAL;
-  AttnArgs a;
-  a.q = q;
-  a.q_stride = q_token_stride;
-  a.k = k_pool;
-  a.v = v_pool;
-  a.tables = tables;
-  a.table_stride = table_stride;
-  a.meta = meta;
+  if (!a.q || !a.k || !a.v || !a.tables || !a.meta || !a.out) return SPECDEC_EINVAL;
   a.batch = batch;
   a.width = width;
   a.H = n_heads;
   a.Hkv = n_kv_heads;
   a.bs = block_size;
-  a.scale = scale;
   a.split = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
                              : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;
-  a.out = out;
-  a.out_stride = out_token_stride;
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
   if (a.max_splits > 1) {
     if (!workspace) return SPECDEC_EINVAL;
@@ -597,4 +664,57 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
   if (a.max_splits > 1)
     attention_combine_kernel<<<dim3((unsigned)units), block, 0, s>>>(a, dtype);
   return launch_status();
+}
+
+SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
+                                        const void *k_pool, const void *v_pool,
+                                        const int32_t *tables, int64_t table_stride,
+                                        const int32_t *meta, int32_t batch, int32_t width,
+                                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                        int32_t block_size, float scale, int32_t max_kv_len,
+                                        int32_t split_tokens, float *workspace,
+                                        int64_t workspace_floats, void *out,
+                                        int64_t out_token_stride, void *stream) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_stride = q_token_stride;
+  a.rope = 0;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.meta = meta;
+  a.scale = scale;
+  a.out = out;
+  a.out_stride = out_token_stride;
+  return launch_attention(a, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size, max_kv_len,
+                          split_tokens, workspace, workspace_floats, stream);
+}
+
+SPECDEC_API int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
+                                             const float *cos_table, const float *sin_table,
+                                             void *k_pool, void *v_pool, const int32_t *tables,
+                                             int64_t table_stride, const int32_t *meta, int32_t batch,
+                                             int32_t width, int32_t n_heads, int32_t n_kv_heads,
+                                             int32_t head_dim, int32_t block_size, float scale,
+                                             int32_t max_kv_len, int32_t split_tokens,
+                                             float *workspace, int64_t workspace_floats, void *out,
+                                             int64_t out_token_stride, void *stream) {
+  if (!cos_table || !sin_table) return SPECDEC_EINVAL;
+  AttnArgs a{};
+  a.q = qkv;
+  a.q_stride = token_stride;
+  a.rope = 1;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.meta = meta;
+  a.scale = scale;
+  a.out = out;
+  a.out_stride = out_token_stride;
+  return launch_attention(a, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size, max_kv_len,
+                          split_tokens, workspace, workspace_floats, stream);
 }

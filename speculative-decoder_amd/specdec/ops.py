@@ -271,3 +271,20 @@ def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, widt
                                        out_token_stride, stream())
     _check(st, "paged_attention")
     return out
+
+
+def rope_paged_attention(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
+                         block_size, scale, max_kv_len, out, out_token_stride,
+                         workspace: AttentionWorkspace | None = None, split_tokens: int = 0):
+    """RoPE + paged append + verify attention in one launch (plus the split
+    combine when needed).  qkv [B, T, (H + 2 Hkv) d] holds unrotated q/k/v."""
+    ws = workspace or workspace_for(qkv.device)
+    ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
+    st = lib().specdec_rope_paged_attention(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), cos.data_ptr(),
+                                            sin.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), tables.data_ptr(),
+                                            tables.stride(0), meta.data_ptr(), batch, width, n_heads, n_kv_heads,
+                                            head_dim, block_size, float(scale), max_kv_len, split_tokens,
+                                            ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(), out_token_stride,
+                                            stream())
+    _check(st, "rope_paged_attention")
+    return out

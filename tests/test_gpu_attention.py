@@ -182,3 +182,42 @@ def test_explicit_split_sizes(split, heads):
     want = of.attention(q.view(2, 1, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
                         torch.tensor(step.past), torch.tensor(step.total), 0.125)
     assert (out.view(2, 1, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize(("bs", "t_new", "lengths"), [(16, 5, [1000, 37]), (4, 3, [50, 9]), (16, 200, [0, 300])])
+def test_fused_rope_append_equals_separate_kernels(dtype, bs, t_new, lengths):
+    """rope_paged_attention == rope_append followed by paged_attention: the
+    attention output and the pool contents at the new positions, bit for bit."""
+    from lm.model import LlamaShape, rope_tables
+
+    h, hkv, d = 8, 4, 64
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=10000.0)
+    cos, sin = (x.cuda() for x in rope_tables(shape, 2048))
+    g = torch.Generator().manual_seed(bs * 31 + t_new)
+    caches = [make_cache(1, hkv, d, 200, bs, dtype, 3) for _ in range(2)]
+    hist = [torch.randn(2, hkv, max(max(lengths), 1), d, generator=g).to(dtype).cuda() for _ in range(2)]
+    qkv = torch.randn(2, t_new, (h + 2 * hkv) * d, generator=g).to(dtype).cuda()
+    outs = []
+    for which, cache in enumerate(caches):
+        for s in (0, 1):
+            cache.add(s)
+        step = cache.append([0, 1], lengths)
+        if max(lengths) > 0:
+            cache.write(0, step, hist[0], hist[1])
+        step = cache.append([0, 1], [t_new, t_new])
+        out = torch.zeros(2, t_new, h * d, dtype=dtype, device="cuda")
+        x = qkv.clone()
+        if which == 0:
+            ops.rope_append(x, h, hkv, d, cos, sin, step.meta, 2, t_new, cache.table_tensor, bs, cache.k[0],
+                            cache.v[0])
+            ops.paged_attention(x, x.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, t_new, h,
+                                hkv, d, bs, 0.125, step.max_total, out, out.stride(1))
+        else:
+            ops.rope_paged_attention(x, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, t_new, h,
+                                     hkv, d, bs, 0.125, step.max_total, out, out.stride(1))
+        k_all, v_all = cache.gather(0, step)
+        outs.append((out, k_all, v_all))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
