@@ -414,6 +414,7 @@ def main():
     ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--batch", type=int, default=1, help="batch of the --only attention run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (sharding is described in "
@@ -426,8 +427,8 @@ def main():
     sys.path.insert(0, str(ROOT / "tests" / "golden"))
 
     if args.only == "attention":
-        r = time_attention(1, 4096, iters=max(args.steps, 1) * 100)
-        print(json.dumps({"attention_b1_L4096": r}))
+        r = time_attention(args.batch, 4096, iters=max(args.steps, 1) * 100)
+        print(json.dumps({f"attention_b{args.batch}_L4096": r}))
         return
     if args.only == "kernels":
         print(json.dumps(bench_kernels()))

@@ -75,21 +75,25 @@ __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
   }
 
   // logits.float() / T, then a max-shifted softmax: one pass keeps a running
-  // (max, sum) per thread, merged across the workgroup; a second pass writes
+  // (max, sum) per thread, merged across the workgroup; a second pass
+  // writes.  exp(v - m) is evaluated as 2^((v - m) * log2 e) on the
+  // hardware exp2 (about 1e-6 relative for the shifts that matter).
+  constexpr float kLog2e = 1.4426950408889634f;
   float m = -INFINITY, s = 0.0f;
   for (int64_t i = tid; i < vocab; i += blockDim.x) {
     const float v = to_f32(x[i]) / temperature;
     if (v > m) {
-      s = (m == -INFINITY) ? 0.0f : s * expf(m - v);
+      s = (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - v) * kLog2e);
       m = v;
     }
-    s += expf(v - m);
+    s += __builtin_amdgcn_exp2f((v - m) * kLog2e);
   }
   const float mg = block_max(m, red_f);
-  s = (m == -INFINITY) ? 0.0f : s * expf(m - mg);
+  s = (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - mg) * kLog2e);
   s = block_sum(s, red_f);
   const float inv = 1.0f / s;
-  for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = expf(to_f32(x[i]) / temperature - mg) * inv;
+  for (int64_t i = tid; i < vocab; i += blockDim.x)
+    y[i] = __builtin_amdgcn_exp2f((to_f32(x[i]) / temperature - mg) * kLog2e) * inv;
 }
 
 // ------------------------------------------- accept stage (per batch) ----
@@ -175,6 +179,187 @@ __device__ int64_t inverse_cdf_row(Elem elem, int64_t vocab, T u, double *scratc
   cdf_tile<T>(elem, vocab, tile, jt, jt == 0 ? 0.0 : carry[jt - 1], target, scratch, &s_end, &count);
   const int64_t idx = jt * tile + (int64_t)block_sum((double)count, scratch);
   return idx > vocab - 1 ? vocab - 1 : idx;
+}
+
+// fp32 rows of up to kRegTiles * 4096 elements: the whole row stays in
+// registers.  vals[j][e] is element j*4096 + 4*tid + e (coalesced loads).
+// The CDF needs each thread to own a contiguous run, so the row passes
+// through LDS a chunk (4 tiles, 16384 elements) at a time: thread t takes
+// elements 16t..16t+15 of the chunk, sums them sequentially in fp64, and
+// one workgroup exclusive scan per chunk gives every thread the prefix at
+// the start of its run.  The target is taken from the prefix of the last
+// element computed the same way, and the answer is the number of prefixes
+// (rounded to fp32) that do not exceed it.
+constexpr int kRegTiles = 12;  // rows up to 49152 elements
+constexpr int kChunkTiles = 4;
+constexpr int kChunk = kChunkTiles * kAcceptThreads * kCdfPerThread;  // 16384
+constexpr int kRun = kChunk / kAcceptThreads;                          // 16 per thread
+__device__ __forceinline__ int lds_pad(int k) { return k + (k >> 5); }
+
+__device__ __forceinline__ int64_t inverse_cdf_regs(const float (&vals)[kRegTiles][kCdfPerThread], int64_t vocab, float u,
+                                    double *scratch, float *lds) {
+  __shared__ double s_total;
+  const int tid = threadIdx.x;
+  const int tile = kAcceptThreads * kCdfPerThread;
+  const int nchunks = (int)((vocab + kChunk - 1) / kChunk);
+  float mine[kRegTiles / kChunkTiles][kRun];
+  double base[kRegTiles / kChunkTiles];
+  double carry = 0.0;
+#pragma unroll
+  for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
+    if (c >= nchunks) break;
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < kChunkTiles; ++jj)
+#pragma unroll
+      for (int e = 0; e < kCdfPerThread; ++e) lds[lds_pad(jj * tile + kCdfPerThread * tid + e)] = vals[c * kChunkTiles + jj][e];
+    __syncthreads();
+    double local = 0.0;
+#pragma unroll
+    for (int m = 0; m < kRun; ++m) {
+      mine[c][m] = lds[lds_pad(kRun * tid + m)];
+      local += (double)mine[c][m];
+    }
+    double total;
+    base[c] = carry + block_exclusive_scan(local, scratch, &total);
+    carry += total;
+  }
+  // the prefix of the row's last element (zeros pad the last chunk)
+  if (tid == kAcceptThreads - 1) {
+    double acc = base[0];
+#pragma unroll
+    for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
+      if (c != nchunks - 1) continue;
+      acc = base[c];
+#pragma unroll
+      for (int m = 0; m < kRun; ++m) acc += (double)mine[c][m];
+    }
+    s_total = acc;
+  }
+  __syncthreads();
+  const float target = u * (float)s_total;
+  int count = 0;
+#pragma unroll
+  for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
+    if (c >= nchunks) break;
+    double acc = base[c];
+#pragma unroll
+    for (int m = 0; m < kRun; ++m) {
+      acc += (double)mine[c][m];
+      const int64_t idx = (int64_t)c * kChunk + kRun * tid + m;
+      if (idx < vocab && (float)acc <= target) ++count;
+    }
+  }
+  __syncthreads();
+  const int64_t idx = (int64_t)block_sum((double)count, scratch);
+  return idx > vocab - 1 ? vocab - 1 : idx;
+}
+
+// Leading-accept count and zero-q flag of batch entry b computed by wave 0:
+// lane t tests draft position t (and t+64, ...); a ballot finds the first
+// rejection.  Same test as accept_stage.
+template <typename T>
+__device__ __forceinline__ void accept_stage_wave(const T *p, const T *q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
+                                                  int64_t q_rs, const int64_t *draft, const T *u_accept, int64_t b,
+                                                  int64_t k, int64_t vocab, int64_t *n_out, int64_t *bad_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t first = k;
+  bool bad = false;
+  for (int64_t t0 = 0; t0 < k; t0 += kWave) {
+    const int64_t t = t0 + lane;
+    bool rej = false, zero = false;
+    if (t < k) {
+      const int64_t x = draft[b * k + t];
+      if (x < 0 || x >= vocab) {
+        rej = zero = true;
+      } else {
+        const T px = p[b * p_bs + t * p_rs + x];
+        const T qx = q[b * q_bs + t * q_rs + x];
+        zero = !(qx > T(0));
+        rej = !(u_accept[b * k + t] * qx < px);  // u < p/q as a product
+      }
+    }
+    const unsigned long long mr = __ballot(rej), mz = __ballot(zero);
+    if (first == k && mr) first = t0 + __ffsll((long long)mr) - 1;
+    bad = bad || mz != 0;
+  }
+  *n_out = first;
+  *bad_out = bad ? 1 : 0;
+}
+
+// fp32 accept-reject with the residual row held in registers (vocab <= 49152).
+__global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
+    const float *__restrict__ p, const float *__restrict__ q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
+    int64_t q_rs, const int64_t *__restrict__ draft, const float *__restrict__ u_accept,
+    const float *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab, int64_t *__restrict__ out) {
+  __shared__ double scratch[kAcceptThreads / kWave + 1];
+  __shared__ float lds[kChunk + kChunk / 32];
+  __shared__ int64_t s_n;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid < kWave) {
+    int64_t n, bad;
+    accept_stage_wave(p, q, p_bs, p_rs, q_bs, q_rs, draft, u_accept, b, k, vocab, &n, &bad);
+    if (tid == 0) {
+      s_n = n;
+      out[b] = n;
+      out[2 * batch + b] = bad;
+    }
+  }
+  __syncthreads();
+  const int64_t n = s_n;
+  const float *pr = p + b * p_bs + n * p_rs;
+  const float *qr = (n < k) ? q + b * q_bs + n * q_rs : nullptr;  // zero row at n == k
+  const int tile = kAcceptThreads * kCdfPerThread;
+  float vals[kRegTiles][kCdfPerThread];
+  double local = 0.0;
+#pragma unroll
+  for (int j = 0; j < kRegTiles; ++j)
+#pragma unroll
+    for (int e = 0; e < kCdfPerThread; ++e) {
+      const int64_t i = (int64_t)j * tile + kCdfPerThread * tid + e;
+      float r = 0.0f;
+      if (i < vocab) {
+        r = qr ? pr[i] - qr[i] : pr[i];
+        r = r > 0.0f ? r : 0.0f;
+      }
+      vals[j][e] = r;
+      local += (double)r;
+    }
+  const float total = (float)block_sum(local, scratch);
+  const float denom = total > FLT_MIN ? total : FLT_MIN;
+  const bool use_residual = total > 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRegTiles; ++j)
+#pragma unroll
+    for (int e = 0; e < kCdfPerThread; ++e) {
+      const int64_t i = (int64_t)j * tile + kCdfPerThread * tid + e;
+      if (use_residual) vals[j][e] = vals[j][e] / denom;
+      else vals[j][e] = i < vocab ? pr[i] : 0.0f;  // p == q: fall back to p
+    }
+  const int64_t idx = inverse_cdf_regs(vals, vocab, u_residual[b], scratch, lds);
+  if (tid == 0) out[batch + b] = idx;
+}
+
+__global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_regs_kernel(const float *__restrict__ probs,
+                                                                                 int64_t vocab, int64_t row_stride,
+                                                                                 const float *__restrict__ u,
+                                                                                 int64_t *__restrict__ out) {
+  __shared__ double scratch[kAcceptThreads / kWave + 1];
+  __shared__ float lds[kChunk + kChunk / 32];
+  const int64_t b = blockIdx.x;
+  const float *row = probs + b * row_stride;
+  const int tile = kAcceptThreads * kCdfPerThread;
+  float vals[kRegTiles][kCdfPerThread];
+#pragma unroll
+  for (int j = 0; j < kRegTiles; ++j)
+#pragma unroll
+    for (int e = 0; e < kCdfPerThread; ++e) {
+      const int64_t i = (int64_t)j * tile + kCdfPerThread * threadIdx.x + e;
+      vals[j][e] = i < vocab ? row[i] : 0.0f;
+    }
+  const int64_t idx = inverse_cdf_regs(vals, vocab, u[b], scratch, lds);
+  if (threadIdx.x == 0) out[b] = idx;
 }
 
 template <typename T>
@@ -302,7 +487,11 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
   if (!p || !out || !u_residual || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
-  if (dtype == SPECDEC_F32) {
+  if (dtype == SPECDEC_F32 && vocab <= (int64_t)kRegTiles * kCdfPerThread * kAcceptThreads) {
+    accept_reject_regs_kernel<<<grid, block, 0, s>>>((const float *)p, (const float *)q, p_batch_stride, p_row_stride,
+                                                     q_batch_stride, q_row_stride, draft, (const float *)u_accept,
+                                                     (const float *)u_residual, batch, k, vocab, out);
+  } else if (dtype == SPECDEC_F32) {
     accept_reject_kernel<float><<<grid, block, 0, s>>>(
         (const float *)p, (const float *)q, p_batch_stride, p_row_stride, q_batch_stride,
         q_row_stride, draft, (const float *)u_accept, (const float *)u_residual, batch, k, vocab,
@@ -353,7 +542,10 @@ SPECDEC_API int specdec_sample_inverse_cdf(const void *probs, int dtype, int64_t
   if (!probs || !u || !out) return SPECDEC_EINVAL;
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
-  if (dtype == SPECDEC_F32) {
+  if (dtype == SPECDEC_F32 && vocab <= (int64_t)kRegTiles * kCdfPerThread * kAcceptThreads) {
+    sample_inverse_cdf_regs_kernel<<<grid, block, 0, s>>>((const float *)probs, vocab, row_stride, (const float *)u,
+                                                          out);
+  } else if (dtype == SPECDEC_F32) {
     sample_inverse_cdf_kernel<float><<<grid, block, 0, s>>>((const float *)probs, vocab,
                                                            row_stride, (const float *)u, out);
   } else if (dtype == SPECDEC_F64) {
