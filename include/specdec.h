@@ -49,7 +49,8 @@ extern "C" {
 #define SPECDEC_F64 1
 #define SPECDEC_BF16 2
 
-/* ABI version; bumped whenever a signature below changes (currently 4). */
+/* ABI version; bumped whenever a signature or the meaning of an argument
+ * below changes (currently 5). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -227,10 +228,13 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * t >= n_new[b] are not written.  head_dim must be 64.  split_tokens = 0
  * selects the fixed split of specdec_attention_split (a query's bits then
  * do not depend on the other queries of the call); a positive value is
- * rounded up to a multiple of 256 (e.g. one split for a short draft
- * context, saving the combine launch).  When a row needs
- * more than one split, a second kernel combining the split partials is
- * launched on the same stream; calls sharing a workspace must be ordered.
+ * rounded up to a multiple of 256; a negative value asks for one workgroup
+ * per (row, kv head, query tile) over every key, for latency when the bits
+ * need not match other calls (the draft; bf16 only, fp32 takes the default).
+ * When a row needs more than four splits, a second kernel combining the
+ * split partials is launched on the same stream (2 to 4 splits are folded
+ * inside one workgroup with the same arithmetic); calls sharing a workspace
+ * must be ordered.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
  * cache/kv.py:108-112. */
 int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,

@@ -30,7 +30,9 @@ from lm.forward import forward_core
 from lm.model import Llama
 from specdec import ops
 
-BUCKET = 2048
+# Context buckets of 1024 keys: up to four 256-token splits, which the
+# attention kernel folds inside one workgroup (no combine launch).
+BUCKET = 1024
 
 
 def enabled() -> bool:

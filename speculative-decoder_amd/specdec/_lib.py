@@ -38,7 +38,7 @@ SIGNATURES: dict[str, list] = {
                                      I32, I32, P, I64, P, I64, P],
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _lib: ctypes.CDLL | None = None
 
 

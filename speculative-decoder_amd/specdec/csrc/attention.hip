@@ -24,7 +24,9 @@
 //
 // Splits write (O / l, lse) partials to a workspace; a second small kernel
 // (attention_combine_kernel), launched right after on the same stream,
-// folds them per (batch, head, tile).
+// folds them per (batch, head, tile).  With 2 to 4 splits one 16-wave
+// workgroup per tile runs all of them and folds them in LDS with the same
+// arithmetic, so short contexts (decode, the draft) need one launch.
 // Every query's reduction order depends only on the absolute key positions,
 // never on how many queries share the call, so a token verified among k+1
 // gets the same bits as the same token decoded alone.
@@ -61,6 +63,9 @@ struct AttnArgs {
   int batch, width, H, Hkv, bs;
   float scale;
   int split, max_splits, n_qtiles;
+  // 16-wave launches only: one split over every key, wave w taking the
+  // 64-token steps w, w+16, ... (results need not match other calls)
+  int flat;
   float *ws;
   void *out;
   int64_t out_stride;
@@ -137,25 +142,42 @@ __device__ void append_new_kv(const AttnArgs &a, const TileInfo &ti, int lo, int
   }
 }
 
-__device__ __forceinline__ void st_agent(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Statistics are in the log2 domain: a wave's (m, l, o) mean
+// o / l = sum_j 2^(t_j - m) v_j / sum_j 2^(t_j - m), with t_j the score times
+// scale * log2(e).  Waves hand them over in LDS as s_m/s_l [wave][query] and
+// s_o [wave][query][dim].
+
+// Fold of waves w0 .. w0+N-1 for query row qq, dims d0 .. d0+3.
+template <int N = 4>
+__device__ __forceinline__ void fold_waves(const float (*s_m)[kRows], const float (*s_l)[kRows],
+                                           const float (*s_o)[kRows][kD + 4], int w0, int qq, int d0, float &M,
+                                           float &L, float (&O)[4]) {
+  M = s_m[w0][qq];
+  for (int w = 1; w < N; ++w) M = fmaxf(M, s_m[w0 + w][qq]);
+  L = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) O[i] = 0.0f;
+  for (int w = 0; w < N; ++w) {
+    const float mw = s_m[w0 + w][qq];
+    const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+    L = __builtin_fmaf(f, s_l[w0 + w][qq], L);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) O[i] = __builtin_fmaf(f, s_o[w0 + w][qq][d0 + i], O[i]);
+  }
 }
 
-// Combine the 4 waves of this workgroup, then the splits (last arriving
-// workgroup), and write the normalised output rows.  Statistics are in the
-// log2 domain: a wave's (m, l, o) mean o / l = sum_j 2^(t_j - m) v_j / sum_j 2^(t_j - m)
-// with t_j the score times scale * log2(e).
-//
-// Split partials cross workgroups (and XCDs) as (O / l, lse = m + log2 l)
-// through device-coherent stores and loads (agent-scope relaxed atomics:
-// write-through / L2-bypass), a wait for the stores to complete, and a
-// relaxed arrival counter -- no full L2 writeback per workgroup.  The last
-// workgroup reads every split in one pass: thread (q, 4 dims) loads the
-// split lse values and float4 rows in groups of 16 splits and folds them
-// with a running maximum, in split order.
+template <typename T>
+__device__ __forceinline__ void store_row4(const AttnArgs &a, const TileInfo &ti, int qq, int d0, const float (&v)[4]) {
+  const int r = ti.qt * kRows + qq;
+  const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
+  T *dst = reinterpret_cast<T *>(a.out) + ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(v[i]);
+}
+
+// Combine the 4 waves of this workgroup.  With one split the normalised rows
+// are the output; otherwise the split partial (O / l, lse = m + log2 l) goes
+// to the workspace for the combine kernel.
 template <typename T>
 __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
   __shared__ float s_m[4][kRows], s_l[4][kRows];
@@ -172,107 +194,169 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
     for (int i = 0; i < 4; ++i) s_o[wave][c][16 * t + 4 * g + i] = o[t][i];
   __syncthreads();
 
-  const int r0 = ti.qt * kRows;
-  const int nq = min(kRows, ti.nrows - r0);  // real query rows in this tile
-  const int qq = tid >> 4, d0 = (tid & 15) * 4;  // this thread: row qq, dims d0..d0+3
-  float M = s_m[0][qq];
-  for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qq]);
-  float L = 0.0f, O[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int w = 0; w < 4; ++w) {
-    const float mw = s_m[w][qq];
-    const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-    L += f * s_l[w][qq];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) O[i] += f * s_o[w][qq][d0 + i];
-  }
-
-  T *out = reinterpret_cast<T *>(a.out);
-  auto store4 = [&](const float (&val)[4]) {
-    const int r = r0 + qq;
-    const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
-    T *dst = out + ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(val[i]);
-  };
-
+  const int nq = min(kRows, ti.nrows - ti.qt * kRows);  // real query rows in this tile
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;         // this thread: row qq, dims d0..d0+3
+  float M, L, O[4];
+  fold_waves(s_m, s_l, s_o, 0, qq, d0, M, L, O);
+  if (qq >= nq) return;
   if (ti.nsplit == 1) {
-    if (qq < nq) {
-      float v[4];
+    float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
-      store4(v);
-    }
+    for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
+    store_row4<T>(a, ti, qq, d0, v);
     return;
   }
-
   // split partial for the combine kernel: O / l [16][64] and lse [16]
   float *ws = a.ws + ((int64_t)ti.unit * a.max_splits + blockIdx.y) * kPart;
-  if (qq < nq) {
-    const bool any = L > 0.0f;
-    f32x4 v;
+  const bool any = L > 0.0f;
+  f32x4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = any ? O[i] / L : 0.0f;
-    *reinterpret_cast<f32x4 *>(ws + qq * kD + d0) = v;
-    if (d0 == 0) ws[kRows * kD + qq] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
+  for (int i = 0; i < 4; ++i) v[i] = any ? O[i] / L : 0.0f;
+  *reinterpret_cast<f32x4 *>(ws + qq * kD + d0) = v;
+  if (d0 == 0) ws[kRows * kD + qq] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
+}
+
+// Folds the split partials s0 .. s0+G-1 that lie below ns into the running
+// (Mx, den, num): the group's largest lse rescales what is accumulated, then
+// each split adds w = 2^(lse - Mx) times its O / l row, in split order.
+// Both the combine kernel (G = 32) and the single-workgroup path below
+// (G = 4, at most 4 splits) use it; splits past ns take no part, so for a
+// query with at most 4 splits both run the same operations in the same
+// order and the result does not depend on which of them ran.
+template <int G>
+__device__ __forceinline__ void fold_splits(int s0, int ns, const float (&lse)[G], const f32x4 (&ov)[G], float &Mx,
+                                            float &den, float (&num)[4]) {
+  float Mg = Mx;
+#pragma unroll
+  for (int u = 0; u < G; ++u)
+    if (s0 + u < ns) Mg = fmaxf(Mg, lse[u]);
+  if (Mg > Mx) {  // rescale what is accumulated to the new maximum
+    const float r = (Mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(Mx - Mg);
+    den *= r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) num[i] *= r;
+    Mx = Mg;
+  }
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    if (s0 + u < ns && lse[u] != -INFINITY) {
+      const float w = __builtin_amdgcn_exp2f(lse[u] - Mx);
+      den += w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) num[i] = __builtin_fmaf(w, ov[u][i], num[i]);
+    }
   }
 }
 
 // Final combine of the split partials, one workgroup per (row, head, tile)
 // with more than one split: thread (q, 4 dims) folds every split in split
-// order; loads go out 32 splits at a time, each group rescaled once to its
-// maximum.
+// order, 32 splits per load group.  The first group's loads are issued
+// before the row metadata arrives (their addresses depend only on the
+// workgroup); splits the row does not have are never folded.
 __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArgs a, int dtype) {
+  const int tid = threadIdx.x;
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  const float *ws0 = a.ws + (int64_t)blockIdx.x * a.max_splits * kPart;
+  float lse[32];
+  f32x4 ov[32];
+#pragma unroll
+  for (int u = 0; u < 32; ++u) {
+    const float *p = ws0 + (int64_t)min(u, a.max_splits - 1) * kPart;
+    lse[u] = p[kRows * kD + qq];
+    ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
+  }
   TileInfo ti;
   if (!tile_info(a, ti, /*any_split=*/true) || ti.nsplit == 1) return;
-  const int tid = threadIdx.x;
-  const int r0 = ti.qt * kRows;
-  const int nq = min(kRows, ti.nrows - r0);
-  const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  const int nq = min(kRows, ti.nrows - ti.qt * kRows);
   if (qq >= nq) return;
-  const float *ws0 = a.ws + (int64_t)ti.unit * a.max_splits * kPart;
   const int ns = ti.nsplit;
   float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < ns; s0 += 32) {
-    // every load is issued before any is used: addresses past the last
-    // split are clamped to it and their weight forced to zero
-    float lse[32];
-    f32x4 ov[32];
+  fold_splits(0, ns, lse, ov, Mx, den, num);
+  for (int s0 = 32; s0 < ns; s0 += 32) {
 #pragma unroll
     for (int u = 0; u < 32; ++u) {
       const float *p = ws0 + (int64_t)min(s0 + u, ns - 1) * kPart;
       lse[u] = p[kRows * kD + qq];
       ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
     }
-    float Mg = Mx;
-#pragma unroll
-    for (int u = 0; u < 32; ++u)
-      if (s0 + u < ns) Mg = fmaxf(Mg, lse[u]);
-    if (Mg > Mx) {  // rescale what is accumulated to the new maximum
-      const float r = (Mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(Mx - Mg);
-      den *= r;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) num[i] *= r;
-      Mx = Mg;
-    }
-#pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      const float w = (s0 + u >= ns || lse[u] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(lse[u] - Mx);
-      den += w;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) num[i] += w * ov[u][i];
-    }
+    fold_splits(s0, ns, lse, ov, Mx, den, num);
   }
-  const int r = r0 + qq;
-  const int t = r / ti.group, hq = ti.h * ti.group + r % ti.group;
-  const int64_t off = ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
-  if (dtype == SPECDEC_BF16) {
-    __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) + off;
+  float v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = __float2bfloat16(num[i] / den);
-  } else {
-    float *dst = reinterpret_cast<float *>(a.out) + off;
+  for (int i = 0; i < 4; ++i) v[i] = num[i] / den;
+  if (dtype == SPECDEC_BF16) store_row4<__hip_bfloat16>(a, ti, qq, d0, v);
+  else store_row4<float>(a, ti, qq, d0, v);
+}
+
+// Single-workgroup variant of finish() for 2 to 4 splits (16 waves, wave w
+// in split w / 4): each group of four waves folds into its split partial
+// exactly as finish() would write it, the partials meet in LDS, and group 0
+// folds them with fold_splits -- the same bits the combine kernel produces,
+// without its launch.
+template <typename T>
+__device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
+  __shared__ float s_m[16][kRows], s_l[16][kRows];
+  __shared__ float s_o[16][kRows][kD + 4];
+  __shared__ float s_pv[4][kRows][kD];
+  __shared__ float s_pl[4][kRows];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  if (g == 0) {
+    s_m[wave][c] = m;
+    s_l[wave][c] = l;
+  }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = num[i] / den;
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_o[wave][c][16 * t + 4 * g + i] = o[t][i];
+  __syncthreads();
+
+  const int grp = wave >> 2, w0 = 4 * grp;
+  const int qq = (tid & 255) >> 4, d0 = (tid & 15) * 4;
+  const int nq = min(kRows, ti.nrows - ti.qt * kRows);
+  float M, L, O[4];
+  if (a.flat) {  // one split: all 16 waves fold straight into the output
+    if (grp == 0 && qq < nq) {
+      fold_waves<16>(s_m, s_l, s_o, 0, qq, d0, M, L, O);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
+      store_row4<T>(a, ti, qq, d0, v);
+    }
+    return;
+  }
+  fold_waves(s_m, s_l, s_o, w0, qq, d0, M, L, O);
+  if (ti.nsplit == 1) {  // uniform: the direct path of finish()
+    if (grp == 0 && qq < nq) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
+      store_row4<T>(a, ti, qq, d0, v);
+    }
+    return;
+  }
+  if (grp < ti.nsplit) {
+    const bool any = L > 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_pv[grp][qq][d0 + i] = any ? O[i] / L : 0.0f;
+    if (d0 == 0) s_pl[grp][qq] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
+  }
+  __syncthreads();
+  if (grp == 0 && qq < nq) {
+    float lse[4];
+    f32x4 ov[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sp = min(u, ti.nsplit - 1);
+      lse[u] = s_pl[sp][qq];
+      ov[u] = *reinterpret_cast<const f32x4 *>(&s_pv[sp][qq][d0]);
+    }
+    float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
+    fold_splits(0, ti.nsplit, lse, ov, Mx, den, num);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = num[i] / den;
+    store_row4<T>(a, ti, qq, d0, v);
   }
 }
 
@@ -313,12 +397,20 @@ __device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l
 // as one 16-byte run per dim.
 // Four waves per SIMD (<= 128 VGPRs): enough resident waves to keep HBM
 // busy at batch 8 and beyond.
-template <int MODE>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
+//
+// NW = 4: one split per workgroup (grid.y = split).  NW = 16: one workgroup
+// covers all 2..4 splits of its tile, four waves per split, and folds them in
+// LDS (finish_grouped) -- no combine launch, same bits; or, with a.flat, one
+// split over every key with all 16 waves striding it.
+template <int MODE, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
     AttnArgs a) {
   TileInfo ti;
-  if (!tile_info(a, ti)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (!tile_info(a, ti, /*any_split=*/NW == 16)) return;
+  const bool flat = NW == 16 && a.flat;
+  const int tid = threadIdx.x, lane = tid & 63, wave = flat ? (tid >> 6) : ((tid >> 6) & 3);
+  const int split_idx = (NW == 16) ? (flat ? 0 : (tid >> 8)) : (int)blockIdx.y;
+  const int wstride = flat ? 16 * 64 : 4 * 64;  // tokens between a wave's steps
   const int g = lane >> 4, c = lane & 15;
   const int r = ti.qt * kRows + c;
   const bool row_ok = r < ti.nrows;
@@ -333,7 +425,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
       reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
 
   if (a.rope) {
-    append_new_kv<__hip_bfloat16>(a, ti, blockIdx.y * a.split, (blockIdx.y + 1) * a.split);
+    if (NW == 16) append_new_kv<__hip_bfloat16>(a, ti, 0, ti.nsplit * a.split);
+    else append_new_kv<__hip_bfloat16>(a, ti, blockIdx.y * a.split, (blockIdx.y + 1) * a.split);
     __threadfence_block();
     __syncthreads();
   }
@@ -373,14 +466,15 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
   const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
   const int kv_len = ti.kv_len;
-  // wave w takes the 64-token steps w, w+4, w+8, ... of this split
-  const int s_lo = blockIdx.y * a.split;
+  // wave w takes the 64-token steps w, w+4, w+8, ... of its split (none
+  // when the split lies past this tile's keys); flat: w, w+16, ...
+  const int s_lo = split_idx * a.split;
   const int s_hi = min(s_lo + a.split, kv_len);
 
   // element offset of the (block, head) tile holding token pos
   auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
 
-  for (int c0 = s_lo + 64 * wave; c0 < s_hi; c0 += 256) {
+  for (int c0 = s_lo + 64 * wave; c0 < s_hi; c0 += wstride) {
     u32x4 kraw[2][2][2];  // [chunk][half][kk]
     u32x4 vraw[2][4];     // [chunk][dim tile]
 #pragma unroll
@@ -458,7 +552,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4,
         o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vraw[ch][tt]), pop, o[tt], 0, 0, 0);
     }
   }
-  finish<__hip_bfloat16>(a, ti, m, l, o);
+  if (NW == 16) finish_grouped<__hip_bfloat16>(a, ti, m, l, o);
+  else finish<__hip_bfloat16>(a, ti, m, l, o);
 }
 
 // ---------------------------------------------------------------- fp32 ----
@@ -614,6 +709,8 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
       n_heads % n_kv_heads || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
+  // split_tokens < 0 (one flat split) needs no partials; sizing it as the
+  // default also covers the fp32 kernels, which take the default instead
   split_tokens = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
                                   : choose_split(batch > 0 ? batch : 1, width > 0 ? width : 1, n_heads,
                                                  n_kv_heads, max_kv_len);
@@ -637,8 +734,11 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   a.H = n_heads;
   a.Hkv = n_kv_heads;
   a.bs = block_size;
-  a.split = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
-                             : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
+  a.flat = split_tokens < 0 && dtype == SPECDEC_BF16;
+  if (a.flat) a.split = (max_kv_len + 63) / 64 * 64;
+  else
+    a.split = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
+                               : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;
@@ -651,10 +751,18 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   dim3 grid((unsigned)units, (unsigned)a.max_splits), block(kAttnThreads);
   hipStream_t s = as_stream(stream);
   const bool bs16 = (block_size % 16) == 0;
+  if (dtype == SPECDEC_BF16 && (a.flat || (a.max_splits >= 2 && a.max_splits <= 4))) {
+    // every split of a tile in one 16-wave workgroup: no combine launch
+    dim3 g1((unsigned)units), b16(16 * kWave);
+    if (block_size == 16) attention_bf16_kernel<1, 16><<<g1, b16, 0, s>>>(a);
+    else if (bs16) attention_bf16_kernel<2, 16><<<g1, b16, 0, s>>>(a);
+    else attention_bf16_kernel<0, 16><<<g1, b16, 0, s>>>(a);
+    return launch_status();
+  }
   if (dtype == SPECDEC_BF16) {
-    if (block_size == 16) attention_bf16_kernel<1><<<grid, block, 0, s>>>(a);
-    else if (bs16) attention_bf16_kernel<2><<<grid, block, 0, s>>>(a);
-    else attention_bf16_kernel<0><<<grid, block, 0, s>>>(a);
+    if (block_size == 16) attention_bf16_kernel<1, 4><<<grid, block, 0, s>>>(a);
+    else if (bs16) attention_bf16_kernel<2, 4><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<0, 4><<<grid, block, 0, s>>>(a);
   } else if (dtype == SPECDEC_F32) {
     if (bs16) attention_f32_kernel<true><<<grid, block, 0, s>>>(a);
     else attention_f32_kernel<false><<<grid, block, 0, s>>>(a);

@@ -14,48 +14,64 @@ namespace specdec {
 
 constexpr int kNormThreads = 256;
 
-// One workgroup per row, the row held in registers (kNormPer values per
-// thread, dim <= kNormThreads * kNormPer).  If delta is non-null:
-// hidden <- hidden + delta (rounded to T) first.  Then
-// out <- weight * T(hidden * rsqrt(mean + eps)).
-constexpr int kNormPer = 32;
+// One workgroup per row, the row held in registers (PER values per thread,
+// dim <= kNormThreads * PER).  If delta is non-null: hidden <- hidden + delta
+// (rounded to T) first.  Then out <- weight * T(hidden * rsqrt(mean + eps)).
+constexpr int kNormPer = 32;  // largest PER: dim <= 8192
 
-template <typename T>
+template <typename T, int PER>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(T *__restrict__ hidden, const T *__restrict__ delta,
                                                                    const T *__restrict__ weight, T *__restrict__ out,
                                                                    int64_t dim, float eps) {
   __shared__ float red[kNormThreads / kWave];
   const int64_t row = blockIdx.x;
   T *h = hidden + row * dim;
-  const T *dl = delta ? delta + row * dim : nullptr;
+  const T *dl = delta ? delta + row * dim : h;  // h stands in when there is no delta
   T *y = out + row * dim;
   const int tid = threadIdx.x;
-  float v[kNormPer], w[kNormPer];
+  // every load is issued before the first store and without a branch
+  // (indices clamped into the row), so the row costs one memory round trip
+  float v[PER], w[PER], dv[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int64_t i = min(tid + (int64_t)k * kNormThreads, dim - 1);
+    v[k] = to_f32(h[i]);
+    w[k] = to_f32(weight[i]);
+    dv[k] = to_f32(dl[i]);
+  }
   float ss = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kNormPer; ++k) {
+  for (int k = 0; k < PER; ++k) {
     const int64_t i = tid + (int64_t)k * kNormThreads;
-    v[k] = 0.0f;
-    w[k] = 0.0f;
-    if (i < dim) {
-      float x = to_f32(h[i]);
-      if (dl) {
-        const T s = from_f32<T>(x + to_f32(dl[i]));
-        h[i] = s;
-        x = to_f32(s);
-      }
-      v[k] = x;
-      w[k] = to_f32(weight[i]);
+    if (delta) {
+      const T s = from_f32<T>(v[k] + dv[k]);
+      if (i < dim) h[i] = s;
+      v[k] = to_f32(s);
     }
+    if (i >= dim) v[k] = 0.0f;
     ss += v[k] * v[k];
   }
   ss = block_sum(ss, red);
   const float inv = rsqrtf(ss / (float)dim + eps);
 #pragma unroll
-  for (int k = 0; k < kNormPer; ++k) {
+  for (int k = 0; k < PER; ++k) {
     const int64_t i = tid + (int64_t)k * kNormThreads;
     if (i < dim) y[i] = from_f32<T>(w[k] * to_f32(from_f32<T>(v[k] * inv)));
   }
+}
+
+template <typename T>
+static void launch_add_rmsnorm(T *hidden, const T *delta, const T *weight, T *out, int64_t rows, int64_t dim,
+                               float eps, hipStream_t s) {
+  dim3 grid((unsigned)rows), block(kNormThreads);
+  if (dim <= 4 * kNormThreads)
+    add_rmsnorm_kernel<T, 4><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else if (dim <= 8 * kNormThreads)
+    add_rmsnorm_kernel<T, 8><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else if (dim <= 16 * kNormThreads)
+    add_rmsnorm_kernel<T, 16><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else
+    add_rmsnorm_kernel<T, kNormPer><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
 }
 
 template <typename T>
@@ -79,15 +95,13 @@ SPECDEC_API int specdec_add_rmsnorm(void *hidden, const void *delta, const void 
   if (dim > (int64_t)kNormThreads * kNormPer) return SPECDEC_EUNSUPPORTED;
   if (rows == 0) return SPECDEC_OK;
   if (!hidden || !weight || !out) return SPECDEC_EINVAL;
-  dim3 grid((unsigned)rows), block(kNormThreads);
   hipStream_t s = as_stream(stream);
   if (dtype == SPECDEC_BF16) {
-    add_rmsnorm_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
-        (__hip_bfloat16 *)hidden, (const __hip_bfloat16 *)delta, (const __hip_bfloat16 *)weight,
-        (__hip_bfloat16 *)out, dim, eps);
+    launch_add_rmsnorm<__hip_bfloat16>((__hip_bfloat16 *)hidden, (const __hip_bfloat16 *)delta,
+                                       (const __hip_bfloat16 *)weight, (__hip_bfloat16 *)out, rows, dim, eps, s);
   } else if (dtype == SPECDEC_F32) {
-    add_rmsnorm_kernel<float><<<grid, block, 0, s>>>((float *)hidden, (const float *)delta, (const float *)weight,
-                                                     (float *)out, dim, eps);
+    launch_add_rmsnorm<float>((float *)hidden, (const float *)delta, (const float *)weight, (float *)out, rows, dim,
+                              eps, s);
   } else {
     return SPECDEC_EINVAL;
   }

@@ -251,12 +251,11 @@ def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_k
 
 def latency_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_kv_len: int) -> int:
     """A split for calls whose bits need not match any other call (the draft
-    model): with few (row, head) units, one split of up to 2048 tokens, so
-    no combine kernel runs; otherwise the default."""
+    model).  With few (row, head) units: -1, one 16-wave workgroup per unit
+    striding every key, so no combine kernel is launched; otherwise 0 (the
+    default)."""
     units = batch * n_kv_heads * -(-(width * (n_heads // n_kv_heads)) // 16)
-    if units >= 64:
-        return 0
-    return min(max(256, -(-max_kv_len // 256) * 256), 2048)
+    return -1 if units < 64 else 0
 
 
 def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,

@@ -89,15 +89,18 @@ def test_bf16_gqa_small_blocks(bs):
         assert (got - want).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("L", [300, 1000, 1020, 4090])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_verify_rows_equal_decode_rows_bitwise(dtype):
+def test_verify_rows_equal_decode_rows_bitwise(dtype, L):
     """The same query at the same position gives identical bits whether it is
     verified among k+1 tokens or decoded alone: the reduction order depends
-    only on key positions (the property the greedy identity relies on)."""
+    only on key positions (the property the greedy identity relies on).  At
+    L = 1020 the verify call needs 5 splits (split kernel + combine kernel)
+    while the first decode calls need 4 (one 16-wave workgroup folding them
+    in LDS): both paths must give the same bits."""
     d, h, hkv, bs = 64, 32, 32, 16
-    L = 1000
     g = torch.Generator().manual_seed(5)
-    cache = make_cache(1, hkv, d, 128, bs, dtype, 1)
+    cache = make_cache(1, hkv, d, (L + 5) // bs + 8, bs, dtype, 1)
     cache.add(0)
     step = cache.append([0], [L + 5])
     kh = torch.randn(1, hkv, L + 5, d, generator=g).to(dtype).cuda()
@@ -155,10 +158,11 @@ def test_repeated_split_combines_stay_exact():
         assert (out.view(1, 5, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
 
 
-@pytest.mark.parametrize("split", [256, 512, 2048])
+@pytest.mark.parametrize("split", [256, 512, 2048, -1])
 @pytest.mark.parametrize("heads", [(32, 32), (9, 3)])
 def test_explicit_split_sizes(split, heads):
-    """Caller-chosen splits (the draft's single-split policy) against SDPA."""
+    """Caller-chosen splits against SDPA; -1 is the draft's flat policy (one
+    16-wave workgroup striding every key)."""
     h, hkv = heads
     d, bs = 64, 16
     g = torch.Generator().manual_seed(split + h)
