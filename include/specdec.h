@@ -56,11 +56,15 @@ int specdec_abi_version(void);
 /* ---------------------------------------------------------------- accept --- */
 
 /* Temperature softmax, or one-hot argmax at temperature 0 (ties -> lowest id).
- * logits [rows, vocab] (row_stride apart, dtype F32/F64/BF16) -> out fp32.
+ * logits [rows, vocab] (row_stride apart, dtype F32/F64/BF16) -> out fp32
+ * (out_stride apart).  At temperature 0 a non-NULL index_out also receives
+ * each row's argmax (index_out[row * index_stride]): the token an
+ * inverse-CDF draw from that one-hot row returns for any u in [0, 1).
  * Replaces lm/sampling.py:13-18 `probabilities`. */
 int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                           int64_t row_stride, float temperature, float *out,
-                          int64_t out_stride, void *stream);
+                          int64_t out_stride, int64_t *index_out, int64_t index_stride,
+                          void *stream);
 
 /* Fused accept-reject for a batch: gather p(x), q(x) of the drafted tokens,
  * test u*q(x) < p(x), count the leading accepts n, build the residual

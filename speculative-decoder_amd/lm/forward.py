@@ -31,6 +31,16 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return ops.add_rmsnorm(x.clone(), None, weight, out, eps)
 
 
+def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool) -> torch.Tensor:
+    """x @ w.T on torch: a matrix-vector product when asked for and x is a
+    single row (about a microsecond less per call at decode sizes), else the
+    GEMM.  The two may round differently, so a model uses one of them for
+    every call whose bits must agree."""
+    if gemv and x.numel() == x.shape[-1]:
+        return torch.mv(w, x.reshape(-1)).view(*x.shape[:-1], w.shape[0])
+    return F.linear(x, w)
+
+
 def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Tensor, max_kv_len: int,
                  last: torch.Tensor | None = None, workspace: ops.AttentionWorkspace | None = None,
                  split_tokens: int = 0) -> torch.Tensor:
@@ -39,8 +49,11 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     length after the append; `last` (int64 [B]) selects one row per batch
     entry before the output projection.  `split_tokens` is the attention
     split (0: the fixed default whose results do not depend on the other
-    queries of the call)."""
+    queries of the call; nonzero marks a latency call -- the draft -- whose
+    bits need not match other calls, which also lets single-row projections
+    run as matrix-vector products)."""
     cfg = llama.config
+    gemv = split_tokens != 0
     b, t = ids.shape
     h, hk, d, inter, eps = (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size,
                             cfg.rms_norm_eps)
@@ -52,14 +65,14 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
     act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
     for i, layer in enumerate(layers):
-        qkv = F.linear(x, layer.wqkv)
+        qkv = _project(x, layer.wqkv, gemv)
         ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t, h,
                                  hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
                                  split_tokens)
-        ops.add_rmsnorm(hidden, F.linear(attn, layer.wo), layer.ln2, x, eps)
-        ops.silu_mul(F.linear(x, layer.wgu), act)
+        ops.add_rmsnorm(hidden, _project(attn, layer.wo, gemv), layer.ln2, x, eps)
+        ops.silu_mul(_project(x, layer.wgu, gemv), act)
         nxt = layers[i + 1].ln1 if i + 1 < len(layers) else llama.norm
-        ops.add_rmsnorm(hidden, F.linear(act, layer.wd), nxt, x, eps)
+        ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), nxt, x, eps)
     if last is not None:
         x = x[torch.arange(b, device=x.device), last]
     return logits(llama, x)

@@ -140,6 +140,7 @@ class DraftStepGraph(_Captured):
         self.ids = torch.zeros(batch, width, dtype=torch.int64, device=dev)
         self.meta = torch.zeros(3, batch, dtype=torch.int32, device=dev)
         self.u = torch.zeros(batch, dtype=torch.float32, device=dev)
+        self.token = torch.zeros(batch, dtype=torch.int64, device=dev)
 
     def run(self, ids, meta, u):
         def prepare():
@@ -150,6 +151,8 @@ class DraftStepGraph(_Captured):
         def work():
             last = self.meta[2].long() - 1
             lg = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split)
+            if self.temperature == 0.0:  # the one-hot row's inverse-CDF draw is its argmax
+                return ops.probabilities(lg, 0.0, index_out=self.token), self.token
             q = ops.probabilities(lg, self.temperature)
             return q, ops.sample_inverse_cdf(q, self.u)
 
@@ -166,7 +169,6 @@ class DraftChainGraph(_Captured):
         self.temperature, self.steps = temperature, steps
         v = llama.config.vocab_size
         self.first = torch.zeros(batch, 1, dtype=torch.int64, device=dev)
-        self.ids = torch.zeros(batch, 1, dtype=torch.int64, device=dev)
         self.metas = torch.zeros(steps, 3, batch, dtype=torch.int32, device=dev)
         self.u = torch.zeros(steps, batch, dtype=torch.float32, device=dev)
         self.q = torch.zeros(batch, steps, v, dtype=torch.float32, device=dev)
@@ -179,15 +181,18 @@ class DraftChainGraph(_Captured):
             self.u.copy_(u, non_blocking=True)
 
         def work():
-            self.ids.copy_(self.first)
+            ids = self.first
             for i in range(self.steps):
-                lg = forward_core(self.llama, self.cache, self.metas[i], self.ids, self.bucket, None, self.ws,
+                lg = forward_core(self.llama, self.cache, self.metas[i], ids, self.bucket, None, self.ws,
                                   self.split)
-                q = ops.probabilities(lg.view(self.batch, -1), self.temperature)
-                tok = ops.sample_inverse_cdf(q, self.u[i])
-                self.q[:, i].copy_(q)
-                self.tokens[:, i].copy_(tok)
-                self.ids.copy_(tok.view(-1, 1))
+                if self.temperature == 0.0:
+                    # the inverse-CDF draw from a one-hot row is its argmax for
+                    # every u, so the softmax kernel writes the token itself
+                    ops.probabilities(lg.view(self.batch, -1), 0.0, out=self.q[:, i], index_out=self.tokens[:, i])
+                else:
+                    ops.probabilities(lg.view(self.batch, -1), self.temperature, out=self.q[:, i])
+                    self.tokens[:, i].copy_(ops.sample_inverse_cdf(self.q[:, i], self.u[i]))
+                ids = self.tokens[:, i:i + 1]
             return self.q, self.tokens
 
         return self.replay(prepare, work)

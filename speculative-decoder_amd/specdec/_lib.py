@@ -15,7 +15,7 @@ I64 = c_int64
 # name -> argument types (all return int)
 SIGNATURES: dict[str, list] = {
     "specdec_abi_version": [],
-    "specdec_probabilities": [P, c_int, I64, I64, I64, c_float, P, I64, P],
+    "specdec_probabilities": [P, c_int, I64, I64, I64, c_float, P, I64, P, I64, P],
     "specdec_accept_reject": [P, P, c_int, I64, I64, I64, I64, P, P, P, I64, I64, I64, P, P],
     "specdec_accept_count": [P, P, c_int, I64, I64, I64, I64, P, P, I64, I64, P, P],
     "specdec_sample_inverse_cdf": [P, c_int, I64, I64, I64, P, P, P],

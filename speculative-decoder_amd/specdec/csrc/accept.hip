@@ -32,66 +32,116 @@ __device__ __forceinline__ float round_to(double x, float) { return static_cast<
 __device__ __forceinline__ double round_to(double x, double) { return x; }
 
 // ------------------------------------------------------------ softmax ----
+// One workgroup per row.  Rows of up to kSoftPer * 1024 elements (49152, the
+// vocab) are read once into registers -- every load issued before the first
+// use, so the row costs one memory round trip -- and written from there;
+// longer rows take the streaming loop below.  Index i of chunk element k of
+// thread tid is k * 1024 + tid (coalesced).
+constexpr int kSoftPer = 48;
+
+// argmax with the first index among equal maxima
+__device__ __forceinline__ void argmax_merge(float &best, int &best_i, float v, int i) {
+  if (v > best || (v == best && i < best_i)) {
+    best = v;
+    best_i = i;
+  }
+}
+
+__device__ __forceinline__ int block_argmax(float best, int best_i, float *red_f, int *red_i) {
+  for (int o = kWave / 2; o > 0; o >>= 1) argmax_merge(best, best_i, __shfl_xor(best, o, kWave), __shfl_xor(best_i, o, kWave));
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  if (lane == 0) {
+    red_f[wid] = best;
+    red_i[wid] = best_i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < (int)(blockDim.x / kWave); ++w) argmax_merge(best, best_i, red_f[w], red_i[w]);
+    red_i[0] = best_i;
+  }
+  __syncthreads();
+  return red_i[0];
+}
+
 template <typename TIn>
 __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
     const TIn *__restrict__ logits, int64_t row_stride, int64_t vocab, float temperature,
-    float *__restrict__ out, int64_t out_stride) {
+    float *__restrict__ out, int64_t out_stride, int64_t *__restrict__ index_out, int64_t index_stride) {
   __shared__ float red_f[kSoftmaxThreads / kWave];
   __shared__ int red_i[kSoftmaxThreads / kWave];
   const int64_t row = blockIdx.x;
   const TIn *x = logits + row * row_stride;
   float *y = out + row * out_stride;
   const int tid = threadIdx.x;
+  constexpr float kLog2e = 1.4426950408889634f;
+  const bool fits = vocab <= (int64_t)kSoftPer * kSoftmaxThreads;
 
   if (temperature == 0.0f) {
-    // argmax of the raw logits, first index among equal maxima
+    // one_hot(argmax(logits)) of the raw logits
     float best = -INFINITY;
     int best_i = INT32_MAX;
-    for (int64_t i = tid; i < vocab; i += blockDim.x) {
-      float v = to_f32(x[i]);
-      if (v > best || (v == best && i < best_i)) { best = v; best_i = (int)i; }
-    }
-    // wave level
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-      float ov = __shfl_xor(best, o, kWave);
-      int oi = __shfl_xor(best_i, o, kWave);
-      if (ov > best || (ov == best && oi < best_i)) { best = ov; best_i = oi; }
-    }
-    const int lane = tid & (kWave - 1), wid = tid / kWave;
-    if (lane == 0) { red_f[wid] = best; red_i[wid] = best_i; }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < (int)(blockDim.x / kWave); ++w) {
-        if (red_f[w] > best || (red_f[w] == best && red_i[w] < best_i)) {
-          best = red_f[w]; best_i = red_i[w];
-        }
+    if (fits) {
+      const int last = (int)vocab - 1;
+      float v[kSoftPer];
+#pragma unroll
+      for (int k = 0; k < kSoftPer; ++k) v[k] = to_f32(x[min(k * kSoftmaxThreads + tid, last)]);
+#pragma unroll
+      for (int k = 0; k < kSoftPer; ++k) {
+        const int i = k * kSoftmaxThreads + tid;
+        if (i < vocab) argmax_merge(best, best_i, v[k], i);
       }
-      red_i[0] = best_i;
+    } else {
+      for (int64_t i = tid; i < vocab; i += blockDim.x) argmax_merge(best, best_i, to_f32(x[i]), (int)i);
     }
-    __syncthreads();
-    const int hot = red_i[0];
+    const int hot = block_argmax(best, best_i, red_f, red_i);
+    if (index_out && tid == 0) index_out[row * index_stride] = hot;
     for (int64_t i = tid; i < vocab; i += blockDim.x) y[i] = (i == hot) ? 1.0f : 0.0f;
     return;
   }
 
-  // logits.float() / T, then a max-shifted softmax: one pass keeps a running
-  // (max, sum) per thread, merged across the workgroup; a second pass
-  // writes.  exp(v - m) is evaluated as 2^((v - m) * log2 e) on the
-  // hardware exp2 (about 1e-6 relative for the shifts that matter).
-  constexpr float kLog2e = 1.4426950408889634f;
-  float m = -INFINITY, s = 0.0f;
+  // softmax(logits.float() / T): exp(v - m) is evaluated as
+  // 2^((v - m) * log2 e) on the hardware exp2 (about 1e-6 relative for the
+  // shifts that matter)
+  if (fits) {
+    const int last = (int)vocab - 1;
+    float v[kSoftPer];
+#pragma unroll
+    for (int k = 0; k < kSoftPer; ++k) v[k] = to_f32(x[min(k * kSoftmaxThreads + tid, last)]);
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSoftPer; ++k) {
+      v[k] = (k * kSoftmaxThreads + tid < vocab) ? v[k] / temperature : -INFINITY;
+      m = fmaxf(m, v[k]);
+    }
+    const float mg = block_max(m, red_f);
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kSoftPer; ++k) {
+      v[k] = __builtin_amdgcn_exp2f((v[k] - mg) * kLog2e);
+      sum += v[k];
+    }
+    const float inv = 1.0f / block_sum(sum, red_f);
+#pragma unroll
+    for (int k = 0; k < kSoftPer; ++k) {
+      const int i = k * kSoftmaxThreads + tid;
+      if (i < vocab) y[i] = v[k] * inv;
+    }
+    return;
+  }
+  // streaming: a running (max, sum) per thread, merged across the workgroup,
+  // then a second pass that writes
+  float m = -INFINITY, sum = 0.0f;
   for (int64_t i = tid; i < vocab; i += blockDim.x) {
     const float v = to_f32(x[i]) / temperature;
     if (v > m) {
-      s = (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - v) * kLog2e);
+      sum = (m == -INFINITY) ? 0.0f : sum * __builtin_amdgcn_exp2f((m - v) * kLog2e);
       m = v;
     }
-    s += __builtin_amdgcn_exp2f((v - m) * kLog2e);
+    sum += __builtin_amdgcn_exp2f((v - m) * kLog2e);
   }
   const float mg = block_max(m, red_f);
-  s = (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - mg) * kLog2e);
-  s = block_sum(s, red_f);
-  const float inv = 1.0f / s;
+  sum = (m == -INFINITY) ? 0.0f : sum * __builtin_amdgcn_exp2f((m - mg) * kLog2e);
+  const float inv = 1.0f / block_sum(sum, red_f);
   for (int64_t i = tid; i < vocab; i += blockDim.x)
     y[i] = __builtin_amdgcn_exp2f((to_f32(x[i]) / temperature - mg) * kLog2e) * inv;
 }
@@ -451,7 +501,8 @@ SPECDEC_API int specdec_abi_version(void) { return 5; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,
-                                      int64_t out_stride, void *stream) {
+                                      int64_t out_stride, int64_t *index_out, int64_t index_stride,
+                                      void *stream) {
   if (rows < 0 || vocab <= 0 || vocab > INT32_MAX || temperature < 0.0f) return SPECDEC_EINVAL;
   if (rows == 0) return SPECDEC_OK;
   if (!logits || !out) return SPECDEC_EINVAL;
@@ -460,15 +511,16 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
   switch (dtype) {
     case SPECDEC_F32:
       probabilities_kernel<float><<<grid, block, 0, s>>>((const float *)logits, row_stride, vocab,
-                                                        temperature, out, out_stride);
+                                                        temperature, out, out_stride, index_out, index_stride);
       break;
     case SPECDEC_F64:
-      probabilities_kernel<double><<<grid, block, 0, s>>>((const double *)logits, row_stride,
-                                                         vocab, temperature, out, out_stride);
+      probabilities_kernel<double><<<grid, block, 0, s>>>((const double *)logits, row_stride, vocab,
+                                                         temperature, out, out_stride, index_out, index_stride);
       break;
     case SPECDEC_BF16:
-      probabilities_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
-          (const __hip_bfloat16 *)logits, row_stride, vocab, temperature, out, out_stride);
+      probabilities_kernel<__hip_bfloat16><<<grid, block, 0, s>>>((const __hip_bfloat16 *)logits, row_stride,
+                                                                 vocab, temperature, out, out_stride, index_out,
+                                                                 index_stride);
       break;
     default: return SPECDEC_EINVAL;
   }

@@ -50,18 +50,35 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 # ------------------------------------------------------------------ accept --
-def probabilities(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """[..., V] logits -> fp32 probabilities (one-hot argmax at temperature 0)."""
+def probabilities(logits: torch.Tensor, temperature: float, out: torch.Tensor | None = None,
+                  index_out: torch.Tensor | None = None) -> torch.Tensor:
+    """[..., V] logits -> fp32 probabilities (one-hot argmax at temperature
+    0).  `out` may be a row-strided view to write into (rows of V fp32 with
+    unit inner stride); at temperature 0 `index_out` (int64, one per row,
+    any row stride) receives each row's argmax."""
     gpu(logits, "logits")
     shape = logits.shape
     x = logits.reshape(-1, shape[-1])
     if x.stride(-1) != 1:
         x = x.contiguous()
-    out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-    st = lib().specdec_probabilities(x.data_ptr(), dtype_code(x), x.shape[0], x.shape[1], x.stride(0),
-                                     float(temperature), out.data_ptr(), out.stride(0), stream())
+    rows, v = x.shape
+    fresh = out is None
+    if fresh:
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    o2 = out if out.dim() == 2 else out.view(rows, v)
+    if o2.dtype != torch.float32 or tuple(o2.shape) != (rows, v) or o2.stride(-1) != 1:
+        raise ValueError("out must be fp32 [rows, V] with unit inner stride")
+    idx_ptr, idx_stride = None, 0
+    if index_out is not None:
+        if temperature != 0.0:
+            raise ValueError("index_out is defined at temperature 0 only")
+        if index_out.dtype != torch.int64 or index_out.numel() != rows:
+            raise ValueError("index_out must hold one int64 per row")
+        idx_ptr, idx_stride = index_out.data_ptr(), (index_out.stride(0) if index_out.dim() else 1)
+    st = lib().specdec_probabilities(x.data_ptr(), dtype_code(x), rows, v, x.stride(0), float(temperature),
+                                     o2.data_ptr(), o2.stride(0), idx_ptr, idx_stride, stream())
     _check(st, "probabilities")
-    return out.view(shape)
+    return out.view(shape) if fresh else out
 
 
 def _rows3(t: torch.Tensor) -> torch.Tensor:

@@ -43,6 +43,33 @@ def test_probabilities_match_torch_softmax(temperature):
         assert (got.double().sum(-1) - 1).abs().max() < 1e-5
 
 
+@pytest.mark.parametrize("vocab", [V, 1000, 70000])
+def test_probabilities_into_strided_rows_with_argmax(vocab):
+    """Writing into a row-strided view (the draft chain's q[:, i]) gives the
+    same rows; at temperature 0 index_out holds each row's argmax, which is
+    what an inverse-CDF draw from the one-hot row returns.  70000 exceeds the
+    register-resident row size and takes the streaming loop."""
+    from specdec import ops
+
+    g = torch.Generator().manual_seed(vocab)
+    x = (torch.randn(3, vocab, generator=g) * 3).cuda()
+    for temperature in (0.0, 0.7):
+        want = osamp.probabilities(x.cpu(), temperature)
+        q = torch.full((3, 2, vocab), -1.0, device="cuda")
+        idx = torch.full((3, 2), -1, dtype=torch.int64, device="cuda")
+        ops.probabilities(x, temperature, out=q[:, 1], index_out=idx[:, 1] if temperature == 0.0 else None)
+        got = q[:, 1].cpu()
+        assert torch.equal(q[:, 0].cpu(), torch.full((3, vocab), -1.0))
+        if temperature == 0.0:
+            assert torch.equal(got, want)
+            assert idx[:, 1].cpu().tolist() == x.cpu().argmax(-1).tolist()
+            assert idx[:, 0].cpu().tolist() == [-1, -1, -1]
+            u = torch.rand(3, generator=g)
+            assert sample_inverse_cdf(q[:, 1].contiguous(), u.cuda()).cpu().tolist() == idx[:, 1].cpu().tolist()
+        else:
+            assert torch.allclose(got, want, rtol=1e-5, atol=1e-12)
+
+
 def test_probabilities_argmax_ties_go_to_lowest_id():
     x = torch.tensor([[1.0, 3.0, 3.0, 2.0], [5.0, 5.0, 5.0, 5.0], [-1.0, -2.0, -1.0, -3.0]])
     got = probabilities(x.cuda(), 0.0).cpu()
