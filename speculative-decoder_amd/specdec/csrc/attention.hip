@@ -46,6 +46,7 @@ constexpr int kAttnThreads = 256;  // 4 waves
 constexpr int kRows = 16;          // query rows per tile
 constexpr int kDefaultSplit = 256;
 constexpr int kPart = kRows * (kD + 1);  // floats per split partial: O/l [16][64], lse [16]
+constexpr int kStage = 16;  // appended tokens per workgroup taken from LDS
 
 struct AttnArgs {
   const void *q;
@@ -424,11 +425,69 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   const u16 *qrow =
       reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
 
-  if (a.rope) {
-    if (NW == 16) append_new_kv<__hip_bfloat16>(a, ti, 0, ti.nsplit * a.split);
-    else append_new_kv<__hip_bfloat16>(a, ti, blockIdx.y * a.split, (blockIdx.y + 1) * a.split);
-    __threadfence_block();
-    __syncthreads();
+  const int Hkv = a.Hkv;
+  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+  const int bs = (MODE == 1) ? 16 : a.bs;
+  const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
+  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
+  const int kv_len = ti.kv_len;
+  const int last_blk = (kv_len - 1) / bs;
+  // wave w takes the 64-token steps w, w+4, w+8, ... of its split (none
+  // when the split lies past this tile's keys); flat: w, w+16, ...
+  const int s_lo = split_idx * a.split;
+  const int s_hi = min(s_lo + a.split, kv_len);
+  const int c_first = s_lo + 64 * wave;
+
+  // Fused append.  The new tokens of this workgroup's key range [lo, hi)
+  // are rotated once into LDS (and written to the pools for later calls);
+  // the key loop takes them from LDS instead of the pool, so no pool store
+  // has to complete before the first key load.  More than kStage of them
+  // (a long prefill) take the plain path: append, fence, then read.
+  const int lo = (NW == 16) ? 0 : (int)blockIdx.y * a.split;
+  const int hi = (NW == 16) ? ti.nsplit * a.split : lo + a.split;
+  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + a.meta[2 * a.batch + ti.b]);
+  const int n_in = max(p1 - p0, 0);
+  const bool staged = MODE != 0 && a.rope && n_in <= kStage;
+  __shared__ __align__(16) u16 s_nk[kStage][kD];
+  __shared__ __align__(16) u16 s_nv[kStage][kD];
+
+  // ---- prologue: every load here depends on the row metadata only, so
+  // all of them are in flight together
+  // this wave's first-step block ids: lane j (j = lane & 3) holds the block
+  // of tokens c0 + 16j .. c0 + 16j + 15
+  int bj = 0;
+  if (MODE != 0 && c_first < s_hi) bj = trow[min((c_first + 16 * (lane & 3)) / bs, last_blk)];
+  constexpr int kThreads = NW * kWave;
+  constexpr int kKT = (kStage * (kD / 2) + kThreads - 1) / kThreads;  // k pairs per thread
+  constexpr int kVT = (kStage * kD + kThreads - 1) / kThreads;        // v elements per thread
+  float sk1[kKT], sk2[kKT], scs[kKT], ssn[kKT];
+  int skb[kKT], svb[kVT];
+  u16 svv[kVT];
+  const u16 *qkv16 = reinterpret_cast<const u16 *>(a.q);
+  auto new_row = [&](int pos) { return qkv16 + ((int64_t)ti.b * a.width + (pos - ti.past)) * a.q_stride; };
+  if (staged) {
+#pragma unroll
+    for (int u = 0; u < kKT; ++u) {
+      const int task = tid + u * kThreads;
+      if (task < n_in * (kD / 2)) {
+        const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
+        const u16 *kx = new_row(pos) + (int64_t)(a.H + ti.h) * kD;
+        sk1[u] = to_f32(__builtin_bit_cast(__hip_bfloat16, kx[i]));
+        sk2[u] = to_f32(__builtin_bit_cast(__hip_bfloat16, kx[i + kD / 2]));
+        scs[u] = a.cos_t[(int64_t)pos * (kD / 2) + i];
+        ssn[u] = a.sin_t[(int64_t)pos * (kD / 2) + i];
+        skb[u] = trow[pos / bs];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kVT; ++u) {
+      const int task = tid + u * kThreads;
+      if (task < n_in * kD) {
+        const int pos = p0 + task / kD, dd = task % kD;
+        svv[u] = new_row(pos)[(int64_t)(a.H + Hkv + ti.h) * kD + dd];
+        svb[u] = trow[pos / bs];
+      }
+    }
   }
 
   // Q operand: lane (query c, group g) holds dims 8g..8g+7 (kk = 0) and
@@ -455,26 +514,65 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
     }
   }
 
+  if (staged) {
+    u16 *kpw = const_cast<u16 *>(kp);
+    u16 *vpw = const_cast<u16 *>(vp);
+#pragma unroll
+    for (int u = 0; u < kKT; ++u) {
+      const int task = tid + u * kThreads;
+      if (task < n_in * (kD / 2)) {
+        const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
+        float y1, y2;
+        rope_pair(sk1[u], sk2[u], scs[u], ssn[u], y1, y2);
+        const u16 b1 = __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(y1));
+        const u16 b2 = __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(y2));
+        s_nk[pos - p0][i] = b1;
+        s_nk[pos - p0][i + kD / 2] = b2;
+        u16 *kd = kpw + ((int64_t)skb[u] * Hkv + ti.h) * tile_elems + (int64_t)(pos % bs) * kD;
+        kd[i] = b1;
+        kd[i + kD / 2] = b2;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kVT; ++u) {
+      const int task = tid + u * kThreads;
+      if (task < n_in * kD) {
+        const int pos = p0 + task / kD, dd = task % kD;
+        s_nv[pos - p0][dd] = svv[u];
+        vpw[((int64_t)svb[u] * Hkv + ti.h) * tile_elems + (int64_t)dd * bs + pos % bs] = svv[u];
+      }
+    }
+  }
+  if (a.rope) {
+    if (!staged) {
+      append_new_kv<__hip_bfloat16>(a, ti, lo, hi);
+      __threadfence_block();
+    }
+    __syncthreads();
+  }
+
   f32x4 o[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  const int Hkv = a.Hkv;
-  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
-  const int bs = (MODE == 1) ? 16 : a.bs;
-  const int64_t tile_elems = (int64_t)bs * kD;  // one (block, head) tile
-  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
-  const int kv_len = ti.kv_len;
-  // wave w takes the 64-token steps w, w+4, w+8, ... of its split (none
-  // when the split lies past this tile's keys); flat: w, w+16, ...
-  const int s_lo = split_idx * a.split;
-  const int s_hi = min(s_lo + a.split, kv_len);
-
   // element offset of the (block, head) tile holding token pos
   auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
 
-  for (int c0 = s_lo + 64 * wave; c0 < s_hi; c0 += wstride) {
+  for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
+    // tile offsets of the step's four 16-token groups (MODE != 0), uniform
+    // across the wave; a lane picks between two of them with a select (a
+    // dynamically indexed array would be placed in memory)
+    int64_t tofs0 = 0, tofs1 = 0, tofs2 = 0, tofs3 = 0;
+    if (MODE != 0) {
+      tofs0 = ((int64_t)__builtin_amdgcn_readlane(bj, 0) * Hkv + ti.h) * tile_elems;
+      tofs1 = ((int64_t)__builtin_amdgcn_readlane(bj, 1) * Hkv + ti.h) * tile_elems;
+      tofs2 = ((int64_t)__builtin_amdgcn_readlane(bj, 2) * Hkv + ti.h) * tile_elems;
+      tofs3 = ((int64_t)__builtin_amdgcn_readlane(bj, 3) * Hkv + ti.h) * tile_elems;
+    }
+    auto group_tile = [&](int ch, bool upper) -> int64_t {
+      return ch == 0 ? (upper ? tofs1 : tofs0) : (upper ? tofs3 : tofs2);
+    };
     u32x4 kraw[2][2][2];  // [chunk][half][kk]
     u32x4 vraw[2][4];     // [chunk][dim tile]
 #pragma unroll
@@ -484,9 +582,11 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
       for (int hf = 0; hf < 2; ++hf) {
         const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
         const bool ok = (MODE == 0) ? tok < kv_len : (tok / bs) * bs < kv_len;
+        const bool fresh = staged && tok >= p0 && tok < p1;  // appended by this call: from LDS
         kraw[ch][hf][0] = kraw[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
-        if (ok) {
-          const u16 *kb = kp + tile_of(tok) + (int64_t)(tok % bs) * kD + 8 * g;
+        if (ok && !fresh) {
+          const int64_t to = (MODE != 0) ? group_tile(ch, (c >> 3) != 0) : tile_of(tok);
+          const u16 *kb = kp + to + (int64_t)(tok % bs) * kD + 8 * g;
           kraw[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
           kraw[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
         }
@@ -496,7 +596,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
       for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{0u, 0u, 0u, 0u};
       if (MODE != 0) {
         if ((vt / bs) * bs < kv_len) {
-          const u16 *vb = vp + tile_of(vt) + vt % bs;
+          const u16 *vb = vp + group_tile(ch, (g >> 1) != 0) + vt % bs;
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
             vraw[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
@@ -514,6 +614,37 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
         }
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
+      }
+    }
+    // next step's block ids, in flight during this step's arithmetic
+    if (MODE != 0 && c0 + wstride < s_hi)
+      bj = trow[min((c0 + wstride + 16 * (lane & 3)) / bs, last_blk)];
+    // keys appended by this call: K rows and V elements from LDS
+    if (staged && c0 + 64 > p0 && c0 < p1) {
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        const int cs = c0 + 32 * ch;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
+          if (tok >= p0 && tok < p1) {
+            kraw[ch][hf][0] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][8 * g]);
+            kraw[ch][hf][1] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][32 + 8 * g]);
+          }
+        }
+        const int vt = cs + 8 * g;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int pos = vt + i;
+          if (pos >= p0 && pos < p1) {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+              const unsigned sh = 16 * (i & 1);
+              const unsigned wd = vraw[ch][tt][i >> 1];
+              vraw[ch][tt][i >> 1] = (wd & ~(0xFFFFu << sh)) | ((unsigned)s_nv[pos - p0][16 * tt + c] << sh);
+            }
+          }
+        }
       }
     }
 
