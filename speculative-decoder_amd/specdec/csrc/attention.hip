@@ -64,6 +64,9 @@ struct AttnArgs {
   int batch, width, H, Hkv, bs;
   float scale;
   int split, max_splits, n_qtiles;
+  // split partial slots per unit in the workspace (max_splits, or 1 when
+  // no combine runs)
+  int parts;
   // 16-wave launches only: one split over every key, wave w taking the
   // 64-token steps w, w+16, ... (results need not match other calls)
   int flat;
@@ -208,7 +211,7 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
     return;
   }
   // split partial for the combine kernel: O / l [16][64] and lse [16]
-  float *ws = a.ws + ((int64_t)ti.unit * a.max_splits + blockIdx.y) * kPart;
+  float *ws = a.ws + ((int64_t)ti.unit * a.parts + blockIdx.y) * kPart;
   const bool any = L > 0.0f;
   f32x4 v;
 #pragma unroll
@@ -250,19 +253,25 @@ __device__ __forceinline__ void fold_splits(int s0, int ns, const float (&lse)[G
 }
 
 // Final combine of the split partials, one workgroup per (row, head, tile)
-// with more than one split: thread (q, 4 dims) folds every split in split
-// order, 32 splits per load group.  The first group's loads are issued
+// with more than one split.  The fold tree depends only on the key
+// positions: splits are folded in groups of four (4 consecutive 256-token
+// splits, fold_splits<4>), each group becomes (O / l, lse) like a split, and
+// the groups are folded in order, eight per step (fold_splits<8>).  A tile
+// with at most four splits is run by one 16-wave workgroup that folds its
+// single group the same way, so a query gets the same bits on either path;
+// splits or groups holding none of a query's keys take no part.  Thread
+// (q, 4 dims) does the folding; the first 32 splits' loads are issued
 // before the row metadata arrives (their addresses depend only on the
-// workgroup); splits the row does not have are never folded.
+// workgroup).
 __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArgs a, int dtype) {
   const int tid = threadIdx.x;
   const int qq = tid >> 4, d0 = (tid & 15) * 4;
-  const float *ws0 = a.ws + (int64_t)blockIdx.x * a.max_splits * kPart;
+  const float *ws0 = a.ws + (int64_t)blockIdx.x * a.parts * kPart;
   float lse[32];
   f32x4 ov[32];
 #pragma unroll
   for (int u = 0; u < 32; ++u) {
-    const float *p = ws0 + (int64_t)min(u, a.max_splits - 1) * kPart;
+    const float *p = ws0 + (int64_t)min(u, a.parts - 1) * kPart;
     lse[u] = p[kRows * kD + qq];
     ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
   }
@@ -270,17 +279,37 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
   if (!tile_info(a, ti, /*any_split=*/true) || ti.nsplit == 1) return;
   const int nq = min(kRows, ti.nrows - ti.qt * kRows);
   if (qq >= nq) return;
-  const int ns = ti.nsplit;
+  const int ns = ti.nsplit, ngroups = (ns + 3) / 4;
   float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
-  fold_splits(0, ns, lse, ov, Mx, den, num);
-  for (int s0 = 32; s0 < ns; s0 += 32) {
+  for (int s0 = 0; s0 < ns; s0 += 32) {
+    if (s0 > 0) {
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      const float *p = ws0 + (int64_t)min(s0 + u, ns - 1) * kPart;
-      lse[u] = p[kRows * kD + qq];
-      ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
+      for (int u = 0; u < 32; ++u) {
+        const float *p = ws0 + (int64_t)min(s0 + u, ns - 1) * kPart;
+        lse[u] = p[kRows * kD + qq];
+        ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
+      }
     }
-    fold_splits(s0, ns, lse, ov, Mx, den, num);
+    float gl[8];
+    f32x4 gv[8];
+#pragma unroll
+    for (int y = 0; y < 8; ++y) {
+      const int n_y = min(max(ns - (s0 + 4 * y), 0), 4);
+      float l4[4];
+      f32x4 v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        l4[u] = lse[4 * y + u];
+        v4[u] = ov[4 * y + u];
+      }
+      float m4 = -INFINITY, d4 = 0.0f, n4[4] = {0.f, 0.f, 0.f, 0.f};
+      fold_splits(0, n_y, l4, v4, m4, d4, n4);
+      const bool any = d4 > 0.0f;
+      gl[y] = any ? m4 + __builtin_amdgcn_logf(d4) : -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gv[y][i] = any ? n4[i] / d4 : 0.0f;
+    }
+    fold_splits(s0 / 4, ngroups, gl, gv, Mx, den, num);
   }
   float v[4];
 #pragma unroll
@@ -289,11 +318,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
   else store_row4<float>(a, ti, qq, d0, v);
 }
 
-// Single-workgroup variant of finish() for 2 to 4 splits (16 waves, wave w
-// in split w / 4): each group of four waves folds into its split partial
-// exactly as finish() would write it, the partials meet in LDS, and group 0
-// folds them with fold_splits -- the same bits the combine kernel produces,
-// without its launch.
+// finish() of a 16-wave bf16 workgroup running every split of its tile (at
+// most four): each group of four waves folds into its split partial exactly
+// as finish() does, the partials meet in LDS and group 0 folds them with
+// fold_splits<4> -- the first level of the combine kernel's fold tree, whose
+// result for a single group is the same bits.  With a.flat (one split over
+// every key, results that need not match other calls) all 16 waves fold
+// straight into the output.
 template <typename T>
 __device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
   __shared__ float s_m[16][kRows], s_l[16][kRows];
@@ -316,7 +347,7 @@ __device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, f
   const int qq = (tid & 255) >> 4, d0 = (tid & 15) * 4;
   const int nq = min(kRows, ti.nrows - ti.qt * kRows);
   float M, L, O[4];
-  if (a.flat) {  // one split: all 16 waves fold straight into the output
+  if (a.flat) {
     if (grp == 0 && qq < nq) {
       fold_waves<16>(s_m, s_l, s_o, 0, qq, d0, M, L, O);
       float v[4];
@@ -399,10 +430,11 @@ __device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l
 // Four waves per SIMD (<= 128 VGPRs): enough resident waves to keep HBM
 // busy at batch 8 and beyond.
 //
-// NW = 4: one split per workgroup (grid.y = split).  NW = 16: one workgroup
-// covers all 2..4 splits of its tile, four waves per split, and folds them in
-// LDS (finish_grouped) -- no combine launch, same bits; or, with a.flat, one
-// split over every key with all 16 waves striding it.
+// NW = 4: one split per workgroup (grid.y = split), partials folded by the
+// combine kernel.  NW = 16: one workgroup runs all (at most four) splits of
+// its tile, four waves each, and folds them in LDS (finish_grouped) -- no
+// combine launch, same bits; or, with a.flat, one split over every key with
+// all 16 waves striding it.
 template <int MODE, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
     AttnArgs a) {
@@ -873,35 +905,38 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;
+  // bf16 tiles with at most four splits (or one flat split) run in one
+  // 16-wave workgroup; otherwise one 4-wave workgroup per split + combine
+  const bool single = dtype == SPECDEC_BF16 && (a.flat || a.max_splits <= 4);
+  a.parts = single ? 1 : a.max_splits;
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
-  if (a.max_splits > 1) {
+  if (a.parts > 1) {
     if (!workspace) return SPECDEC_EINVAL;
-    if (workspace_floats < units * a.max_splits * kPart) return SPECDEC_EINVAL;
+    if (workspace_floats < units * a.parts * kPart) return SPECDEC_EINVAL;
   }
   if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
-  dim3 grid((unsigned)units, (unsigned)a.max_splits), block(kAttnThreads);
   hipStream_t s = as_stream(stream);
   const bool bs16 = (block_size % 16) == 0;
-  if (dtype == SPECDEC_BF16 && (a.flat || (a.max_splits >= 2 && a.max_splits <= 4))) {
-    // every split of a tile in one 16-wave workgroup: no combine launch
-    dim3 g1((unsigned)units), b16(16 * kWave);
-    if (block_size == 16) attention_bf16_kernel<1, 16><<<g1, b16, 0, s>>>(a);
-    else if (bs16) attention_bf16_kernel<2, 16><<<g1, b16, 0, s>>>(a);
-    else attention_bf16_kernel<0, 16><<<g1, b16, 0, s>>>(a);
-    return launch_status();
-  }
-  if (dtype == SPECDEC_BF16) {
+  dim3 grid((unsigned)units, (unsigned)a.parts);
+  if (single) {
+    dim3 block(16 * kWave);
+    if (block_size == 16) attention_bf16_kernel<1, 16><<<grid, block, 0, s>>>(a);
+    else if (bs16) attention_bf16_kernel<2, 16><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<0, 16><<<grid, block, 0, s>>>(a);
+  } else if (dtype == SPECDEC_BF16) {
+    dim3 block(kAttnThreads);
     if (block_size == 16) attention_bf16_kernel<1, 4><<<grid, block, 0, s>>>(a);
     else if (bs16) attention_bf16_kernel<2, 4><<<grid, block, 0, s>>>(a);
     else attention_bf16_kernel<0, 4><<<grid, block, 0, s>>>(a);
   } else if (dtype == SPECDEC_F32) {
+    dim3 block(kAttnThreads);
     if (bs16) attention_f32_kernel<true><<<grid, block, 0, s>>>(a);
     else attention_f32_kernel<false><<<grid, block, 0, s>>>(a);
   } else {
     return SPECDEC_EINVAL;
   }
-  if (a.max_splits > 1)
-    attention_combine_kernel<<<dim3((unsigned)units), block, 0, s>>>(a, dtype);
+  if (a.parts > 1)
+    attention_combine_kernel<<<dim3((unsigned)units), dim3(kAttnThreads), 0, s>>>(a, dtype);
   return launch_status();
 }
 
