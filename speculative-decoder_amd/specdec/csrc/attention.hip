@@ -64,8 +64,7 @@ struct AttnArgs {
   int batch, width, H, Hkv, bs;
   float scale;
   int split, max_splits, n_qtiles;
-  // split partial slots per unit in the workspace (max_splits, or 1 when
-  // no combine runs)
+  // split partial slots per unit in the workspace (1 when no combine runs)
   int parts;
   // 16-wave launches only: one split over every key, wave w taking the
   // 64-token steps w, w+16, ... (results need not match other calls)
@@ -179,11 +178,10 @@ __device__ __forceinline__ void store_row4(const AttnArgs &a, const TileInfo &ti
   for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(v[i]);
 }
 
-// Combine the 4 waves of this workgroup.  With one split the normalised rows
-// are the output; otherwise the split partial (O / l, lse = m + log2 l) goes
-// to the workspace for the combine kernel.
-template <typename T>
-__device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
+// Fold of the 4 waves of a 256-thread workgroup through LDS: thread
+// (qq = tid / 16, d0 = 4 * (tid % 16)) receives (M, L, O) of query row qq,
+// dims d0 .. d0+3.  Ends with a barrier, so the LDS can be reused.
+__device__ __forceinline__ void fold_wg4(float m, float l, const f32x4 (&o)[4], float &M, float &L, float (&O)[4]) {
   __shared__ float s_m[4][kRows], s_l[4][kRows];
   __shared__ float s_o[4][kRows][kD + 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -197,12 +195,16 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) s_o[wave][c][16 * t + 4 * g + i] = o[t][i];
   __syncthreads();
+  fold_waves(s_m, s_l, s_o, 0, tid >> 4, (tid & 15) * 4, M, L, O);
+  __syncthreads();
+}
 
-  const int nq = min(kRows, ti.nrows - ti.qt * kRows);  // real query rows in this tile
-  const int qq = tid >> 4, d0 = (tid & 15) * 4;         // this thread: row qq, dims d0..d0+3
-  float M, L, O[4];
-  fold_waves(s_m, s_l, s_o, 0, qq, d0, M, L, O);
-  if (qq >= nq) return;
+// A split's folded (M, L, O) for one thread's row and dims: the output when
+// the tile has one split, else the split partial (O / l, lse = m + log2 l)
+// in workspace slot `slot` for the combine kernel.
+template <typename T>
+__device__ __forceinline__ void write_split(const AttnArgs &a, const TileInfo &ti, int slot, int qq, int d0, float M,
+                                            float L, const float (&O)[4]) {
   if (ti.nsplit == 1) {
     float v[4];
 #pragma unroll
@@ -210,14 +212,22 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
     store_row4<T>(a, ti, qq, d0, v);
     return;
   }
-  // split partial for the combine kernel: O / l [16][64] and lse [16]
-  float *ws = a.ws + ((int64_t)ti.unit * a.parts + blockIdx.y) * kPart;
+  float *ws = a.ws + ((int64_t)ti.unit * a.parts + slot) * kPart;
   const bool any = L > 0.0f;
   f32x4 v;
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = any ? O[i] / L : 0.0f;
   *reinterpret_cast<f32x4 *>(ws + qq * kD + d0) = v;
   if (d0 == 0) ws[kRows * kD + qq] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
+}
+
+// Combine the 4 waves of a one-split workgroup (grid.y = split).
+template <typename T>
+__device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
+  float M, L, O[4];
+  fold_wg4(m, l, o, M, L, O);
+  const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 4;
+  if (qq < min(kRows, ti.nrows - ti.qt * kRows)) write_split<T>(a, ti, blockIdx.y, qq, d0, M, L, O);
 }
 
 // Folds the split partials s0 .. s0+G-1 that lie below ns into the running
@@ -252,6 +262,18 @@ __device__ __forceinline__ void fold_splits(int s0, int ns, const float (&lse)[G
   }
 }
 
+// First level of the fold tree: up to four consecutive split partials
+// folded into the group's (O / l, lse).
+__device__ __forceinline__ void group_partial(int n, const float (&lse)[4], const f32x4 (&ov)[4], float &glse,
+                                              f32x4 &gov) {
+  float m4 = -INFINITY, d4 = 0.0f, n4[4] = {0.f, 0.f, 0.f, 0.f};
+  fold_splits(0, n, lse, ov, m4, d4, n4);
+  const bool any = d4 > 0.0f;
+  glse = any ? m4 + __builtin_amdgcn_logf(d4) : -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gov[i] = any ? n4[i] / d4 : 0.0f;
+}
+
 // Final combine of the split partials, one workgroup per (row, head, tile)
 // with more than one split.  The fold tree depends only on the key
 // positions: splits are folded in groups of four (4 consecutive 256-token
@@ -266,6 +288,8 @@ __device__ __forceinline__ void fold_splits(int s0, int ns, const float (&lse)[G
 __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArgs a, int dtype) {
   const int tid = threadIdx.x;
   const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  // rows past width * (H / Hkv) exist in no batch entry: nothing to load
+  if ((int)(blockIdx.x % a.n_qtiles) * kRows + qq >= a.width * (a.H / a.Hkv)) return;
   const float *ws0 = a.ws + (int64_t)blockIdx.x * a.parts * kPart;
   float lse[32];
   f32x4 ov[32];
@@ -302,12 +326,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
         l4[u] = lse[4 * y + u];
         v4[u] = ov[4 * y + u];
       }
-      float m4 = -INFINITY, d4 = 0.0f, n4[4] = {0.f, 0.f, 0.f, 0.f};
-      fold_splits(0, n_y, l4, v4, m4, d4, n4);
-      const bool any = d4 > 0.0f;
-      gl[y] = any ? m4 + __builtin_amdgcn_logf(d4) : -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) gv[y][i] = any ? n4[i] / d4 : 0.0f;
+      group_partial(n_y, l4, v4, gl[y], gv[y]);
     }
     fold_splits(s0 / 4, ngroups, gl, gv, Mx, den, num);
   }
@@ -475,7 +494,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   // the key loop takes them from LDS instead of the pool, so no pool store
   // has to complete before the first key load.  More than kStage of them
   // (a long prefill) take the plain path: append, fence, then read.
-  const int lo = (NW == 16) ? 0 : (int)blockIdx.y * a.split;
+  const int lo = (NW == 16) ? 0 : split_idx * a.split;
   const int hi = (NW == 16) ? ti.nsplit * a.split : lo + a.split;
   const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + a.meta[2 * a.batch + ti.b]);
   const int n_in = max(p1 - p0, 0);
@@ -583,13 +602,12 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
     __syncthreads();
   }
 
+  // element offset of the (block, head) tile holding token pos
+  auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
   f32x4 o[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
-
-  // element offset of the (block, head) tile holding token pos
-  auto tile_of = [&](int pos) -> int64_t { return ((int64_t)trow[pos / bs] * Hkv + ti.h) * tile_elems; };
 
   for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
     // tile offsets of the step's four 16-token groups (MODE != 0), uniform
@@ -908,8 +926,8 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   // bf16 tiles with at most four splits (or one flat split) run in one
   // 16-wave workgroup; otherwise one 4-wave workgroup per split + combine
   const bool single = dtype == SPECDEC_BF16 && (a.flat || a.max_splits <= 4);
-  a.parts = single ? 1 : a.max_splits;
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
+  a.parts = single ? 1 : a.max_splits;
   if (a.parts > 1) {
     if (!workspace) return SPECDEC_EINVAL;
     if (workspace_floats < units * a.parts * kPart) return SPECDEC_EINVAL;

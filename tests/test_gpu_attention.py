@@ -122,6 +122,39 @@ def test_verify_rows_equal_decode_rows_bitwise(dtype, L):
         assert torch.equal(out1[0, 0], out5[0, t]), t
 
 
+def test_batch8_verify_rows_equal_batch1_decode_rows_bitwise():
+    """At batch 8 and context ~4096 the kernel runs four splits per
+    workgroup (group partials, then the combine); decoding one row alone at
+    batch 1 runs one split per workgroup and folds the groups in the combine.
+    The fold tree is the same, so the bits are."""
+    d, h, hkv, bs, L, B = 64, 32, 32, 16, 4090, 8
+    g = torch.Generator().manual_seed(21)
+    cache = make_cache(1, hkv, d, B * ((L + 8) // bs + 2) + 8, bs, torch.bfloat16, 6)
+    ids = list(range(B))
+    for s in ids:
+        cache.add(s)
+    lengths = [L - 7 * b for b in range(B)]
+    step = cache.append(ids, [n + 5 for n in lengths])
+    cache.write(0, step, torch.randn(B, hkv, L + 5, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(B, hkv, L + 5, d, generator=g).to(torch.bfloat16).cuda())
+    q = torch.randn(B, 5, h * d, generator=g).to(torch.bfloat16).cuda()
+    for s, n in zip(ids, lengths):
+        cache.truncate(s, n)
+    step8 = cache.append(ids, [5] * B)
+    out8 = torch.zeros(B, 5, h * d, dtype=torch.bfloat16, device="cuda")
+    ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step8.meta, B, 5, h, hkv, d, bs,
+                        0.125, step8.max_total, out8, out8.stride(1))
+    for row in (0, 5):
+        for t in range(5):
+            cache.truncate(row, lengths[row] + t)
+            step1 = cache.append([row], [1])
+            out1 = torch.zeros(1, 1, h * d, dtype=torch.bfloat16, device="cuda")
+            q1 = q[row:row + 1, t:t + 1].contiguous()
+            ops.paged_attention(q1, q1.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step1.meta, 1, 1, h,
+                                hkv, d, bs, 0.125, step1.max_total, out1, out1.stride(1))
+            assert torch.equal(out1[0, 0], out8[row, t]), (row, t)
+
+
 def test_prefill_many_query_tiles():
     """A 200-token prefill (13 query tiles per head) against SDPA."""
     for got, want in run_case(2, [0, 17], 4, 2, 16, torch.float32, 200, seed=3, rollback=False):
