@@ -218,8 +218,8 @@ int specdec_attention_workspace(int32_t batch, int32_t width, int32_t n_heads,
                                 int64_t *floats);
 
 /* Split-KV size the attention kernel uses by default for a call shape
- * (tokens per workgroup; a fixed 256 whenever all queries of a kv head fit
- * one 16-row tile and the context is at most 32768, so that a query's
+ * (tokens per workgroup; a fixed 512 whenever all queries of a kv head fit
+ * one 16-row tile and the context is at most 65536, so that a query's
  * reduction order does not depend on how many tokens are verified with it). */
 int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
                             int32_t n_kv_heads, int32_t max_kv_len);

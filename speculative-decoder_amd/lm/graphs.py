@@ -30,9 +30,9 @@ from lm.forward import forward_core
 from lm.model import Llama
 from specdec import ops
 
-# Context buckets of 1024 keys: up to four 256-token splits, which the
+# Context buckets of 2048 keys: up to four 512-token splits, which the
 # attention kernel folds inside one workgroup (no combine launch).
-BUCKET = 1024
+BUCKET = 2048
 
 
 def enabled() -> bool:

@@ -89,15 +89,15 @@ def test_bf16_gqa_small_blocks(bs):
         assert (got - want).abs().max().item() < 2e-2
 
 
-@pytest.mark.parametrize("L", [300, 1000, 1020, 4090])
+@pytest.mark.parametrize("L", [300, 1000, 2044, 4090])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_verify_rows_equal_decode_rows_bitwise(dtype, L):
     """The same query at the same position gives identical bits whether it is
     verified among k+1 tokens or decoded alone: the reduction order depends
     only on key positions (the property the greedy identity relies on).  At
-    L = 1020 the verify call needs 5 splits (split kernel + combine kernel)
-    while the first decode calls need 4 (one 16-wave workgroup folding them
-    in LDS): both paths must give the same bits."""
+    L = 2044 the verify call needs 5 splits of 512 (split kernel + combine
+    kernel) while the first decode calls need 4 (one 16-wave workgroup
+    folding them in LDS): both paths must give the same bits."""
     d, h, hkv, bs = 64, 32, 32, 16
     g = torch.Generator().manual_seed(5)
     cache = make_cache(1, hkv, d, (L + 5) // bs + 8, bs, dtype, 1)

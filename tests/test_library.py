@@ -29,10 +29,10 @@ def test_attention_workspace_query_needs_no_gpu():
 
     lib = _lib.load()
     floats = ctypes.c_int64()
-    # B=1, T=5, 32/32 heads, d=64, 4101 keys: one tile per head, 17 splits of 256
+    # B=1, T=5, 32/32 heads, d=64, 4101 keys: one tile per head, 9 splits of 512
     assert lib.specdec_attention_workspace(1, 5, 32, 32, 64, 4101, 0, ctypes.byref(floats)) == 0
-    assert floats.value == 32 * 17 * 16 * 65
-    assert lib.specdec_attention_split(1, 5, 32, 32, 4101) == 256
+    assert floats.value == 32 * 9 * 16 * 65
+    assert lib.specdec_attention_split(1, 5, 32, 32, 4101) == 512
     assert lib.specdec_attention_workspace(1, 5, 32, 32, 128, 10, 0, ctypes.byref(floats)) == 3
 
 
