@@ -1,5 +1,5 @@
-// Elementwise layer glue of the Llama forward, fused so a layer is nine
-// launches: residual add + RMSNorm, and SiLU(gate) * up.
+// Elementwise layer glue of the Llama forward: residual add + RMSNorm, and
+// SiLU(gate) * up.
 //
 // Numerics follow transformers' Llama modules as lm/forward.py:56,64-65
 // calls them: the residual add rounds to the activation type, RMSNorm
@@ -60,18 +60,98 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(T *__restrict
   }
 }
 
+// ---- rows of 16-byte vectors -------------------------------------------
+// Element e of a 16-byte vector of T.
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+template <typename T> __device__ __forceinline__ float vec_elem(const u32x4 &v, int e);
+template <> __device__ __forceinline__ float vec_elem<float>(const u32x4 &v, int e) {
+  const unsigned u = v[e];  // (a vector element straight inside __builtin_bit_cast reads element 0)
+  return __builtin_bit_cast(float, u);
+}
+template <> __device__ __forceinline__ float vec_elem<__hip_bfloat16>(const u32x4 &v, int e) {
+  return __uint_as_float((e & 1) ? (v[e >> 1] & 0xFFFF0000u) : (v[e >> 1] << 16));
+}
+template <typename T> __device__ __forceinline__ void vec_set(u32x4 &v, int e, T x);
+template <> __device__ __forceinline__ void vec_set<float>(u32x4 &v, int e, float x) {
+  v[e] = __builtin_bit_cast(unsigned, x);
+}
+template <> __device__ __forceinline__ void vec_set<__hip_bfloat16>(u32x4 &v, int e, __hip_bfloat16 x) {
+  const unsigned b = __builtin_bit_cast(unsigned short, x), sh = 16 * (e & 1);
+  v[e >> 1] = (v[e >> 1] & ~(0xFFFFu << sh)) | (b << sh);
+}
+
+// One wave per row, the row as 16-byte vectors in registers (NV per lane):
+// the same arithmetic as add_rmsnorm_kernel, with the sum of squares
+// reduced across the wave (no LDS, no barrier) -- the decode-size case,
+// where a launch is a few microseconds of latency.  Needs dim a multiple
+// of 16 / sizeof(T) and 16-byte aligned rows.
+template <typename T, int NV>
+__global__ __launch_bounds__(kWave) void add_rmsnorm_wave_kernel(T *__restrict__ hidden, const T *__restrict__ delta,
+                                                                 const T *__restrict__ weight, T *__restrict__ out,
+                                                                 int64_t dim, float eps) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x, nvec = (int)(dim / E);
+  u32x4 *h = reinterpret_cast<u32x4 *>(hidden + row * dim);
+  const u32x4 *dl = delta ? reinterpret_cast<const u32x4 *>(delta + row * dim) : h;
+  const u32x4 *w = reinterpret_cast<const u32x4 *>(weight);
+  u32x4 *y = reinterpret_cast<u32x4 *>(out + row * dim);
+  u32x4 hv[NV], dv[NV], wv[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {  // every load first, indices clamped into the row
+    const int i = min(lane + kWave * k, nvec - 1);
+    hv[k] = h[i];
+    dv[k] = dl[i];
+    wv[k] = w[i];
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const bool in = lane + kWave * k < nvec;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float x = vec_elem<T>(hv[k], e);
+      if (delta) {
+        const T s = from_f32<T>(x + vec_elem<T>(dv[k], e));
+        vec_set<T>(hv[k], e, s);
+        x = to_f32(s);
+      }
+      ss += in ? x * x : 0.0f;
+    }
+    if (delta && in) h[lane + kWave * k] = hv[k];
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (lane + kWave * k >= nvec) continue;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      vec_set<T>(o, e, from_f32<T>(vec_elem<T>(wv[k], e) * to_f32(from_f32<T>(vec_elem<T>(hv[k], e) * inv))));
+    y[lane + kWave * k] = o;
+  }
+}
+
+// SiLU(gate) * up over 16-byte vectors: thread i of row r handles elements
+// 8i .. 8i+7 (bf16; 4 for fp32), one load of each operand.
 template <typename T>
-static void launch_add_rmsnorm(T *hidden, const T *delta, const T *weight, T *out, int64_t rows, int64_t dim,
-                               float eps, hipStream_t s) {
-  dim3 grid((unsigned)rows), block(kNormThreads);
-  if (dim <= 4 * kNormThreads)
-    add_rmsnorm_kernel<T, 4><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
-  else if (dim <= 8 * kNormThreads)
-    add_rmsnorm_kernel<T, 8><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
-  else if (dim <= 16 * kNormThreads)
-    add_rmsnorm_kernel<T, 16><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
-  else
-    add_rmsnorm_kernel<T, kNormPer><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+__global__ __launch_bounds__(256) void silu_mul_vec_kernel(const T *__restrict__ gu, T *__restrict__ out,
+                                                            int64_t inter) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t r = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= inter / E) return;
+  const u32x4 g = reinterpret_cast<const u32x4 *>(gu + r * 2 * inter)[i];
+  const u32x4 u = reinterpret_cast<const u32x4 *>(gu + r * 2 * inter + inter)[i];
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float x = vec_elem<T>(g, e);
+    const T a = from_f32<T>(x / (1.0f + expf(-x)));
+    vec_set<T>(o, e, from_f32<T>(to_f32(a) * vec_elem<T>(u, e)));
+  }
+  reinterpret_cast<u32x4 *>(out + r * inter)[i] = o;
 }
 
 template <typename T>
@@ -83,6 +163,32 @@ __global__ void silu_mul_kernel(const T *__restrict__ gu, T *__restrict__ out, i
     const T a = from_f32<T>(g / (1.0f + expf(-g)));
     out[i] = from_f32<T>(to_f32(a) * to_f32(gu[r * 2 * inter + inter + c]));
   }
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+template <typename T>
+static void launch_add_rmsnorm(T *hidden, const T *delta, const T *weight, T *out, int64_t rows, int64_t dim,
+                               float eps, hipStream_t s) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t nvec = dim / E;
+  if (dim % E == 0 && nvec <= 8 * kWave && aligned16(hidden) && aligned16(weight) && aligned16(out) &&
+      (!delta || aligned16(delta))) {
+    dim3 grid((unsigned)rows), block(kWave);
+    if (nvec <= 2 * kWave) add_rmsnorm_wave_kernel<T, 2><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+    else if (nvec <= 4 * kWave) add_rmsnorm_wave_kernel<T, 4><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+    else add_rmsnorm_wave_kernel<T, 8><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+    return;
+  }
+  dim3 grid((unsigned)rows), block(kNormThreads);
+  if (dim <= 4 * kNormThreads)
+    add_rmsnorm_kernel<T, 4><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else if (dim <= 8 * kNormThreads)
+    add_rmsnorm_kernel<T, 8><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else if (dim <= 16 * kNormThreads)
+    add_rmsnorm_kernel<T, 16><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
+  else
+    add_rmsnorm_kernel<T, kNormPer><<<grid, block, 0, s>>>(hidden, delta, weight, out, dim, eps);
 }
 
 }  // namespace specdec
@@ -113,9 +219,20 @@ SPECDEC_API int specdec_silu_mul(const void *gate_up, void *out, int dtype, int6
   if (rows < 0 || inter <= 0) return SPECDEC_EINVAL;
   if (rows == 0) return SPECDEC_OK;
   if (!gate_up || !out) return SPECDEC_EINVAL;
+  hipStream_t s = as_stream(stream);
+  const int E = (dtype == SPECDEC_BF16) ? 8 : 4;
+  if ((dtype == SPECDEC_BF16 || dtype == SPECDEC_F32) && inter % E == 0 && rows <= 65535 &&
+      aligned16(gate_up) && aligned16(out)) {
+    dim3 grid((unsigned)((inter / E + 255) / 256), (unsigned)rows), block(256);
+    if (dtype == SPECDEC_BF16)
+      silu_mul_vec_kernel<__hip_bfloat16><<<grid, block, 0, s>>>((const __hip_bfloat16 *)gate_up,
+                                                                 (__hip_bfloat16 *)out, inter);
+    else
+      silu_mul_vec_kernel<float><<<grid, block, 0, s>>>((const float *)gate_up, (float *)out, inter);
+    return launch_status();
+  }
   int64_t blocks = (rows * inter + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipStream_t s = as_stream(stream);
   if (dtype == SPECDEC_BF16) {
     silu_mul_kernel<__hip_bfloat16><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
         (const __hip_bfloat16 *)gate_up, (__hip_bfloat16 *)out, rows, inter);
