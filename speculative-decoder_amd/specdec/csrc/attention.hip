@@ -609,22 +609,28 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
 
-  for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
+  // K/V operands of one 64-token step
+  struct StepRegs {
+    u32x4 k[2][2][2];  // [chunk][half][kk]
+    u32x4 v[2][4];     // [chunk][dim tile]
+  };
+  // this lane's block ids for the step at c0 (lane j & 3: tokens c0 + 16j ..)
+  auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
+  // issue every K/V load of the step at c0; bjv holds its block ids
+  auto issue = [&](int c0, int bjv, StepRegs &r) {
     // tile offsets of the step's four 16-token groups (MODE != 0), uniform
     // across the wave; a lane picks between two of them with a select (a
     // dynamically indexed array would be placed in memory)
     int64_t tofs0 = 0, tofs1 = 0, tofs2 = 0, tofs3 = 0;
     if (MODE != 0) {
-      tofs0 = ((int64_t)__builtin_amdgcn_readlane(bj, 0) * Hkv + ti.h) * tile_elems;
-      tofs1 = ((int64_t)__builtin_amdgcn_readlane(bj, 1) * Hkv + ti.h) * tile_elems;
-      tofs2 = ((int64_t)__builtin_amdgcn_readlane(bj, 2) * Hkv + ti.h) * tile_elems;
-      tofs3 = ((int64_t)__builtin_amdgcn_readlane(bj, 3) * Hkv + ti.h) * tile_elems;
+      tofs0 = ((int64_t)__builtin_amdgcn_readlane(bjv, 0) * Hkv + ti.h) * tile_elems;
+      tofs1 = ((int64_t)__builtin_amdgcn_readlane(bjv, 1) * Hkv + ti.h) * tile_elems;
+      tofs2 = ((int64_t)__builtin_amdgcn_readlane(bjv, 2) * Hkv + ti.h) * tile_elems;
+      tofs3 = ((int64_t)__builtin_amdgcn_readlane(bjv, 3) * Hkv + ti.h) * tile_elems;
     }
     auto group_tile = [&](int ch, bool upper) -> int64_t {
       return ch == 0 ? (upper ? tofs1 : tofs0) : (upper ? tofs3 : tofs2);
     };
-    u32x4 kraw[2][2][2];  // [chunk][half][kk]
-    u32x4 vraw[2][4];     // [chunk][dim tile]
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       const int cs = c0 + 32 * ch;
@@ -633,23 +639,23 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
         const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
         const bool ok = (MODE == 0) ? tok < kv_len : (tok / bs) * bs < kv_len;
         const bool fresh = staged && tok >= p0 && tok < p1;  // appended by this call: from LDS
-        kraw[ch][hf][0] = kraw[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
+        r.k[ch][hf][0] = r.k[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
         if (ok && !fresh) {
           const int64_t to = (MODE != 0) ? group_tile(ch, (c >> 3) != 0) : tile_of(tok);
           const u16 *kb = kp + to + (int64_t)(tok % bs) * kD + 8 * g;
-          kraw[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
-          kraw[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
+          r.k[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
+          r.k[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
         }
       }
       const int vt = cs + 8 * g;  // first of this lane group's 8 tokens
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{0u, 0u, 0u, 0u};
+      for (int tt = 0; tt < 4; ++tt) r.v[ch][tt] = u32x4{0u, 0u, 0u, 0u};
       if (MODE != 0) {
         if ((vt / bs) * bs < kv_len) {
           const u16 *vb = vp + group_tile(ch, (g >> 1) != 0) + vt % bs;
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
-            vraw[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
+            r.v[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
         }
       } else {
         unsigned int w[4][4] = {};
@@ -663,13 +669,13 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
             w[tt][i >> 1] |= (unsigned)vb[(int64_t)(16 * tt + c) * bs] << (16 * (i & 1));
         }
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) vraw[ch][tt] = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
+        for (int tt = 0; tt < 4; ++tt) r.v[ch][tt] = u32x4{w[tt][0], w[tt][1], w[tt][2], w[tt][3]};
       }
     }
-    // next step's block ids, in flight during this step's arithmetic
-    if (MODE != 0 && c0 + wstride < s_hi)
-      bj = trow[min((c0 + wstride + 16 * (lane & 3)) / bs, last_blk)];
-    // keys appended by this call: K rows and V elements from LDS
+  };
+  // keys appended by this call: K rows and V elements from LDS, then the
+  // step's scores, online softmax and P V
+  auto compute = [&](int c0, StepRegs &r) {
     if (staged && c0 + 64 > p0 && c0 < p1) {
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
@@ -678,8 +684,8 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
         for (int hf = 0; hf < 2; ++hf) {
           const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
           if (tok >= p0 && tok < p1) {
-            kraw[ch][hf][0] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][8 * g]);
-            kraw[ch][hf][1] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][32 + 8 * g]);
+            r.k[ch][hf][0] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][8 * g]);
+            r.k[ch][hf][1] = *reinterpret_cast<const u32x4 *>(&s_nk[tok - p0][32 + 8 * g]);
           }
         }
         const int vt = cs + 8 * g;
@@ -690,25 +696,24 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
               const unsigned sh = 16 * (i & 1);
-              const unsigned wd = vraw[ch][tt][i >> 1];
-              vraw[ch][tt][i >> 1] = (wd & ~(0xFFFFu << sh)) | ((unsigned)s_nv[pos - p0][16 * tt + c] << sh);
+              const unsigned wd = r.v[ch][tt][i >> 1];
+              r.v[ch][tt][i >> 1] = (wd & ~(0xFFFFu << sh)) | ((unsigned)s_nv[pos - p0][16 * tt + c] << sh);
             }
           }
         }
       }
     }
-
     // scores of both chunks (S^T = K Q^T), in log2 units
     float sv[16];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][0]), qop[0], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kraw[ch][hf][1]), qop[1], s, 0, 0, 0);
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[ch][hf][0]), qop[0], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[ch][hf][1]), qop[1], sc, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = s[i] * c2;
+        for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = sc[i] * c2;
       }
     }
     // keys past a query's position (or past kv_len) only occur in chunks
@@ -730,8 +735,16 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
       for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[8 * ch + j];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
-        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vraw[ch][tt]), pop, o[tt], 0, 0, 0);
+        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.v[ch][tt]), pop, o[tt], 0, 0, 0);
     }
+  };
+
+  for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
+    StepRegs r;
+    issue(c0, bj, r);
+    // next step's block ids, in flight during this step's arithmetic
+    if (MODE != 0 && c0 + wstride < s_hi) bj = step_blocks(c0 + wstride);
+    compute(c0, r);
   }
   if (NW == 16) finish_grouped<__hip_bfloat16>(a, ti, m, l, o);
   else finish<__hip_bfloat16>(a, ti, m, l, o);
