@@ -333,7 +333,7 @@ def time_fn(fn, iters=100, graph=False):
     return start.elapsed_time(end) * 1000 / iters
 
 
-def bench_kernels():
+def bench_kernels(attention_grid=True):
     from make_golden import planted_rows
     from specdec import ops
 
@@ -372,6 +372,21 @@ def bench_kernels():
     us_app = time_fn(lambda: ops.rope_append(qkv, 32, 32, 64, cos, sin, step.meta, 1, 5, cache.table_tensor, BLOCK,
                                              cache.k[0], cache.v[0]), graph=True)
     res["append_b1_t5"] = {"us": us_app, "bytes": 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2}
+    # config 2': one round's rollback of 8 rows (a rejected tail each) and the
+    # regrowth for the next verify: the block plan the cache launches
+    ids = list(range(8))
+    cache8, _, _, _ = setup_attention(8, 1005)  # 1010 cached: the rollback frees a block, the regrowth takes one
+    lens = [cache8.length(s) for s in ids]
+
+    def rollback_and_grow():
+        for s, n in zip(ids, lens):
+            cache8.truncate(s, n - 5 + 1)
+        cache8.append(ids, [4] * 8)
+
+    res["rollback_grow_b8"] = {"us_host_inclusive": time_fn(rollback_and_grow, iters=50)}
+    del cache8
+    if not attention_grid:
+        return res
     # attention over the config-2 grid
     for b in (1, 4, 8):
         for L in (512, 1024, 2048, 4096):
@@ -438,7 +453,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "small", "copy"], default="all",
+                    help="small: the kernels of configs 1-3 without the attention grid (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--batch", type=int, default=8, help="batch of the --only attention run")
@@ -458,8 +474,8 @@ def main():
         r = time_attention(args.batch, 4096, iters=max(args.steps, 1) * 100, rotate=not args.one_pool)
         print(json.dumps({f"attention_b{args.batch}_L4096": r}))
         return
-    if args.only == "kernels":
-        print(json.dumps(bench_kernels()))
+    if args.only in ("kernels", "small"):
+        print(json.dumps(bench_kernels(attention_grid=args.only == "kernels")))
         return
     if args.only == "copy":
         # reference copy of a known size for scaling the FETCH_SIZE / WRITE_SIZE counters
