@@ -233,8 +233,8 @@ __device__ void finish(const AttnArgs &a, const TileInfo &ti, float m, float l, 
 // Folds the split partials s0 .. s0+G-1 that lie below ns into the running
 // (Mx, den, num): the group's largest lse rescales what is accumulated, then
 // each split adds w = 2^(lse - Mx) times its O / l row, in split order.
-// Both the combine kernel (G = 32) and the single-workgroup path below
-// (G = 4, at most 4 splits) use it; splits past ns take no part, so for a
+// The combine kernel (G = 4 per group, then G = 8 over groups) and the
+// single-workgroup path below (G = 4, at most 4 splits) use it; splits past ns take no part, so for a
 // query with at most 4 splits both run the same operations in the same
 // order and the result does not depend on which of them ran.
 template <int G>
@@ -282,10 +282,14 @@ __device__ __forceinline__ void group_partial(int n, const float (&lse)[4], cons
 // with at most four splits is run by one 16-wave workgroup that folds its
 // single group the same way, so a query gets the same bits on either path;
 // splits or groups holding none of a query's keys take no part.  Thread
-// (q, 4 dims) does the folding; the first 32 splits' loads are issued
-// before the row metadata arrives (their addresses depend only on the
-// workgroup).
+// (q, 4 dims) does the folding.  The first NG groups' loads (4 * NG splits,
+// NG = min(8, groups of the longest tile)) are issued before the row
+// metadata arrives, since their addresses depend only on the workgroup;
+// groups NG .. 7 of the first step lie past every tile's last split and are
+// skipped by the fold as they would be with all eight loaded.
+template <int NG>
 __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArgs a, int dtype) {
+  constexpr int NL = 4 * NG;
   const int tid = threadIdx.x;
   const int qq = tid >> 4, d0 = (tid & 15) * 4;
   // rows past width * (H / Hkv) exist in no batch entry: nothing to load
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
   float lse[32];
   f32x4 ov[32];
 #pragma unroll
-  for (int u = 0; u < 32; ++u) {
+  for (int u = 0; u < NL; ++u) {
     const float *p = ws0 + (int64_t)min(u, a.parts - 1) * kPart;
     lse[u] = p[kRows * kD + qq];
     ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
@@ -306,9 +310,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
   const int ns = ti.nsplit, ngroups = (ns + 3) / 4;
   float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < ns; s0 += 32) {
-    if (s0 > 0) {
+    if (s0 > 0) {  // only when NG == 8
 #pragma unroll
-      for (int u = 0; u < 32; ++u) {
+      for (int u = 0; u < NL; ++u) {
         const float *p = ws0 + (int64_t)min(s0 + u, ns - 1) * kPart;
         lse[u] = p[kRows * kD + qq];
         ov[u] = *reinterpret_cast<const f32x4 *>(p + qq * kD + d0);
@@ -318,6 +322,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
     f32x4 gv[8];
 #pragma unroll
     for (int y = 0; y < 8; ++y) {
+      if (y >= NG) {  // past ngroups: fold_splits skips it
+        gl[y] = -INFINITY;
+        gv[y] = f32x4{0.f, 0.f, 0.f, 0.f};
+        continue;
+      }
       const int n_y = min(max(ns - (s0 + 4 * y), 0), 4);
       float l4[4];
       f32x4 v4[4];
@@ -968,8 +977,19 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   } else {
     return SPECDEC_EINVAL;
   }
-  if (a.parts > 1)
-    attention_combine_kernel<<<dim3((unsigned)units), dim3(kAttnThreads), 0, s>>>(a, dtype);
+  if (a.parts > 1) {
+    dim3 cg((unsigned)units), cb(kAttnThreads);
+    switch (min((a.parts + 3) / 4, 8)) {
+      case 1: attention_combine_kernel<1><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 2: attention_combine_kernel<2><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 3: attention_combine_kernel<3><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 4: attention_combine_kernel<4><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 5: attention_combine_kernel<5><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 6: attention_combine_kernel<6><<<cg, cb, 0, s>>>(a, dtype); break;
+      case 7: attention_combine_kernel<7><<<cg, cb, 0, s>>>(a, dtype); break;
+      default: attention_combine_kernel<8><<<cg, cb, 0, s>>>(a, dtype); break;
+    }
+  }
   return launch_status();
 }
 
