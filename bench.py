@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the B=8, context-4096 verify attention (both
 # kernels): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention`,
 # each scaled by what the counter reads for a copy of known size.
-ATTN_B8_TRAFFIC = 277_417_103
+ATTN_B8_TRAFFIC = 277_081_050
 V = 49152
 PROMPT = 256
 NEW_TOKENS = 128

@@ -122,12 +122,13 @@ def test_verify_rows_equal_decode_rows_bitwise(dtype, L):
         assert torch.equal(out1[0, 0], out5[0, t]), t
 
 
-def test_batch8_verify_rows_equal_batch1_decode_rows_bitwise():
-    """At batch 8 and context ~4096 the kernel runs four splits per
-    workgroup (group partials, then the combine); decoding one row alone at
-    batch 1 runs one split per workgroup and folds the groups in the combine.
-    The fold tree is the same, so the bits are."""
-    d, h, hkv, bs, L, B = 64, 32, 32, 16, 4090, 8
+@pytest.mark.parametrize("L", [4090, 4100])
+def test_batch8_verify_rows_equal_batch1_decode_rows_bitwise(L):
+    """Batch 8 against one row decoded alone at batch 1, both with split
+    partials folded by the combine kernel (L = 4100: eight full splits and
+    a short ninth).  The fold tree depends only on key positions, so the
+    bits are the same."""
+    d, h, hkv, bs, B = 64, 32, 32, 16, 8
     g = torch.Generator().manual_seed(21)
     cache = make_cache(1, hkv, d, B * ((L + 8) // bs + 2) + 8, bs, torch.bfloat16, 6)
     ids = list(range(B))
