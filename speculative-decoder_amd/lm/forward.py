@@ -104,9 +104,16 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
 
 
 def logits(model, hidden: torch.Tensor) -> torch.Tensor:
-    """The output projection in at least fp32: in bf16 near-tied candidates
-    round to the same logit and argmax would break the tie by whichever
-    rounding a (k+1)-token verify and a 1-token decode produced."""
+    """The output projection with fp32 accumulation and fp32 logits: in bf16
+    near-tied candidates round to the same logit and argmax would break the
+    tie by whichever rounding a (k+1)-token verify and a 1-token decode
+    produced.  The reference multiplies by an fp32 copy of the head
+    (lm/forward.py:71-84); bf16 weights are read here as stored, half the
+    bytes, and since the product of two bf16 values is exact in fp32 the
+    arithmetic is the fp32 head's up to the GEMM's summation order."""
     llama = as_llama(model)
-    wide = llama.head_wide
-    return F.linear(hidden.to(wide.dtype), wide)
+    w = llama.head_wide
+    if w.dtype not in (torch.bfloat16, torch.float16):
+        return F.linear(hidden.to(w.dtype), w)
+    flat = hidden.reshape(-1, hidden.shape[-1]).to(w.dtype)
+    return torch.mm(flat, w.t(), out_dtype=torch.float32).view(*hidden.shape[:-1], w.shape[0])

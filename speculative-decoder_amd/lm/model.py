@@ -121,7 +121,10 @@ class Llama:
     layers: list[Layer]
     norm: torch.Tensor
     lm_head: torch.Tensor
-    head_wide: torch.Tensor  # lm_head in at least fp32, made once
+    # lm_head as the output projection reads it: bf16/fp16 weights on the GPU
+    # as stored (the GEMM accumulates in and writes fp32), else an fp32 (or
+    # wider) copy made once
+    head_wide: torch.Tensor
     rope_cos: torch.Tensor = field(repr=False)
     rope_sin: torch.Tensor = field(repr=False)
 
@@ -161,7 +164,10 @@ class Llama:
             layers.append(Layer(get(p + "input_layernorm.weight"), wqkv, get(p + "self_attn.o_proj.weight"),
                                 get(p + "post_attention_layernorm.weight"), wgu, get(p + "mlp.down_proj.weight")))
         head = embed if shape.tie_word_embeddings else get("lm_head.weight")
-        wide = head.to(torch.promote_types(head.dtype, torch.float32)).contiguous()
+        if head.is_cuda and head.dtype in (torch.bfloat16, torch.float16):
+            wide = head
+        else:
+            wide = head.to(torch.promote_types(head.dtype, torch.float32)).contiguous()
         cos, sin = rope_tables(shape, shape.max_position_embeddings)
         return cls(shape, embed, layers, get("model.norm.weight"), head, wide, cos.to(embed.device),
                    sin.to(embed.device))
