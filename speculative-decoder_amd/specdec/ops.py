@@ -41,6 +41,22 @@ def gpu(t: torch.Tensor, name: str = "tensor") -> torch.Tensor:
     return t
 
 
+def _on(dev: torch.device, t: torch.Tensor, name: str, dtype: torch.dtype | None = None,
+        contiguous: bool = False, numel: int | None = None) -> torch.Tensor:
+    """Host-side check of a tensor whose pointer goes to a kernel: on `dev`,
+    of `dtype`, contiguous, holding `numel` elements, as asked.  A pointer to
+    host memory or a short buffer would otherwise become a GPU memory fault."""
+    if t.device != dev:
+        raise RuntimeError(f"{name} must be on {dev} (got {t.device}); the hot path has no CPU fallback")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name} must hold {numel} elements (got {t.numel()})")
+    return t
+
+
 def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -65,6 +81,7 @@ def probabilities(logits: torch.Tensor, temperature: float, out: torch.Tensor | 
     fresh = out is None
     if fresh:
         out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    _on(x.device, out, "out")
     o2 = out if out.dim() == 2 else out.view(rows, v)
     if o2.dtype != torch.float32 or tuple(o2.shape) != (rows, v) or o2.stride(-1) != 1:
         raise ValueError("out must be fp32 [rows, V] with unit inner stride")
@@ -72,8 +89,9 @@ def probabilities(logits: torch.Tensor, temperature: float, out: torch.Tensor | 
     if index_out is not None:
         if temperature != 0.0:
             raise ValueError("index_out is defined at temperature 0 only")
-        if index_out.dtype != torch.int64 or index_out.numel() != rows:
-            raise ValueError("index_out must hold one int64 per row")
+        _on(x.device, index_out, "index_out", torch.int64, numel=rows)
+        if index_out.dim() > 1 and not index_out.is_contiguous():
+            raise ValueError("index_out must be a vector or contiguous")
         idx_ptr, idx_stride = index_out.data_ptr(), (index_out.stride(0) if index_out.dim() else 1)
     st = lib().specdec_probabilities(x.data_ptr(), dtype_code(x), rows, v, x.stride(0), float(temperature),
                                      o2.data_ptr(), o2.stride(0), idx_ptr, idx_stride, stream())
@@ -87,11 +105,25 @@ def _rows3(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _accept_inputs(p, q, draft, u_accept) -> tuple[int, int]:
+    """Shapes and devices of the accept inputs: p [B, k+1, V], q [B, k, V] of
+    p's dtype, draft int64 [B, k] and u_accept [B, k] (p's dtype), contiguous."""
+    b, k = draft.shape
+    if p.dim() != 3 or q.dim() != 3 or tuple(p.shape[:2]) != (b, k + 1) or tuple(q.shape) != (b, k, p.shape[2]):
+        raise ValueError(f"p must be [B, k+1, V] and q [B, k, V] for draft [B, k] = [{b}, {k}] "
+                         f"(got p {tuple(p.shape)}, q {tuple(q.shape)})")
+    _on(p.device, q, "q", p.dtype)
+    _on(p.device, draft, "draft", torch.int64, True)
+    _on(p.device, u_accept, "u_accept", p.dtype, True, b * k)
+    return b, k
+
+
 def accept_reject(p, q, draft, u_accept, u_residual) -> torch.Tensor:
     """Fused accept + residual + inverse CDF; returns int64 [3, B] on the GPU:
     n_accepted, next_token, zero-q flag."""
     p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
-    b, k = draft.shape
+    b, k = _accept_inputs(p, q, draft, u_accept)
+    _on(p.device, u_residual, "u_residual", p.dtype, True, b)
     out = torch.empty(3, b, dtype=torch.int64, device=p.device)
     st = lib().specdec_accept_reject(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
                                      q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(),
@@ -103,7 +135,7 @@ def accept_reject(p, q, draft, u_accept, u_residual) -> torch.Tensor:
 def accept_count(p, q, draft, u_accept) -> torch.Tensor:
     """Accept stage alone; int64 [2, B]: n_accepted, zero-q flag."""
     p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
-    b, k = draft.shape
+    b, k = _accept_inputs(p, q, draft, u_accept)
     out = torch.empty(2, b, dtype=torch.int64, device=p.device)
     st = lib().specdec_accept_count(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
                                     q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(), b, k,
@@ -117,6 +149,7 @@ def sample_inverse_cdf(probs: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     if probs.stride(-1) != 1:
         probs = probs.contiguous()
     b, v = probs.shape
+    _on(probs.device, u, "u", probs.dtype, True, b)
     out = torch.empty(b, dtype=torch.int64, device=probs.device)
     st = lib().specdec_sample_inverse_cdf(probs.data_ptr(), dtype_code(probs), b, v, probs.stride(0),
                                           u.data_ptr(), out.data_ptr(), stream())
@@ -136,7 +169,10 @@ def one_hot(ids: torch.Tensor, vocab: int) -> torch.Tensor:
 def ngram_lookup(history: torch.Tensor, lengths: torch.Tensor, k: int, max_n: int):
     """history int32 [B, cap], lengths int32 [B] -> (draft int64 [B, k], match int32 [B, 2])."""
     gpu(history, "history")
+    if history.dtype != torch.int32 or history.dim() != 2 or history.stride(1) != 1:
+        raise ValueError("history must be int32 [B, capacity] with unit inner stride")
     b = history.shape[0]
+    _on(history.device, lengths, "lengths", torch.int32, True, b)
     draft = torch.empty(b, k, dtype=torch.int64, device=history.device)
     match = torch.empty(b, 2, dtype=torch.int32, device=history.device)
     st = lib().specdec_ngram_lookup(history.data_ptr(), history.stride(0), lengths.data_ptr(), b, k, max_n,
@@ -146,7 +182,32 @@ def ngram_lookup(history: torch.Tensor, lengths: torch.Tensor, k: int, max_n: in
 
 
 # ------------------------------------------------------------------- cache --
+def _tables(tables: torch.Tensor) -> torch.Tensor:
+    gpu(tables, "tables")
+    if tables.dtype != torch.int32 or tables.dim() != 2 or tables.stride(1) != 1:
+        raise ValueError("block tables must be int32 [rows, capacity] with unit inner stride")
+    return tables
+
+
+def _meta(dev: torch.device, meta: torch.Tensor, batch: int) -> torch.Tensor:
+    """Per-call row metadata: int32 [3, batch] (table row, cached length, new tokens)."""
+    return _on(dev, meta, "meta", torch.int32, True, 3 * batch)
+
+
+def _stack_and_marks(free_stack: torch.Tensor, used: torch.Tensor) -> None:
+    _on(free_stack.device, free_stack, "free_stack", torch.int32, True)
+    _on(free_stack.device, used, "used", torch.uint8, True)
+    if used.numel() < free_stack.numel():
+        raise ValueError("used needs a mark per block")
+
+
 def block_plan(tables, free_stack, used, top: int, entries, n_push: int, n_pop: int, popped=None) -> None:
+    dev = gpu(tables, "tables").device
+    _tables(tables)
+    _stack_and_marks(free_stack, used)
+    _on(dev, entries, "entries", torch.int32, True)
+    if popped is not None:
+        _on(dev, popped, "popped", torch.int32, True)
     st = lib().specdec_block_plan(tables.data_ptr(), tables.stride(0), free_stack.data_ptr(), used.data_ptr(),
                                   free_stack.numel(), top, entries.data_ptr(), n_push, n_pop, ptr(popped),
                                   stream())
@@ -154,12 +215,18 @@ def block_plan(tables, free_stack, used, top: int, entries, n_push: int, n_pop: 
 
 
 def block_free_checked(free_stack, used, top: int, block: int, status) -> None:
+    dev = gpu(free_stack, "free_stack").device
+    _stack_and_marks(free_stack, used)
+    _on(dev, status, "status", torch.int32)
     st = lib().specdec_block_free_checked(free_stack.data_ptr(), used.data_ptr(), free_stack.numel(), top,
                                           block, status.data_ptr(), stream())
     _check(st, "block_free_checked")
 
 
 def block_slots(row: torch.Tensor, start: int, stop: int, block_size: int) -> torch.Tensor:
+    gpu(row, "row")
+    if row.dtype != torch.int32 or (stop > start and row.numel() * block_size < stop):
+        raise ValueError("row must be int32 holding a block for every position below stop")
     out = torch.empty(max(stop - start, 0), dtype=torch.int64, device=row.device)
     st = lib().specdec_block_slots(row.data_ptr(), start, stop, block_size, out.data_ptr(), stream())
     _check(st, "block_slots")
@@ -168,7 +235,9 @@ def block_slots(row: torch.Tensor, start: int, stop: int, block_size: int) -> to
 
 def slot_map(tables, meta, batch: int, block_size: int, width: int, read_width: int, write_offsets,
              n_write: int):
-    dev = tables.device
+    dev = _tables(tables).device
+    _meta(dev, meta, batch)
+    _on(dev, write_offsets, "write_offsets", torch.int32, True, batch)
     write = torch.empty(n_write, dtype=torch.int64, device=dev)
     write_index = torch.empty(n_write, dtype=torch.int64, device=dev)
     read = torch.empty(batch, read_width, dtype=torch.int64, device=dev)
@@ -181,6 +250,8 @@ def slot_map(tables, meta, batch: int, block_size: int, width: int, read_width: 
 
 def rope_append(qkv, n_heads, n_kv_heads, head_dim, cos, sin, meta, batch, width, tables, block_size,
                 k_pool, v_pool) -> None:
+    dev = gpu(qkv, "qkv").device
+    _qkv_side(dev, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool)
     st = lib().specdec_rope_append(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), n_heads, n_kv_heads, head_dim,
                                    cos.data_ptr(), sin.data_ptr(), cos.shape[0], meta.data_ptr(), batch, width,
                                    tables.data_ptr(), tables.stride(0), block_size, k_pool.data_ptr(),
@@ -189,7 +260,13 @@ def rope_append(qkv, n_heads, n_kv_heads, head_dim, cos, sin, meta, batch, width
 
 
 def kv_write(k, v, meta, batch, width, tables, block_size, k_pool, v_pool) -> None:
-    k, v = k.contiguous(), v.contiguous()
+    k, v = gpu(k, "k").contiguous(), v.contiguous()
+    dev = k.device
+    _on(dev, v, "v", k.dtype, numel=k.numel())
+    _meta(dev, meta, batch)
+    _tables(tables)
+    _on(dev, k_pool, "k_pool", k.dtype, True)
+    _on(dev, v_pool, "v_pool", k.dtype, True)
     st = lib().specdec_kv_write(k.data_ptr(), v.data_ptr(), dtype_code(k), k.shape[1], k.shape[3], meta.data_ptr(),
                                 batch, width, tables.data_ptr(), tables.stride(0), block_size, k_pool.data_ptr(),
                                 v_pool.data_ptr(), stream())
@@ -197,6 +274,10 @@ def kv_write(k, v, meta, batch, width, tables, block_size, k_pool, v_pool) -> No
 
 
 def kv_gather(k_pool, v_pool, meta, batch, tables, block_size, read_width):
+    dev = gpu(k_pool, "k_pool").device
+    _on(dev, v_pool, "v_pool", k_pool.dtype, True)
+    _meta(dev, meta, batch)
+    _tables(tables)
     n_kv, d = k_pool.shape[1], k_pool.shape[3]
     k_out = torch.empty(batch, n_kv, read_width, d, dtype=k_pool.dtype, device=k_pool.device)
     v_out = torch.empty_like(k_out)
@@ -213,6 +294,12 @@ def add_rmsnorm(hidden: torch.Tensor, delta: torch.Tensor | None, weight: torch.
     """hidden += delta (if given), out = RMSNorm(hidden) * weight; rows are the
     leading dims.  hidden and out must be contiguous."""
     dim = hidden.shape[-1]
+    dev = gpu(hidden, "hidden").device
+    _on(dev, hidden, "hidden", contiguous=True)
+    _on(dev, out, "out", hidden.dtype, True, hidden.numel())
+    _on(dev, weight, "weight", hidden.dtype, True, dim)
+    if delta is not None:
+        _on(dev, delta, "delta", hidden.dtype, True, hidden.numel())
     st = lib().specdec_add_rmsnorm(hidden.data_ptr(), ptr(delta), weight.data_ptr(), out.data_ptr(),
                                    dtype_code(hidden), hidden.numel() // dim, dim, float(eps), stream())
     _check(st, "add_rmsnorm")
@@ -221,6 +308,9 @@ def add_rmsnorm(hidden: torch.Tensor, delta: torch.Tensor | None, weight: torch.
 
 def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     inter = gate_up.shape[-1] // 2
+    dev = gpu(gate_up, "gate_up").device
+    _on(dev, gate_up, "gate_up", contiguous=True)
+    _on(dev, out, "out", gate_up.dtype, True, gate_up.numel() // 2)
     st = lib().specdec_silu_mul(gate_up.data_ptr(), out.data_ptr(), dtype_code(gate_up), gate_up.numel() // (2 * inter),
                                 inter, stream())
     _check(st, "silu_mul")
@@ -275,9 +365,27 @@ def latency_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_kv_
     return -1 if units < 64 else 0
 
 
+def _qkv_side(dev, x, cos, sin, meta, batch, width, tables, k_pool, v_pool, out=None) -> None:
+    """Devices and dtypes of the pointer arguments an attention or append
+    launch shares: pools of the activations' dtype, fp32 RoPE tables, int32
+    metadata and block tables; `out` of the activations' dtype."""
+    if cos is not None:
+        _on(dev, cos, "cos", torch.float32, True)
+        _on(dev, sin, "sin", torch.float32, True, cos.numel())
+    _meta(dev, meta, batch)
+    _tables(tables)
+    _on(dev, k_pool, "k_pool", x.dtype, True)
+    _on(dev, v_pool, "v_pool", x.dtype, True, k_pool.numel())
+    if out is not None:
+        _on(dev, out, "out", x.dtype)
+    if x.stride(-1) != 1 or (batch > 0 and width > 0 and x.numel() == 0):
+        raise ValueError("activations need unit inner stride")
+
+
 def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
                     block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None,
                     split_tokens: int = 0):
+    _qkv_side(gpu(q, "q").device, q, None, None, meta, batch, width, tables, k_pool, v_pool, out)
     ws = workspace or workspace_for(q.device)
     ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
     st = lib().specdec_paged_attention(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
@@ -294,6 +402,7 @@ def rope_paged_attention(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, wid
                          workspace: AttentionWorkspace | None = None, split_tokens: int = 0):
     """RoPE + paged append + verify attention in one launch (plus the split
     combine when needed).  qkv [B, T, (H + 2 Hkv) d] holds unrotated q/k/v."""
+    _qkv_side(gpu(qkv, "qkv").device, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool, out)
     ws = workspace or workspace_for(qkv.device)
     ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
     st = lib().specdec_rope_paged_attention(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), cos.data_ptr(),

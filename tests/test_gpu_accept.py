@@ -240,3 +240,31 @@ def test_custom_residual_is_used():
     want = oa.accept_reject(p, q, draft, u_accept=ua, u_residual=ur, residual=argmax_of_residual)
     assert got.n_accepted.tolist() == want.n_accepted.tolist() == [0] * 64
     assert got.next_token.tolist() == want.next_token.tolist() == [0] * 64
+
+
+def test_wrappers_reject_host_buffers_next_to_device_ones():
+    """A host tensor among device inputs (or a short or mistyped one) raises
+    on the host; nothing is launched with a host pointer."""
+    from specdec import ops
+
+    v = 64
+    p = torch.rand(2, 5, v, device="cuda")
+    q = torch.rand(2, 4, v, device="cuda")
+    draft = torch.zeros(2, 4, dtype=torch.int64, device="cuda")
+    ua = torch.rand(2, 4, device="cuda")
+    with pytest.raises(RuntimeError, match="must be on"):
+        ops.accept_reject(p, q, draft, ua, torch.rand(2))
+    with pytest.raises(RuntimeError, match="must be on"):
+        ops.accept_reject(p, q, draft.cpu(), ua, torch.rand(2, device="cuda"))
+    with pytest.raises(ValueError, match="4 elements|8 elements"):
+        ops.accept_count(p, q, draft, ua[:1])
+    with pytest.raises(TypeError):
+        ops.accept_count(p, q, draft.int(), ua)
+    with pytest.raises(ValueError):
+        ops.accept_count(p, q[:, :3], draft, ua)
+    with pytest.raises(RuntimeError, match="must be on"):
+        ops.probabilities(torch.randn(3, v, device="cuda"), 1.0, out=torch.empty(3, v))
+    with pytest.raises(RuntimeError, match="must be on"):
+        ops.ngram_lookup(torch.zeros(2, 8, dtype=torch.int32, device="cuda"), torch.full((2,), 8, dtype=torch.int32),
+                         4, 3)
+    torch.cuda.synchronize()
