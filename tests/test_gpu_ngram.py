@@ -76,3 +76,41 @@ def test_drafter_incremental_history_matches_full_lookup():
 def test_empty_context_raises():
     with pytest.raises(IndexError):
         lookup([], 3, 3)
+
+
+def _unique_row(length, first=100):
+    return list(range(first, first + length))
+
+
+def test_long_histories_across_lds_tiles():
+    """Histories longer than one 8192-position tile: the scan walks tiles from
+    the end and may stop only once the longest n has matched.  Cases: the
+    only 3-gram match in the earliest tile, a more recent 2-gram that must
+    not win over it, 3-grams whose aligned position sits on either side of a
+    tile boundary, and lengths at the edge of one tile."""
+    rows = []
+    r = _unique_row(20000)
+    r[-3:] = [1, 2, 3]
+    r[10:13] = [1, 2, 3]
+    rows.append(r)
+    r = list(rows[0])
+    r[15000:15002] = [2, 3]
+    rows.append(r)
+    for shift in (0, 1, 2, 3):
+        r = _unique_row(20000)
+        r[-3:] = [1, 2, 3]
+        lo0 = 20000 - 8193  # first position of the last tile scanned first
+        e = lo0 - shift
+        r[e - 2: e + 1] = [1, 2, 3]
+        rows.append(r)
+    for length in (8192, 8193, 8194, 8195, 16387):
+        r = _unique_row(length)
+        r[-1] = r[0]  # a single 1-gram match at the very start
+        rows.append(r)
+        r = _unique_row(length)  # no match at all: the fallback
+        rows.append(r)
+    for k in (1, 4):
+        got, match = lookup_batch(rows, k, 3)
+        for row, g, m in zip(rows, got, match):
+            want, start, n = on.lookup_match(row, k, 3)
+            assert g == want and tuple(m) == (start, n), (len(row), start, n, tuple(m))
