@@ -19,6 +19,8 @@
 
 namespace specdec {
 
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
 constexpr int kAcceptThreads = 1024;
 constexpr int kSoftmaxThreads = 1024;
 
@@ -246,6 +248,32 @@ constexpr int kChunk = kChunkTiles * kAcceptThreads * kCdfPerThread;  // 16384
 constexpr int kRun = kChunk / kAcceptThreads;                          // 16 per thread
 __device__ __forceinline__ int lds_pad(int k) { return k + (k >> 5); }
 
+// A row read through a raw buffer descriptor of `elems` fp32 elements:
+// loads past its end return 0 (the hardware range check on the vector
+// offset), so the register-resident kernels load a whole row with no clamp,
+// no select and no branch between the loads.  Word 3 is the gfx9-family
+// descriptor format for untyped dword access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const float *row, unsigned elems) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), 0, (int)(elems * 4u), 0x00020000);
+}
+
+// Elements 4*tid .. 4*tid+3 of tile j of a row (the layout of vals[j][e]):
+// one 16-byte load when the row length is a multiple of 4 (a load then never
+// straddles the row's end), else four 4-byte loads.
+template <bool VEC4>
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rb, int j, int tid, float (&out)[kCdfPerThread]) {
+  const unsigned off = (unsigned)(j * kAcceptThreads * kCdfPerThread + kCdfPerThread * tid) * 4u;
+  if (VEC4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+#pragma unroll
+    for (int e = 0; e < kCdfPerThread; ++e) out[e] = __builtin_bit_cast(float, (unsigned)v[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kCdfPerThread; ++e)
+      out[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off + 4u * e, 0, 0));
+  }
+}
+
 __device__ __forceinline__ int64_t inverse_cdf_regs(const float (&vals)[kRegTiles][kCdfPerThread], int64_t vocab, float u,
                                     double *scratch, float *lds) {
   __shared__ double s_total;
@@ -338,6 +366,7 @@ __device__ __forceinline__ void accept_stage_wave(const T *p, const T *q, int64_
 }
 
 // fp32 accept-reject with the residual row held in registers (vocab <= 49152).
+template <bool VEC4>
 __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
     const float *__restrict__ p, const float *__restrict__ q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
     int64_t q_rs, const int64_t *__restrict__ draft, const float *__restrict__ u_accept,
@@ -359,20 +388,29 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
   __syncthreads();
   const int64_t n = s_n;
   const float *pr = p + b * p_bs + n * p_rs;
-  const float *qr = (n < k) ? q + b * q_bs + n * q_rs : nullptr;  // zero row at n == k
+  // the q row, or (bonus position, n == k) a zero row: then p's own row is
+  // read and its values are not used
+  const bool has_q = n < k;
+  const float *qr = has_q ? q + b * q_bs + n * q_rs : pr;
   const int tile = kAcceptThreads * kCdfPerThread;
-  float vals[kRegTiles][kCdfPerThread];
+  // Every load of both rows goes out before the first is used, with no
+  // branch between them (elements past the vocab read as 0 through the
+  // buffer descriptors): one memory round trip for the row pair instead of
+  // one per element.
+  const __amdgpu_buffer_rsrc_t pb = row_buffer(pr, (unsigned)vocab), qb = row_buffer(qr, (unsigned)vocab);
+  float vals[kRegTiles][kCdfPerThread], qv[kRegTiles][kCdfPerThread];
+#pragma unroll
+  for (int j = 0; j < kRegTiles; ++j) {
+    load_tile<VEC4>(pb, j, tid, vals[j]);
+    load_tile<VEC4>(qb, j, tid, qv[j]);
+  }
   double local = 0.0;
 #pragma unroll
   for (int j = 0; j < kRegTiles; ++j)
 #pragma unroll
     for (int e = 0; e < kCdfPerThread; ++e) {
-      const int64_t i = (int64_t)j * tile + kCdfPerThread * tid + e;
-      float r = 0.0f;
-      if (i < vocab) {
-        r = qr ? pr[i] - qr[i] : pr[i];
-        r = r > 0.0f ? r : 0.0f;
-      }
+      float r = has_q ? vals[j][e] - qv[j][e] : vals[j][e];
+      r = r > 0.0f ? r : 0.0f;
       vals[j][e] = r;
       local += (double)r;
     }
@@ -385,12 +423,13 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
     for (int e = 0; e < kCdfPerThread; ++e) {
       const int64_t i = (int64_t)j * tile + kCdfPerThread * tid + e;
       if (use_residual) vals[j][e] = vals[j][e] / denom;
-      else vals[j][e] = i < vocab ? pr[i] : 0.0f;  // p == q: fall back to p
+      else vals[j][e] = i < vocab ? pr[i] : 0.0f;  // p == q: fall back to p (rare: reloaded)
     }
   const int64_t idx = inverse_cdf_regs(vals, vocab, u_residual[b], scratch, lds);
   if (tid == 0) out[batch + b] = idx;
 }
 
+template <bool VEC4>
 __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_regs_kernel(const float *__restrict__ probs,
                                                                                  int64_t vocab, int64_t row_stride,
                                                                                  const float *__restrict__ u,
@@ -401,13 +440,9 @@ __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_regs_kernel
   const float *row = probs + b * row_stride;
   const int tile = kAcceptThreads * kCdfPerThread;
   float vals[kRegTiles][kCdfPerThread];
+  const __amdgpu_buffer_rsrc_t rb = row_buffer(row, (unsigned)vocab);  // zeros past the vocab
 #pragma unroll
-  for (int j = 0; j < kRegTiles; ++j)
-#pragma unroll
-    for (int e = 0; e < kCdfPerThread; ++e) {
-      const int64_t i = (int64_t)j * tile + kCdfPerThread * threadIdx.x + e;
-      vals[j][e] = i < vocab ? row[i] : 0.0f;
-    }
+  for (int j = 0; j < kRegTiles; ++j) load_tile<VEC4>(rb, j, threadIdx.x, vals[j]);
   const int64_t idx = inverse_cdf_regs(vals, vocab, u[b], scratch, lds);
   if (threadIdx.x == 0) out[b] = idx;
 }
@@ -540,9 +575,16 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
   if (dtype == SPECDEC_F32 && vocab <= (int64_t)kRegTiles * kCdfPerThread * kAcceptThreads) {
-    accept_reject_regs_kernel<<<grid, block, 0, s>>>((const float *)p, (const float *)q, p_batch_stride, p_row_stride,
-                                                     q_batch_stride, q_row_stride, draft, (const float *)u_accept,
-                                                     (const float *)u_residual, batch, k, vocab, out);
+    if (vocab % 4 == 0)
+      accept_reject_regs_kernel<true><<<grid, block, 0, s>>>((const float *)p, (const float *)q, p_batch_stride,
+                                                             p_row_stride, q_batch_stride, q_row_stride, draft,
+                                                             (const float *)u_accept, (const float *)u_residual,
+                                                             batch, k, vocab, out);
+    else
+      accept_reject_regs_kernel<false><<<grid, block, 0, s>>>((const float *)p, (const float *)q, p_batch_stride,
+                                                              p_row_stride, q_batch_stride, q_row_stride, draft,
+                                                              (const float *)u_accept, (const float *)u_residual,
+                                                              batch, k, vocab, out);
   } else if (dtype == SPECDEC_F32) {
     accept_reject_kernel<float><<<grid, block, 0, s>>>(
         (const float *)p, (const float *)q, p_batch_stride, p_row_stride, q_batch_stride,
@@ -595,8 +637,12 @@ SPECDEC_API int specdec_sample_inverse_cdf(const void *probs, int dtype, int64_t
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
   if (dtype == SPECDEC_F32 && vocab <= (int64_t)kRegTiles * kCdfPerThread * kAcceptThreads) {
-    sample_inverse_cdf_regs_kernel<<<grid, block, 0, s>>>((const float *)probs, vocab, row_stride, (const float *)u,
-                                                          out);
+    if (vocab % 4 == 0)
+      sample_inverse_cdf_regs_kernel<true><<<grid, block, 0, s>>>((const float *)probs, vocab, row_stride,
+                                                                  (const float *)u, out);
+    else
+      sample_inverse_cdf_regs_kernel<false><<<grid, block, 0, s>>>((const float *)probs, vocab, row_stride,
+                                                                   (const float *)u, out);
   } else if (dtype == SPECDEC_F32) {
     sample_inverse_cdf_kernel<float><<<grid, block, 0, s>>>((const float *)probs, vocab,
                                                            row_stride, (const float *)u, out);
