@@ -75,7 +75,7 @@ struct AttnArgs {
 };
 
 struct TileInfo {
-  int b, h, qt, group, row, past, nrows, kv_len, nsplit, unit;
+  int b, h, qt, group, row, past, nnew, nrows, kv_len, nsplit, unit;
 };
 
 __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
@@ -86,10 +86,14 @@ __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool 
   ti.h = bh % a.Hkv;
   ti.b = bh / a.Hkv;
   ti.group = a.H / a.Hkv;
+  // the row's three metadata words in one scalar round trip: the empty asm
+  // uses all three here, so none of the loads is sunk past the early exits
+  // below into a round trip of its own
   ti.row = a.meta[ti.b];
   ti.past = a.meta[a.batch + ti.b];
-  const int nnew = a.meta[2 * a.batch + ti.b];
-  ti.nrows = nnew * ti.group;
+  ti.nnew = a.meta[2 * a.batch + ti.b];
+  __asm__ volatile("" ::"s"(ti.row), "s"(ti.past), "s"(ti.nnew));
+  ti.nrows = ti.nnew * ti.group;
   const int r0 = ti.qt * kRows;
   if (r0 >= ti.nrows) return false;
   const int t_hi = min(r0 + kRows - 1, ti.nrows - 1) / ti.group;
@@ -117,8 +121,7 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 // overlap write identical values.
 template <typename T>
 __device__ void append_new_kv(const AttnArgs &a, const TileInfo &ti, int lo, int hi) {
-  const int nnew = a.meta[2 * a.batch + ti.b];
-  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + nnew);
+  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + ti.nnew);
   if (p0 >= p1) return;
   const int half = kD / 2;
   const T *qkv = reinterpret_cast<const T *>(a.q);
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   // (a long prefill) take the plain path: append, fence, then read.
   const int lo = (NW == 16) ? 0 : split_idx * a.split;
   const int hi = (NW == 16) ? ti.nsplit * a.split : lo + a.split;
-  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + a.meta[2 * a.batch + ti.b]);
+  const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + ti.nnew);
   const int n_in = max(p1 - p0, 0);
   const bool staged = MODE != 0 && a.rope && n_in <= kStage;
   __shared__ __align__(16) u16 s_nk[kStage][kD];
@@ -520,7 +523,10 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   constexpr int kThreads = NW * kWave;
   constexpr int kKT = (kStage * (kD / 2) + kThreads - 1) / kThreads;  // k pairs per thread
   constexpr int kVT = (kStage * kD + kThreads - 1) / kThreads;        // v elements per thread
-  float sk1[kKT], sk2[kKT], scs[kKT], ssn[kKT];
+  // k halves kept as raw bf16 bits until the rotation, so no wait for them
+  // comes before the q and cos/sin loads below are issued
+  u16 sk1[kKT], sk2[kKT];
+  float scs[kKT], ssn[kKT];
   int skb[kKT], svb[kVT];
   u16 svv[kVT];
   const u16 *qkv16 = reinterpret_cast<const u16 *>(a.q);
@@ -532,8 +538,8 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
       if (task < n_in * (kD / 2)) {
         const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
         const u16 *kx = new_row(pos) + (int64_t)(a.H + ti.h) * kD;
-        sk1[u] = to_f32(__builtin_bit_cast(__hip_bfloat16, kx[i]));
-        sk2[u] = to_f32(__builtin_bit_cast(__hip_bfloat16, kx[i + kD / 2]));
+        sk1[u] = kx[i];
+        sk2[u] = kx[i + kD / 2];
         scs[u] = a.cos_t[(int64_t)pos * (kD / 2) + i];
         ssn[u] = a.sin_t[(int64_t)pos * (kD / 2) + i];
         skb[u] = trow[pos / bs];
@@ -583,7 +589,8 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
       if (task < n_in * (kD / 2)) {
         const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
         float y1, y2;
-        rope_pair(sk1[u], sk2[u], scs[u], ssn[u], y1, y2);
+        rope_pair(to_f32(__builtin_bit_cast(__hip_bfloat16, sk1[u])), to_f32(__builtin_bit_cast(__hip_bfloat16, sk2[u])),
+                  scs[u], ssn[u], y1, y2);
         const u16 b1 = __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(y1));
         const u16 b2 = __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(y2));
         s_nk[pos - p0][i] = b1;
