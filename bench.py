@@ -353,8 +353,14 @@ def bench_kernels(attention_grid=True):
         us_soft = time_fn(lambda: ops.probabilities(both, 1.0), graph=True)
         us_acc = time_fn(lambda: ops.accept_reject(p, q, draft, ua, ur), graph=True)
         logit_bytes = (2 * k + 1) * V * 4 * b
+        # the accept kernel reads the rejected position's p and q rows (and
+        # gathers 2k probabilities): 2 V fp32 per batch entry
+        accept_bytes = 2 * V * 4 * b
         res[f"accept_b{b}_k{k}"] = {"softmax_us": us_soft, "accept_us": us_acc, "logit_bytes": logit_bytes,
-                                    "softmax_gbs": 2 * logit_bytes / us_soft / 1e3}
+                                    "softmax_gbs": 2 * logit_bytes / us_soft / 1e3,
+                                    "softmax_frac_of_peak": 2 * logit_bytes / us_soft / 1e3 / HBM_PEAK_GBS,
+                                    "accept_bytes": accept_bytes, "accept_gbs": accept_bytes / us_acc / 1e3,
+                                    "accept_frac_of_peak": accept_bytes / us_acc / 1e3 / HBM_PEAK_GBS}
     # config 3: n-gram, B=16
     for length in (2048, 4096, 8192):
         rows = planted_rows(16, length, V, seed=length)
@@ -362,7 +368,8 @@ def bench_kernels(attention_grid=True):
         lens = torch.full((16,), length, dtype=torch.int32, device="cuda")
         us = time_fn(lambda: ops.ngram_lookup(hist, lens, 4, 3), graph=True)
         nbytes = 16 * length * 4
-        res[f"ngram_b16_L{length}"] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3}
+        res[f"ngram_b16_L{length}"] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+                                       "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
     # config 2': cache append (rope + scatter of 5 tokens) and rollback plan
     cache, step, q, out = setup_attention(1, 4096)
     qkv = torch.randn(1, 5, 96 * 64, device="cuda").to(torch.bfloat16)
@@ -371,7 +378,9 @@ def bench_kernels(attention_grid=True):
     cos, sin = (t.cuda() for t in rope_tables(SMOLLM2_1_7B, 8192))
     us_app = time_fn(lambda: ops.rope_append(qkv, 32, 32, 64, cos, sin, step.meta, 1, 5, cache.table_tensor, BLOCK,
                                              cache.k[0], cache.v[0]), graph=True)
-    res["append_b1_t5"] = {"us": us_app, "bytes": 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2}
+    app_bytes = 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2
+    res["append_b1_t5"] = {"us": us_app, "bytes": app_bytes, "gbs": app_bytes / us_app / 1e3,
+                           "frac_of_peak": app_bytes / us_app / 1e3 / HBM_PEAK_GBS}
     # config 2': one round's rollback of 8 rows (a rejected tail each) and the
     # regrowth for the next verify: the block plan the cache launches
     ids = list(range(8))
@@ -425,27 +434,92 @@ def cpu_baseline(t_state, d_state, prompt, new_tokens=64):
             "seconds": dt, "tokens": out[0]}
 
 
-def cpu_attention_baseline(length=4096):
-    """Oracle attention step (gather copy + masked SDPA) at B=1, L=4096 on the CPU."""
+def cpu_attention_baseline(length=4096, batch=1, seconds=3.0):
+    """Oracle attention step (gather copy + masked SDPA) at context 4096 on the CPU."""
     import oracle.forward as of
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     pool = torch.randn(4096 * BLOCK, 32, 64, generator=g).to(torch.bfloat16)
-    read = (torch.randperm(4096, generator=g)[: -(-(length + 5) // BLOCK)][:, None] * BLOCK
-            + torch.arange(BLOCK)).flatten()[: length + 5][None]
-    q = torch.randn(1, 32, 5, 64, generator=g).to(torch.bfloat16)
-    past, total = torch.tensor([length]), torch.tensor([length + 5])
+    nblk = -(-(length + 5) // BLOCK)
+    perm = torch.randperm(4096, generator=g)[: batch * nblk].view(batch, nblk)
+    read = (perm[:, :, None] * BLOCK + torch.arange(BLOCK)).flatten(1)[:, : length + 5]
+    q = torch.randn(batch, 32, 5, 64, generator=g).to(torch.bfloat16)
+    past, total = torch.full((batch,), length), torch.full((batch,), length + 5)
     n = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < 3.0:
+    while time.perf_counter() - t0 < seconds:
         k_all = pool[read].transpose(1, 2)
         v_all = pool[read].transpose(1, 2)
         of.attention(q, k_all, v_all, past, total, 0.125)
         n += 1
     us = (time.perf_counter() - t0) / n * 1e6
-    return {"us": us, "gbs": attention_bytes(1, [length]) / us / 1e3, "cores": threads}
+    return {"us": us, "gbs": attention_bytes(batch, [length] * batch) / us / 1e3, "cores": threads}
+
+
+def cpu_kernel_baselines(seconds=1.0):
+    """The oracle (the reference's algorithms in torch on the host cores) on
+    the kernels' own workloads, each repeated for about `seconds`:
+    temperature softmax and accept-reject (config 1 and batch 8), n-gram
+    lookup (config 3), and the cache's append + rollback bookkeeping
+    (config 2': slot maps and block tables for 8 rows, one layer's write of
+    5 tokens)."""
+    import oracle.accept as oa
+    import oracle.kv as okv
+    import oracle.ngram as on
+    import oracle.sampling as osamp
+    from make_golden import planted_rows
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+
+    def timed(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n * 1e6
+
+    res = {"cores": threads}
+    for b, k in ((1, 4), (8, 4)):
+        g = torch.Generator().manual_seed(1)
+        tl = torch.randn(b, k + 1, V, generator=g) * 2
+        dl = tl[:, :k] + torch.randn(b, k, V, generator=g) * 0.5
+        p, q = osamp.probabilities(tl, 1.0), osamp.probabilities(dl, 1.0)
+        draft = torch.randint(0, V, (b, k), generator=g)
+        ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
+        both = torch.cat([tl.reshape(-1, V), dl.reshape(-1, V)])
+        res[f"softmax_b{b}_k{k}_us"] = timed(lambda: osamp.probabilities(both, 1.0))
+        res[f"accept_b{b}_k{k}_us"] = timed(lambda: oa.accept_reject(p, q, draft, u_accept=ua, u_residual=ur))
+    for length in (2048, 4096, 8192):
+        rows = planted_rows(16, length, V, seed=length)
+        res[f"ngram_b16_L{length}_us"] = timed(lambda: [on.lookup_match(r, 4, 3) for r in rows])
+    cache = okv.KVCache(1, 32, 64, 8 * 70, BLOCK, torch.bfloat16)
+    ids = list(range(8))
+    for s in ids:
+        cache.add(s)
+    cache.append(ids, [1010] * 8)
+
+    def rollback_and_grow():
+        for s in ids:
+            cache.truncate(s, 1010 - 5 + 1)
+        cache.append(ids, [4] * 8)
+
+    res["rollback_grow_b8_us"] = timed(rollback_and_grow)
+    one = okv.KVCache(1, 32, 64, 300, BLOCK, torch.bfloat16)
+    one.add(0)
+    one.append([0], [4096])
+    kv_new = torch.randn(1, 32, 5, 64).to(torch.bfloat16)
+
+    def append_write():
+        one.truncate(0, 4096)
+        slots = one.append([0], [5])
+        one.write(0, slots, kv_new, kv_new)
+
+    res["append_b1_t5_us"] = timed(append_write)
+    return res
 
 
 def main():
@@ -515,6 +589,8 @@ def main():
         cpu["bf16_first_divergence_from_gpu"] = next(
             (i for i, (x, y) in enumerate(zip(cpu_tokens, gpu_tokens)) if x != y), None)
         cpu["attention_b1_L4096"] = cpu_attention_baseline()
+        cpu["attention_b8_L4096"] = cpu_attention_baseline(batch=8)
+        cpu["kernels"] = cpu_kernel_baselines()
     line = {
         "metric": "spec-decode accepted tokens/s, 1.7B/135M k=4 b=1; verify-attn HBM GB/s",
         "value": e2e["tokens_per_s"],
@@ -546,7 +622,29 @@ def main():
     }
     if cpu:
         line["cpu_baseline"]["speedup"] = e2e["tokens_per_s"] / cpu["value"]
+        line["cpu_baseline"]["kernel_speedups"] = kernel_speedups(kernels, cpu, attn, attn1)
     print(json.dumps(line))
+
+
+def kernel_speedups(kernels, cpu, attn8, attn1):
+    """Host-oracle time over GPU time for each kernel timed on both sides."""
+    ck = cpu.get("kernels", {})
+    pairs = {"attention_b1_L4096": (cpu["attention_b1_L4096"]["us"], attn1["us"]),
+             "attention_b8_L4096": (cpu["attention_b8_L4096"]["us"], attn8["us"])}
+    for b, k in ((1, 4), (8, 4)):
+        g = kernels.get(f"accept_b{b}_k{k}")
+        if g:
+            pairs[f"softmax_b{b}_k{k}"] = (ck[f"softmax_b{b}_k{k}_us"], g["softmax_us"])
+            pairs[f"accept_b{b}_k{k}"] = (ck[f"accept_b{b}_k{k}_us"], g["accept_us"])
+    for length in (2048, 4096, 8192):
+        g = kernels.get(f"ngram_b16_L{length}")
+        if g:
+            pairs[f"ngram_b16_L{length}"] = (ck[f"ngram_b16_L{length}_us"], g["us"])
+    if "append_b1_t5" in kernels:
+        pairs["append_b1_t5"] = (ck["append_b1_t5_us"], kernels["append_b1_t5"]["us"])
+    if "rollback_grow_b8" in kernels:
+        pairs["rollback_grow_b8"] = (ck["rollback_grow_b8_us"], kernels["rollback_grow_b8"]["us_host_inclusive"])
+    return {name: c / g for name, (c, g) in pairs.items()}
 
 
 if __name__ == "__main__":
