@@ -199,6 +199,31 @@ def test_config1_matches_oracle(seed, temperature):
         assert int(ok.sum()) >= b - 1
 
 
+@pytest.mark.parametrize("vocab", [1001, 4099, 49151])
+def test_fp32_rows_of_any_length_match_oracle(vocab):
+    """fp32 rows whose length is not a multiple of 4 (the register-resident
+    kernels then load 4 bytes at a time; elements past the row read as
+    zero): accept-reject and the standalone inverse-CDF sampler against the
+    oracle, bit-exact except rows decided within 1e-6 of a threshold."""
+    b, k = 8, 4
+    for seed in range(3):
+        g = torch.Generator().manual_seed(vocab + seed)
+        target = torch.randn(b, k + 1, vocab, generator=g) * 2.0
+        draft_logits = target[:, :k] + torch.randn(b, k, vocab, generator=g) * 0.5
+        p = osamp.probabilities(target, 1.0)
+        q = osamp.probabilities(draft_logits, 1.0)
+        draft = torch.multinomial(q.reshape(-1, vocab), 1, generator=g).view(b, k)
+        ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
+        want = oa.accept_reject(p, q, draft, u_accept=ua, u_residual=ur)
+        got = accept_reject(p.cuda(), q.cuda(), draft, u_accept=ua, u_residual=ur)
+        near = oa.accept_reject_exclusion(p, q, draft, ua, ur)
+        ok = (got.n_accepted == want.n_accepted) & (got.next_token == want.next_token)
+        assert bool((ok | near).all()), (vocab, seed, got, want, near)
+        # the sampler alone on the target's bonus rows
+        rows = p[:, k].contiguous()
+        assert torch.equal(sample_inverse_cdf(rows.cuda(), ur).cpu(), oa.sample_inverse_cdf(rows, ur))
+
+
 def test_config1_distribution_matches_target_softmax():
     """10,000 seeded rounds on config 1: the first emitted token's empirical
     distribution is the target softmax (chi-square GoF over tokens with
