@@ -535,8 +535,8 @@ def main():
     ap.add_argument("--one-pool", action="store_true", help="--only attention: re-read one layer pool")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (sharding is described in "
-              "DESIGN.md, not built)", file=sys.stderr)
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (the path is built and "
+              "measured on a single GPU; sharding across GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
