@@ -378,8 +378,10 @@ def _qkv_side(dev, x, cos, sin, meta, batch, width, tables, k_pool, v_pool, out=
     _on(dev, v_pool, "v_pool", x.dtype, True, k_pool.numel())
     if out is not None:
         _on(dev, out, "out", x.dtype)
-    if x.stride(-1) != 1 or (batch > 0 and width > 0 and x.numel() == 0):
+    if x.stride(-1) != 1:
         raise ValueError("activations need unit inner stride")
+    if batch > 0 and width > 0 and x.numel() == 0:
+        raise ValueError(f"no activations for batch {batch}, width {width}")
 
 
 def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
