@@ -18,6 +18,16 @@ def t64(xs):
     return torch.tensor([float(x) for x in xs], dtype=torch.float64)
 
 
+def test_rejection_mass_is_one_minus_overlap():
+    """The probability of rejecting the draft, sum(max(0, p - q)), and the
+    overlap sum(min(p, q)) of the toy pair add up to one (exact fractions)."""
+    beta = sum(max(Fraction(0), p - q) for p, q in zip(P, Q))
+    overlap = sum(min(p, q) for p, q in zip(P, Q))
+    assert beta == Fraction(2, 5) and beta + overlap == 1
+    # the accept probabilities of the toy pair weigh q to the same overlap
+    assert sum(q * a for q, a in zip(Q, ACCEPT)) == overlap
+
+
 def test_residual_hand_values():
     r = oa.residual_distribution(t64(P), t64(Q))
     assert torch.allclose(r, t64([Fraction(3, 4), Fraction(1, 4), 0, 0, 0]), atol=1e-15, rtol=0)
