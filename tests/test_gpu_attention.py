@@ -89,7 +89,7 @@ def test_bf16_gqa_small_blocks(bs):
         assert (got - want).abs().max().item() < 2e-2
 
 
-@pytest.mark.parametrize("L", [300, 1000, 2044, 4090])
+@pytest.mark.parametrize("L", [300, 509, 1000, 2044, 4090])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_verify_rows_equal_decode_rows_bitwise(dtype, L):
     """The same query at the same position gives identical bits whether it is
