@@ -164,7 +164,7 @@ def test_prefill_many_query_tiles():
 
 def test_repeated_split_combines_stay_exact():
     """Many back-to-back launches over the same workspace (every call splits
-    17 ways and combines in a second kernel): each result is compared with
+    9 ways and combines in a second kernel): each result is compared with
     SDPA, so a stale or overwritten partial shows."""
     d, h, hkv, bs, L = 64, 32, 32, 16, 4096
     g = torch.Generator().manual_seed(11)
@@ -259,3 +259,83 @@ def test_fused_rope_append_equals_separate_kernels(dtype, bs, t_new, lengths):
         outs.append((out, k_all, v_all))
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
+
+
+def _filled(batch, lengths, seed, h=32, hkv=32, t_new=5):
+    """A bf16 cache of `batch` rows with lengths[b] cached keys each (random
+    K/V, shuffled blocks, block 16), t_new more appended, and q for them."""
+    d, bs = 64, 16
+    g = torch.Generator().manual_seed(seed)
+    cache = make_cache(1, hkv, d, sum((n + t_new) // bs + 2 for n in lengths) + 8, bs, torch.bfloat16, seed)
+    ids = list(range(batch))
+    for s in ids:
+        cache.add(s)
+    step = cache.append(ids, [n + t_new for n in lengths])
+    t_max = max(lengths) + t_new
+    cache.write(0, step, torch.randn(batch, hkv, t_max, d, generator=g).to(torch.bfloat16).cuda(),
+                torch.randn(batch, hkv, t_max, d, generator=g).to(torch.bfloat16).cuda())
+    for s, n in zip(ids, lengths):
+        cache.truncate(s, n)
+    step = cache.append(ids, [t_new] * batch)
+    q = torch.randn(batch, t_new, h * d, generator=g).to(torch.bfloat16).cuda()
+    return cache, step, q
+
+
+def _attend(cache, step, q, ws, out=None, h=32, hkv=32):
+    batch, t_new = q.shape[0], q.shape[1]
+    if out is None:
+        out = torch.zeros(batch, t_new, h * 64, dtype=torch.bfloat16, device="cuda")
+    ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, t_new, h, hkv,
+                        64, cache.block_size, 0.125, step.max_total, out, out.stride(1), ws)
+    return out
+
+
+# (batch, cached lengths): 9 splits of 512 at batch 8, 6, ragged 2..9, 18
+# (five groups of four in the combine) and 34 (two rounds of its
+# eight-group fold)
+_SPLIT_SHAPES = [(8, [4100 - 7 * b for b in range(8)]), (1, [3000]), (3, [2600, 700, 4500]), (2, [9000, 5000]),
+                 (1, [17000])]
+
+
+def test_split_workspace_shared_across_shapes():
+    """One workspace for calls of different shapes: the tile and split
+    counts differ, so one call's partials lie where another's were.  Each
+    result equals the same call on a fresh workspace bit for bit and
+    matches SDPA."""
+    built = [_filled(b, lengths, seed=40 + i) for i, (b, lengths) in enumerate(_SPLIT_SHAPES)]
+    shared = ops.AttentionWorkspace(torch.device("cuda"))
+    for rep in range(2):
+        for i, (cache, step, q) in enumerate(built):
+            got = _attend(cache, step, q, shared)
+            fresh = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
+            torch.cuda.synchronize()
+            assert torch.equal(got, fresh), (rep, i)
+            if rep == 0:
+                b, t_new = q.shape[0], q.shape[1]
+                k_all, v_all = cache.gather(0, step)
+                want = of.attention(q.view(b, t_new, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(),
+                                    v_all.cpu().float(), torch.tensor(step.past), torch.tensor(step.total), 0.125)
+                err = (got.view(b, t_new, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+                assert err < 2e-2, (i, err)
+
+
+def test_split_graph_replays_match_eager():
+    """A split-path call (split kernel + combine) captured in a HIP graph:
+    each replay -- with eager calls of another shape on the same workspace
+    in between -- gives the eager bits."""
+    from lm.graphs import _capture
+
+    cache, step, q = _filled(2, [5000, 2600], seed=61)
+    other = _filled(3, [2600, 700, 4500], seed=62)
+    ws = ops.AttentionWorkspace(torch.device("cuda"))
+    ws.reserve(1 << 24)  # no growth inside the capture
+    want = _attend(cache, step, q, ws)
+    want_other = _attend(*other, ws)
+    out = torch.zeros_like(want)
+    graph, _ = _capture(lambda: _attend(cache, step, q, ws, out))
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        assert torch.equal(_attend(*other, ws), want_other), i
