@@ -339,3 +339,25 @@ def test_split_graph_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, want), i
         assert torch.equal(_attend(*other, ws), want_other), i
+
+
+def test_ragged_batch8_rows_equal_rows_verified_alone_bitwise():
+    """Batch 8 with rows of 1 to 16 splits: the call runs one workgroup per
+    split plus the combine kernel for every tile.  Each row verified alone
+    at batch 1 takes the 16-wave path (up to four splits, folded in LDS) or
+    the same split path; either way the bits are the same, and the batch
+    result matches SDPA."""
+    lengths = [7900, 100, 2500, 4100, 600, 7000, 3000, 1500]
+    cache, step, q = _filled(8, lengths, seed=71)
+    out8 = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
+    k_all, v_all = cache.gather(0, step)
+    want = of.attention(q.view(8, 5, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(), v_all.cpu().float(),
+                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
+    err = (out8.view(8, 5, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+    assert err < 2e-2, err
+    for row, n in enumerate(lengths):
+        cache.truncate(row, n)
+        step1 = cache.append([row], [5])
+        q1 = q[row:row + 1].contiguous()
+        out1 = _attend(cache, step1, q1, ops.AttentionWorkspace(torch.device("cuda")))
+        assert torch.equal(out1[0], out8[row]), row
