@@ -35,10 +35,10 @@ sys.path.insert(0, str(ROOT / "speculative-decoder_amd"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of the B=8, context-4096 verify attention (both
-# kernels): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention`,
+# HBM bytes per launch of the B=8, context-4096 verify attention (one tiled
+# launch): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention`,
 # each scaled by what the counter reads for a copy of known size.
-ATTN_B8_TRAFFIC = 277_081_050
+ATTN_B8_TRAFFIC = 270_661_099
 V = 49152
 PROMPT = 256
 NEW_TOKENS = 128
@@ -609,7 +609,8 @@ def main():
                    "batch": 1, "k": K, "prompt": PROMPT, "new_tokens": NEW_TOKENS, "block_size": BLOCK},
         "roofline": {"bound": "hbm", "achieved": attn["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": ATTN_B8_TRAFFIC,
-                     "kernel": "verify paged attention (attention_bf16_kernel + attention_combine_kernel), "
+                     "kernel": "verify paged attention (attention_bf16_kernel<1, 16, true>: one 16-wave workgroup "
+                               "per (row, kv head) tile taking its 512-token splits in rounds, no combine launch), "
                                "B=8, context 4096 (+5 appended), 32/32 heads x 64, bf16, block 16, K/V from HBM",
                      "us_per_launch": attn["us"], "bytes_per_launch": attn["bytes"]},
         "cpu_baseline": cpu,

@@ -237,8 +237,10 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * need not match other calls (the draft; bf16 only, fp32 takes the default).
  * When a row needs more than four splits, a second kernel combining the
  * split partials is launched on the same stream (2 to 4 splits are folded
- * inside one workgroup with the same arithmetic); calls sharing a workspace
- * must be ordered.
+ * inside one workgroup with the same arithmetic, and so are 5 to 12 splits
+ * when the call has a (row, kv head) tile for every compute unit and at
+ * most 8 query rows per kv head: the workspace is then not used); calls
+ * sharing a workspace must be ordered.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
  * cache/kv.py:108-112. */
 int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,

@@ -26,7 +26,12 @@
 // (attention_combine_kernel), launched right after on the same stream,
 // folds them per (batch, head, tile).  With 2 to 4 splits one 16-wave
 // workgroup per tile runs all of them and folds them in LDS with the same
-// arithmetic, so short contexts (decode, the draft) need one launch.
+// arithmetic, so short contexts (decode, the draft) need one launch.  So
+// does a tiled call (5 to 12 splits, a tile for every CU): one 16-wave
+// workgroup per tile whose four wave groups take its splits in rounds,
+// every wave keeping each split's softmax state in LDS with no barrier
+// until the last; the fold then follows the split kernel's and the combine
+// kernel's arithmetic.
 // Every query's reduction order depends only on the absolute key positions,
 // never on how many queries share the call, so a token verified among k+1
 // gets the same bits as the same token decoded alone.
@@ -47,6 +52,9 @@ constexpr int kRows = 16;          // query rows per tile
 constexpr int kDefaultSplit = 512;
 constexpr int kPart = kRows * (kD + 1);  // floats per split partial: O/l [16][64], lse [16]
 constexpr int kStage = 16;  // appended tokens per workgroup taken from LDS
+// Tiled calls (one 16-wave workgroup per tile, wave groups taking splits in
+// rounds): splits and live query rows whose per-wave softmax states fit LDS
+constexpr int kTSplits = 12, kTRows = 8;
 
 struct AttnArgs {
   const void *q;
@@ -69,6 +77,9 @@ struct AttnArgs {
   // 16-wave launches only: one split over every key, wave w taking the
   // 64-token steps w, w+16, ... (results need not match other calls)
   int flat;
+  // 16-wave launches only: every split of the tile, wave group grp taking
+  // splits grp, grp + 4, ... (at most kTSplits splits, kTRows live rows)
+  int tiled;
   float *ws;
   void *out;
   int64_t out_stride;
@@ -153,10 +164,11 @@ __device__ void append_new_kv(const AttnArgs &a, const TileInfo &ti, int lo, int
 // scale * log2(e).  Waves hand them over in LDS as s_m/s_l [wave][query] and
 // s_o [wave][query][dim].
 
-// Fold of waves w0 .. w0+N-1 for query row qq, dims d0 .. d0+3.
-template <int N = 4>
-__device__ __forceinline__ void fold_waves(const float (*s_m)[kRows], const float (*s_l)[kRows],
-                                           const float (*s_o)[kRows][kD + 4], int w0, int qq, int d0, float &M,
+// Fold of waves w0 .. w0+N-1 for query row qq, dims d0 .. d0+3 (R rows
+// per wave in LDS).
+template <int N = 4, int R = kRows>
+__device__ __forceinline__ void fold_waves(const float (*s_m)[R], const float (*s_l)[R],
+                                           const float (*s_o)[R][kD + 4], int w0, int qq, int d0, float &M,
                                            float &L, float (&O)[4]) {
   M = s_m[w0][qq];
   for (int w = 1; w < N; ++w) M = fmaxf(M, s_m[w0 + w][qq]);
@@ -356,12 +368,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_combine_kernel(AttnArg
 // result for a single group is the same bits.  With a.flat (one split over
 // every key, results that need not match other calls) all 16 waves fold
 // straight into the output.
+// LDS floats of finish_grouped, carved from the kernel's pool.
+constexpr int kGroupedFloats = 32 * kRows + 16 * kRows * (kD + 4) + 4 * kRows * kD + 4 * kRows;
 template <typename T>
-__device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4]) {
-  __shared__ float s_m[16][kRows], s_l[16][kRows];
-  __shared__ float s_o[16][kRows][kD + 4];
-  __shared__ float s_pv[4][kRows][kD];
-  __shared__ float s_pl[4][kRows];
+__device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, float l, const f32x4 (&o)[4],
+                               float *pool) {
+  float(*s_m)[kRows] = reinterpret_cast<float(*)[kRows]>(pool);
+  float(*s_l)[kRows] = reinterpret_cast<float(*)[kRows]>(pool + 16 * kRows);
+  float(*s_o)[kRows][kD + 4] = reinterpret_cast<float(*)[kRows][kD + 4]>(pool + 32 * kRows);
+  float *pv0 = pool + 32 * kRows + 16 * kRows * (kD + 4);
+  float(*s_pv)[kRows][kD] = reinterpret_cast<float(*)[kRows][kD]>(pv0);
+  float(*s_pl)[kRows] = reinterpret_cast<float(*)[kRows]>(pv0 + 4 * kRows * kD);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   if (g == 0) {
@@ -423,6 +440,74 @@ __device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, f
   }
 }
 
+// Tiled calls: each wave's (m, l, O) of one split, rows < kTRows, kept in
+// LDS slot 4 * split + (wave & 3) until every wave is done -- no barrier
+// between splits, so the tile's waves run free.
+constexpr int kTiledFloats = kTSplits * 4 * kTRows * (2 + kD + 4);
+__device__ __forceinline__ void keep_wave_state(float *pool, int split, float m, float l, const f32x4 (&o)[4]) {
+  float(*st_m)[kTRows] = reinterpret_cast<float(*)[kTRows]>(pool);
+  float(*st_l)[kTRows] = reinterpret_cast<float(*)[kTRows]>(pool + kTSplits * 4 * kTRows);
+  float(*st_o)[kTRows][kD + 4] = reinterpret_cast<float(*)[kTRows][kD + 4]>(pool + 2 * kTSplits * 4 * kTRows);
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int slot = 4 * split + ((threadIdx.x >> 6) & 3);
+  if (c < kTRows) {
+    if (g == 0) {
+      st_m[slot][c] = m;
+      st_l[slot][c] = l;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st_o[slot][c][16 * t + 4 * g + i] = o[t][i];
+  }
+}
+
+// After the last split of a tiled call: each split's four wave states are
+// folded as fold_wg4 folds them, turned into the partial write_split would
+// write, and the partials folded with the combine kernel's tree, so a query
+// gets the bits it gets from the split kernel and the combine.
+template <typename T>
+__device__ void fold_tiled(const AttnArgs &a, const TileInfo &ti, const float *pool) {
+  const float(*st_m)[kTRows] = reinterpret_cast<const float(*)[kTRows]>(pool);
+  const float(*st_l)[kTRows] = reinterpret_cast<const float(*)[kTRows]>(pool + kTSplits * 4 * kTRows);
+  const float(*st_o)[kTRows][kD + 4] =
+      reinterpret_cast<const float(*)[kTRows][kD + 4]>(pool + 2 * kTSplits * 4 * kTRows);
+  __syncthreads();
+  const int tid = threadIdx.x;
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  const int nq = min(kRows, ti.nrows - ti.qt * kRows);
+  if (tid >= 256 || qq >= nq) return;
+  const int ns = ti.nsplit, ngroups = (ns + 3) / 4;
+  float gl[8];
+  f32x4 gv[8];
+#pragma unroll
+  for (int y = 0; y < 8; ++y) {
+    const int n_y = min(max(ns - 4 * y, 0), 4);
+    gl[y] = -INFINITY;
+    gv[y] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (4 * y >= kTSplits || n_y == 0) continue;
+    float l4[4];
+    f32x4 v4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sp = min(4 * y + u, ns - 1);
+      float M, L, O[4];
+      fold_waves<4, kTRows>(st_m + 4 * sp, st_l + 4 * sp, st_o + 4 * sp, 0, qq, d0, M, L, O);
+      const bool any = L > 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v4[u][i] = any ? O[i] / L : 0.0f;
+      l4[u] = any ? M + __builtin_amdgcn_logf(L) : -INFINITY;
+    }
+    group_partial(n_y, l4, v4, gl[y], gv[y]);
+  }
+  float Mx = -INFINITY, den = 0.0f, num[4] = {0.f, 0.f, 0.f, 0.f};
+  fold_splits(0, ngroups, gl, gv, Mx, den, num);
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = num[i] / den;
+  store_row4<T>(a, ti, qq, d0, v);
+}
+
 // Online-softmax update over N scores per lane (t = score * scale * log2 e,
 // -inf where not visible), replaced by their weights 2^(t - m).
 template <int N>
@@ -465,15 +550,16 @@ __device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l
 // combine kernel.  NW = 16: one workgroup runs all (at most four) splits of
 // its tile, four waves each, and folds them in LDS (finish_grouped) -- no
 // combine launch, same bits; or, with a.flat, one split over every key with
-// all 16 waves striding it.
-template <int MODE, int NW>
+// all 16 waves striding it; or, TILED, all of a tile's 5 to 12 splits in
+// rounds of four (keep_wave_state, fold_tiled), same bits again.
+template <int MODE, int NW, bool TILED = false>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
     AttnArgs a) {
   TileInfo ti;
   if (!tile_info(a, ti, /*any_split=*/NW == 16)) return;
   const bool flat = NW == 16 && a.flat;
   const int tid = threadIdx.x, lane = tid & 63, wave = flat ? (tid >> 6) : ((tid >> 6) & 3);
-  const int split_idx = (NW == 16) ? (flat ? 0 : (tid >> 8)) : (int)blockIdx.y;
+  int split_idx = (NW == 16) ? (flat ? 0 : (tid >> 8)) : (int)blockIdx.y;
   const int wstride = flat ? 16 * 64 : 4 * 64;  // tokens between a wave's steps
   const int g = lane >> 4, c = lane & 15;
   const int r = ti.qt * kRows + c;
@@ -497,9 +583,9 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   const int last_blk = (kv_len - 1) / bs;
   // wave w takes the 64-token steps w, w+4, w+8, ... of its split (none
   // when the split lies past this tile's keys); flat: w, w+16, ...
-  const int s_lo = split_idx * a.split;
-  const int s_hi = min(s_lo + a.split, kv_len);
-  const int c_first = s_lo + 64 * wave;
+  int s_lo = split_idx * a.split;
+  int s_hi = min(s_lo + a.split, kv_len);
+  int c_first = s_lo + 64 * wave;
 
   // Fused append.  The new tokens of this workgroup's key range [lo, hi)
   // are rotated once into LDS (and written to the pools for later calls);
@@ -513,6 +599,9 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   const bool staged = MODE != 0 && a.rope && n_in <= kStage;
   __shared__ __align__(16) u16 s_nk[kStage][kD];
   __shared__ __align__(16) u16 s_nv[kStage][kD];
+  // 16 waves: the LDS of finish_grouped, or of a tiled call's wave states
+  constexpr int kPool = NW != 16 ? 4 : TILED ? kTiledFloats : kGroupedFloats;
+  __shared__ __align__(16) float s_pool[kPool];
 
   // ---- prologue: every load here depends on the row metadata only, so
   // all of them are in flight together
@@ -755,15 +844,34 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
     }
   };
 
-  for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
-    StepRegs r;
-    issue(c0, bj, r);
-    // next step's block ids, in flight during this step's arithmetic
-    if (MODE != 0 && c0 + wstride < s_hi) bj = step_blocks(c0 + wstride);
-    compute(c0, r);
+  // tiled: wave group grp runs splits grp, grp + 4, ... one after another,
+  // keeping each split's state in LDS without waiting for the other waves
+  constexpr bool tiled = NW == 16 && TILED;
+  const int rounds = tiled ? (ti.nsplit + 3) / 4 : 1;
+  for (int round = 0;; ++round) {
+    for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
+      StepRegs r;
+      issue(c0, bj, r);
+      // next step's block ids, in flight during this step's arithmetic
+      if (MODE != 0 && c0 + wstride < s_hi) bj = step_blocks(c0 + wstride);
+      compute(c0, r);
+    }
+    if (!tiled) break;
+    keep_wave_state(s_pool, split_idx, m, l, o);
+    if (round + 1 >= rounds) break;
+    split_idx += 4;
+    s_lo = split_idx * a.split;
+    s_hi = min(s_lo + a.split, kv_len);
+    c_first = s_lo + 64 * wave;
+    if (MODE != 0 && c_first < s_hi) bj = step_blocks(c_first);
+    m = -INFINITY;
+    l = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  if (NW == 16) finish_grouped<__hip_bfloat16>(a, ti, m, l, o);
-  else finish<__hip_bfloat16>(a, ti, m, l, o);
+  if constexpr (NW != 16) finish<__hip_bfloat16>(a, ti, m, l, o);
+  else if constexpr (tiled) fold_tiled<__hip_bfloat16>(a, ti, s_pool);
+  else finish_grouped<__hip_bfloat16>(a, ti, m, l, o, s_pool);
 }
 
 // ---------------------------------------------------------------- fp32 ----
@@ -932,6 +1040,20 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
   return SPECDEC_OK;
 }
 
+// Compute units of the current device (0 if it cannot be read), looked up
+// once per device.
+static int cu_count() {
+  static int counts[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
 static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width, int32_t n_heads,
                             int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_kv_len,
                             int32_t split_tokens, float *workspace, int64_t workspace_floats, void *stream) {
@@ -954,10 +1076,17 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   a.ws = workspace;
-  // bf16 tiles with at most four splits (or one flat split) run in one
-  // 16-wave workgroup; otherwise one 4-wave workgroup per split + combine
-  const bool single = dtype == SPECDEC_BF16 && (a.flat || a.max_splits <= 4);
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
+  // bf16 tiles with more than four splits (at most kTSplits), when every CU
+  // gets a tile and a tile's live rows fit kTRows, run tiled: one 16-wave
+  // workgroup per tile takes all of its splits, no partials, no combine
+  a.tiled = dtype == SPECDEC_BF16 && !a.flat && block_size % 16 == 0 && a.max_splits > 4 &&
+            a.max_splits <= kTSplits && a.n_qtiles == 1 && width * (n_heads / n_kv_heads) <= kTRows &&
+            units >= cu_count();
+  // bf16 tiles with at most four splits (or one flat split, or tiled) run
+  // in one 16-wave workgroup; otherwise one 4-wave workgroup per split +
+  // combine
+  const bool single = dtype == SPECDEC_BF16 && (a.flat || a.tiled || a.max_splits <= 4);
   a.parts = single ? 1 : a.max_splits;
   if (a.parts > 1) {
     if (!workspace) return SPECDEC_EINVAL;
@@ -967,7 +1096,11 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   hipStream_t s = as_stream(stream);
   const bool bs16 = (block_size % 16) == 0;
   dim3 grid((unsigned)units, (unsigned)a.parts);
-  if (single) {
+  if (a.tiled) {
+    dim3 block(16 * kWave);
+    if (block_size == 16) attention_bf16_kernel<1, 16, true><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<2, 16, true><<<grid, block, 0, s>>>(a);
+  } else if (single) {
     dim3 block(16 * kWave);
     if (block_size == 16) attention_bf16_kernel<1, 16><<<grid, block, 0, s>>>(a);
     else if (bs16) attention_bf16_kernel<2, 16><<<grid, block, 0, s>>>(a);

@@ -361,3 +361,70 @@ def test_ragged_batch8_rows_equal_rows_verified_alone_bitwise():
         q1 = q[row:row + 1].contiguous()
         out1 = _attend(cache, step1, q1, ops.AttentionWorkspace(torch.device("cuda")))
         assert torch.equal(out1[0], out8[row]), row
+
+
+def test_tiled_batch8_rows_equal_rows_verified_alone_bitwise():
+    """Batch 8 with rows of 1 to 12 splits (at most 6144 keys, 5 queries):
+    256 tiles, one per CU, so the call runs tiled -- one 16-wave workgroup
+    per tile whose wave groups take its splits in rounds, each wave keeping
+    its per-split softmax state in LDS, folded at the end with the split
+    kernel's and the combine's arithmetic.  Each row verified alone at
+    batch 1 (16-wave or split + combine path) gives the same bits, and the
+    batch result matches SDPA."""
+    lengths = [6100, 100, 2500, 4100, 600, 5000, 3000, 1500]
+    cache, step, q = _filled(8, lengths, seed=81)
+    out8 = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
+    k_all, v_all = cache.gather(0, step)
+    want = of.attention(q.view(8, 5, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(), v_all.cpu().float(),
+                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
+    err = (out8.view(8, 5, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+    assert err < 2e-2, err
+    for row, n in enumerate(lengths):
+        cache.truncate(row, n)
+        step1 = cache.append([row], [5])
+        q1 = q[row:row + 1].contiguous()
+        out1 = _attend(cache, step1, q1, ops.AttentionWorkspace(torch.device("cuda")))
+        assert torch.equal(out1[0], out8[row]), row
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_tiled_fused_rope_append_equals_separate_kernels(bs):
+    """The tiled path (batch 8, 32 kv heads: a tile per CU; 7 to 8 splits)
+    with the fused RoPE + append -- the appended tokens staged in LDS, the
+    rest read from the pools -- gives the bits of rope_append followed by
+    paged_attention, and leaves the same pool contents."""
+    from lm.model import LlamaShape, rope_tables
+
+    h = hkv = 32
+    d, batch, t_new = 64, 8, 5
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=10000.0)
+    cos, sin = (x.cuda() for x in rope_tables(shape, 8192))
+    g = torch.Generator().manual_seed(bs)
+    lengths = [4000 - 300 * b for b in range(batch)]
+    blocks = sum((n + t_new) // bs + 2 for n in lengths) + 8
+    caches = [make_cache(1, hkv, d, blocks, bs, torch.bfloat16, 3) for _ in range(2)]
+    hist = [torch.randn(batch, hkv, max(lengths), d, generator=g).to(torch.bfloat16).cuda() for _ in range(2)]
+    qkv = torch.randn(batch, t_new, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16).cuda()
+    ids = list(range(batch))
+    outs = []
+    for which, cache in enumerate(caches):
+        for s in ids:
+            cache.add(s)
+        step = cache.append(ids, lengths)
+        cache.write(0, step, hist[0], hist[1])
+        step = cache.append(ids, [t_new] * batch)
+        out = torch.zeros(batch, t_new, h * d, dtype=torch.bfloat16, device="cuda")
+        x = qkv.clone()
+        if which == 0:
+            ops.rope_append(x, h, hkv, d, cos, sin, step.meta, batch, t_new, cache.table_tensor, bs, cache.k[0],
+                            cache.v[0])
+            ops.paged_attention(x, x.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, t_new,
+                                h, hkv, d, bs, 0.125, step.max_total, out, out.stride(1))
+        else:
+            ops.rope_paged_attention(x, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch,
+                                     t_new, h, hkv, d, bs, 0.125, step.max_total, out, out.stride(1))
+        k_all, v_all = cache.gather(0, step)
+        outs.append((out, k_all, v_all))
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
