@@ -552,8 +552,13 @@ __device__ __forceinline__ void online_update(float (&sv)[N], float &m, float &l
 // combine launch, same bits; or, with a.flat, one split over every key with
 // all 16 waves striding it; or, TILED, all of a tile's 5 to 12 splits in
 // rounds of four (keep_wave_state, fold_tiled), same bits again.
-template <int MODE, int NW, bool TILED = false>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_bf16_kernel(
+// PF (4 waves, 512-token splits, few workgroups): two waves per SIMD, so a
+// wave holds both of its steps' K/V at once -- their loads go out together
+// and the steps are computed in the same order (same bits, one memory
+// round trip fewer).
+template <int MODE, int NW, bool TILED = false, bool PF = false>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(PF ? 2 : 4, PF ? 2 : 4))) void
+attention_bf16_kernel(
     AttnArgs a) {
   TileInfo ti;
   if (!tile_info(a, ti, /*any_split=*/NW == 16)) return;
@@ -607,8 +612,9 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   // all of them are in flight together
   // this wave's first-step block ids: lane j (j = lane & 3) holds the block
   // of tokens c0 + 16j .. c0 + 16j + 15
-  int bj = 0;
+  int bj = 0, bj1 = 0;  // bj1: the second step's (PF)
   if (MODE != 0 && c_first < s_hi) bj = trow[min((c_first + 16 * (lane & 3)) / bs, last_blk)];
+  if (PF && c_first + wstride < s_hi) bj1 = trow[min((c_first + wstride + 16 * (lane & 3)) / bs, last_blk)];
   constexpr int kThreads = NW * kWave;
   constexpr int kKT = (kStage * (kD / 2) + kThreads - 1) / kThreads;  // k pairs per thread
   constexpr int kVT = (kStage * kD + kThreads - 1) / kThreads;        // v elements per thread
@@ -849,12 +855,23 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(4, 4
   constexpr bool tiled = NW == 16 && TILED;
   const int rounds = tiled ? (ti.nsplit + 3) / 4 : 1;
   for (int round = 0;; ++round) {
-    for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
-      StepRegs r;
-      issue(c0, bj, r);
-      // next step's block ids, in flight during this step's arithmetic
-      if (MODE != 0 && c0 + wstride < s_hi) bj = step_blocks(c0 + wstride);
-      compute(c0, r);
+    if constexpr (PF) {  // at most two steps per wave
+      if (c_first < s_hi) {
+        const bool two = c_first + wstride < s_hi;
+        StepRegs r0, r1;
+        issue(c_first, bj, r0);
+        if (two) issue(c_first + wstride, bj1, r1);
+        compute(c_first, r0);
+        if (two) compute(c_first + wstride, r1);
+      }
+    } else {
+      for (int c0 = c_first; c0 < s_hi; c0 += wstride) {
+        StepRegs r;
+        issue(c0, bj, r);
+        // next step's block ids, in flight during this step's arithmetic
+        if (MODE != 0 && c0 + wstride < s_hi) bj = step_blocks(c0 + wstride);
+        compute(c0, r);
+      }
     }
     if (!tiled) break;
     keep_wave_state(s_pool, split_idx, m, l, o);
@@ -1105,6 +1122,13 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
     if (block_size == 16) attention_bf16_kernel<1, 16><<<grid, block, 0, s>>>(a);
     else if (bs16) attention_bf16_kernel<2, 16><<<grid, block, 0, s>>>(a);
     else attention_bf16_kernel<0, 16><<<grid, block, 0, s>>>(a);
+  } else if (dtype == SPECDEC_BF16 && block_size % 16 == 0 && a.split == kDefaultSplit &&
+             units * a.parts <= 2 * (int64_t)cu_count()) {
+    // few workgroups (batch 1 at long contexts): two waves per SIMD is all
+    // the grid fills, so each wave takes both of its steps' loads at once
+    dim3 block(kAttnThreads);
+    if (block_size == 16) attention_bf16_kernel<1, 4, false, true><<<grid, block, 0, s>>>(a);
+    else attention_bf16_kernel<2, 4, false, true><<<grid, block, 0, s>>>(a);
   } else if (dtype == SPECDEC_BF16) {
     dim3 block(kAttnThreads);
     if (block_size == 16) attention_bf16_kernel<1, 4><<<grid, block, 0, s>>>(a);
