@@ -16,7 +16,8 @@ from dataclasses import dataclass
 
 import torch
 
-from cache.paged import BlockAllocator, BlockTable, FragmentationStats, OutOfBlocks, _gpu_device, _TableStore
+from cache.paged import (BlockAllocator, BlockTable, FragmentationStats, OutOfBlocks, _gpu_device, _TableStore,
+                         _upload_i32)
 from specdec import ops
 
 
@@ -147,13 +148,14 @@ class KVCache:
                 alloc._take(needed)
                 table._n += needed
             table.length += n
-        alloc._plan(self._store, pops)
+        rows = [self.tables[s].row for s in seq_ids]
+        host = rows + past + list(n_new)
+        meta = alloc._plan(self._store, pops, tail=host)  # one upload for the plan and the metadata
         if failure is not None:
             raise failure
-        rows = [self.tables[s].row for s in seq_ids]
-        meta = torch.tensor(rows + past + list(n_new), dtype=torch.int32).pin_memory()
-        meta = meta.to(self.device, non_blocking=True).view(3, len(seq_ids))
-        return PagedStep(self, meta, rows, past, list(n_new), width)
+        if meta is None:
+            meta = _upload_i32(host, self.device)
+        return PagedStep(self, meta.view(3, len(seq_ids)), rows, past, list(n_new), width)
 
     def append_steps(self, seq_ids: list[int], steps: list[list[int]]) -> tuple[torch.Tensor, list[PagedStep]]:
         """Reserve slots for several consecutive appends at once, as if
@@ -184,10 +186,11 @@ class KVCache:
                 break
             host += rows + past + list(n_new)
             infos.append((past, list(n_new)))
-        alloc._plan(self._store, pops)
+        metas = alloc._plan(self._store, pops, tail=host)
         if failure is not None:
             raise failure
-        metas = torch.tensor(host, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
+        if metas is None:
+            metas = _upload_i32(host, self.device)
         metas = metas.view(len(steps), 3, len(seq_ids))
         out = [PagedStep(self, metas[i], rows, past, n_new, max(n_new)) for i, (past, n_new) in enumerate(infos)]
         return metas, out

@@ -41,7 +41,8 @@ def _gpu_device(device) -> torch.device:
 
 
 def _upload_i32(values: list[int], device: torch.device) -> torch.Tensor:
-    host = torch.tensor(values, dtype=torch.int32).pin_memory()
+    """An int32 device copy of `values`, staged straight into pinned memory."""
+    host = torch.tensor(values, dtype=torch.int32, pin_memory=True)
     return host.to(device, non_blocking=True)
 
 
@@ -101,9 +102,14 @@ class BlockAllocator:
         return self.num_blocks - self._free
 
     # -- device plan ---------------------------------------------------------
-    def _plan(self, store: _TableStore | None, pops: list[tuple[int, int, int]], popped=None) -> None:
+    def _plan(self, store: _TableStore | None, pops: list[tuple[int, int, int]], popped=None,
+              tail: list[int] | None = None) -> torch.Tensor | None:
         """Apply every queued push (grouped per store, in order) and then `pops`
-        (row, col, count) on `store`, in one launch per store."""
+        (row, col, count) on `store`, in one launch per store.  `tail` (int32
+        values the caller needs on the device, e.g. a forward's row metadata)
+        rides in the last launch's upload; its device copy is returned, or
+        None when nothing was launched."""
+        tail_dev = None
         groups: list[tuple[_TableStore, list[tuple[int, int, int]]]] = []
         for st, row, col, cnt in self._pending:
             if groups and groups[-1][0] is st:
@@ -128,9 +134,15 @@ class BlockAllocator:
                 off += cnt
             if not entries:
                 continue
-            ops.block_plan(st.tensor, self._stack, self._used, self._dev_top, _upload_i32(entries, self.device),
-                           len(pushes), len(these_pops), popped if last else None)
+            if last and tail is not None:
+                both = _upload_i32(entries + tail, self.device)
+                up, tail_dev = both[: len(entries)], both[len(entries):]
+            else:
+                up = _upload_i32(entries, self.device)
+            ops.block_plan(st.tensor, self._stack, self._used, self._dev_top, up, len(pushes), len(these_pops),
+                           popped if last else None)
             self._dev_top += pushed - off
+        return tail_dev
 
     def _queue_push(self, store: _TableStore, row: int, col: int, count: int) -> None:
         if count > 0:
