@@ -319,13 +319,18 @@ def test_split_workspace_shared_across_shapes():
                 assert err < 2e-2, (i, err)
 
 
-def test_split_graph_replays_match_eager():
-    """A split-path call (split kernel + combine) captured in a HIP graph:
-    each replay -- with eager calls of another shape on the same workspace
-    in between -- gives the eager bits."""
+@pytest.mark.parametrize("shape", ["split", "tiled"])
+def test_split_graph_replays_match_eager(shape):
+    """A split-path call (split kernel + combine; or, at batch 8, one tiled
+    launch) captured in a HIP graph: each replay -- with eager calls of
+    another shape on the same workspace in between -- gives the eager
+    bits."""
     from lm.graphs import _capture
 
-    cache, step, q = _filled(2, [5000, 2600], seed=61)
+    if shape == "split":
+        cache, step, q = _filled(2, [5000, 2600], seed=61)
+    else:
+        cache, step, q = _filled(8, [3000 + 100 * b for b in range(8)], seed=63)
     other = _filled(3, [2600, 700, 4500], seed=62)
     ws = ops.AttentionWorkspace(torch.device("cuda"))
     ws.reserve(1 << 24)  # no growth inside the capture
