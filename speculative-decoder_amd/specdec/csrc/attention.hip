@@ -1099,7 +1099,7 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   // workgroup per tile takes all of its splits, no partials, no combine
   a.tiled = dtype == SPECDEC_BF16 && !a.flat && block_size % 16 == 0 && a.max_splits > 4 &&
             a.max_splits <= kTSplits && a.n_qtiles == 1 && width * (n_heads / n_kv_heads) <= kTRows &&
-            units >= cu_count();
+            cu_count() > 0 && units >= cu_count();
   // bf16 tiles with at most four splits (or one flat split, or tiled) run
   // in one 16-wave workgroup; otherwise one 4-wave workgroup per split +
   // combine
