@@ -234,19 +234,19 @@ __device__ int64_t inverse_cdf_row(Elem elem, int64_t vocab, T u, double *scratc
 }
 
 // fp32 rows of up to kRegTiles * 4096 elements: the whole row stays in
-// registers.  vals[j][e] is element j*4096 + 4*tid + e (coalesced loads).
-// The CDF needs each thread to own a contiguous run, so the row passes
-// through LDS a chunk (4 tiles, 16384 elements) at a time: thread t takes
-// elements 16t..16t+15 of the chunk, sums them sequentially in fp64, and
-// one workgroup exclusive scan per chunk gives every thread the prefix at
-// the start of its run.  The target is taken from the prefix of the last
-// element computed the same way, and the answer is the number of prefixes
-// (rounded to fp32) that do not exceed it.
+// registers, in runs.  The row is three chunks of 16384 elements; thread t
+// owns the contiguous run 16t .. 16t+15 of each chunk, and vals[j][e] is
+// element (j / 4) * 16384 + 16t + 4 (j % 4) + e.  A run is summed
+// sequentially in fp64, one workgroup exclusive scan per chunk (the three
+// interleaved) gives every thread the prefix at the start of its runs, and
+// the answer is the number of prefixes (rounded to fp32) that do not
+// exceed the target, which is taken from the prefix of the last element
+// computed the same way.
 constexpr int kRegTiles = 12;  // rows up to 49152 elements
 constexpr int kChunkTiles = 4;
 constexpr int kChunk = kChunkTiles * kAcceptThreads * kCdfPerThread;  // 16384
 constexpr int kRun = kChunk / kAcceptThreads;                          // 16 per thread
-__device__ __forceinline__ int lds_pad(int k) { return k + (k >> 5); }
+constexpr int kChunks = kRegTiles / kChunkTiles;                       // 3
 
 // A row read through a raw buffer descriptor of `elems` fp32 elements:
 // loads past its end return 0 (the hardware range check on the vector
@@ -257,12 +257,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const float *row, u
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), 0, (int)(elems * 4u), 0x00020000);
 }
 
-// Elements 4*tid .. 4*tid+3 of tile j of a row (the layout of vals[j][e]):
-// one 16-byte load when the row length is a multiple of 4 (a load then never
-// straddles the row's end), else four 4-byte loads.
+// Element index of vals[j][e] for thread tid.
+__device__ __forceinline__ int run_elem(int j, int tid, int e) {
+  return (j / kChunkTiles) * kChunk + kRun * tid + kCdfPerThread * (j % kChunkTiles) + e;
+}
+
+// vals[j][0..3] of a row for thread tid: one 16-byte load when the row
+// length is a multiple of 4 (a load then never straddles the row's end),
+// else four 4-byte loads.  A wave's 16-byte loads cover 64 runs 64 bytes
+// apart; its four loads of a chunk together read every byte of 4 KB.
 template <bool VEC4>
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rb, int j, int tid, float (&out)[kCdfPerThread]) {
-  const unsigned off = (unsigned)(j * kAcceptThreads * kCdfPerThread + kCdfPerThread * tid) * 4u;
+__device__ __forceinline__ void load_run(__amdgpu_buffer_rsrc_t rb, int j, int tid, float (&out)[kCdfPerThread]) {
+  const unsigned off = (unsigned)run_elem(j, tid, 0) * 4u;
   if (VEC4) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
 #pragma unroll
@@ -274,43 +280,68 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rb, int j, int 
   }
 }
 
-__device__ __forceinline__ int64_t inverse_cdf_regs(const float (&vals)[kRegTiles][kCdfPerThread], int64_t vocab, float u,
-                                    double *scratch, float *lds) {
+__device__ __forceinline__ int64_t inverse_cdf_regs(const float (&vals)[kRegTiles][kCdfPerThread], int64_t vocab,
+                                                     float u, double *scratch) {
+  __shared__ double s_wave[kAcceptThreads / kWave][kChunks];  // each wave's inclusive run-sum total, per chunk
   __shared__ double s_total;
-  const int tid = threadIdx.x;
-  const int tile = kAcceptThreads * kCdfPerThread;
+  // the runs of chunks 1 and 2 wait out the scans here, each thread in its
+  // own column (element m of thread t at [m][t]: no bank conflicts, no
+  // barrier), which frees their registers
+  __shared__ float s_park[kChunks - 1][kRun][kAcceptThreads];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int nchunks = (int)((vocab + kChunk - 1) / kChunk);
-  float mine[kRegTiles / kChunkTiles][kRun];
-  double base[kRegTiles / kChunkTiles];
-  double carry = 0.0;
+  auto elem = [&](int c, int m) -> float {
+    return c == 0 ? vals[m / kCdfPerThread][m % kCdfPerThread] : s_park[c - 1][m][tid];
+  };
+  // run sums, then the three chunks' scans interleaved: an inclusive scan in
+  // the wave (Hillis-Steele over shuffles), the waves' totals through LDS --
+  // block_exclusive_scan's arithmetic, one barrier pair for all three
+  double x[kChunks];
 #pragma unroll
-  for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
-    if (c >= nchunks) break;
-    __syncthreads();
+  for (int c = 0; c < kChunks; ++c) {
+    double a = 0.0;
 #pragma unroll
-    for (int jj = 0; jj < kChunkTiles; ++jj)
+    for (int m = 0; m < kRun; ++m) a += (double)vals[kChunkTiles * c + m / kCdfPerThread][m % kCdfPerThread];
+    x[c] = a;
+  }
 #pragma unroll
-      for (int e = 0; e < kCdfPerThread; ++e) lds[lds_pad(jj * tile + kCdfPerThread * tid + e)] = vals[c * kChunkTiles + jj][e];
-    __syncthreads();
-    double local = 0.0;
+  for (int c = 1; c < kChunks; ++c)
 #pragma unroll
-    for (int m = 0; m < kRun; ++m) {
-      mine[c][m] = lds[lds_pad(kRun * tid + m)];
-      local += (double)mine[c][m];
+    for (int m = 0; m < kRun; ++m) s_park[c - 1][m][tid] = vals[kChunkTiles * c + m / kCdfPerThread][m % kCdfPerThread];
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1)
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const double y = __shfl_up(x[c], o, kWave);
+      if (lane >= o) x[c] += y;
     }
-    double total;
-    base[c] = carry + block_exclusive_scan(local, scratch, &total);
-    carry += total;
+  __syncthreads();
+  if (lane == kWave - 1)
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) s_wave[wid][c] = x[c];
+  __syncthreads();
+  double base[kChunks], carry = 0.0;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    double wave_prefix = 0.0, all = 0.0;
+    for (int w = 0; w < kAcceptThreads / kWave; ++w) {
+      if (w < wid) wave_prefix += s_wave[w][c];
+      all += s_wave[w][c];
+    }
+    double excl = __shfl_up(x[c], 1, kWave);
+    if (lane == 0) excl = 0.0;
+    base[c] = carry + (wave_prefix + excl);
+    carry += all;
   }
   // the prefix of the row's last element (zeros pad the last chunk)
   if (tid == kAcceptThreads - 1) {
     double acc = base[0];
 #pragma unroll
-    for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
+    for (int c = 0; c < kChunks; ++c) {
       if (c != nchunks - 1) continue;
       acc = base[c];
 #pragma unroll
-      for (int m = 0; m < kRun; ++m) acc += (double)mine[c][m];
+      for (int m = 0; m < kRun; ++m) acc += (double)elem(c, m);
     }
     s_total = acc;
   }
@@ -318,17 +349,16 @@ __device__ __forceinline__ int64_t inverse_cdf_regs(const float (&vals)[kRegTile
   const float target = u * (float)s_total;
   int count = 0;
 #pragma unroll
-  for (int c = 0; c < kRegTiles / kChunkTiles; ++c) {
+  for (int c = 0; c < kChunks; ++c) {
     if (c >= nchunks) break;
     double acc = base[c];
 #pragma unroll
     for (int m = 0; m < kRun; ++m) {
-      acc += (double)mine[c][m];
+      acc += (double)elem(c, m);
       const int64_t idx = (int64_t)c * kChunk + kRun * tid + m;
       if (idx < vocab && (float)acc <= target) ++count;
     }
   }
-  __syncthreads();
   const int64_t idx = (int64_t)block_sum((double)count, scratch);
   return idx > vocab - 1 ? vocab - 1 : idx;
 }
@@ -372,7 +402,6 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
     int64_t q_rs, const int64_t *__restrict__ draft, const float *__restrict__ u_accept,
     const float *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab, int64_t *__restrict__ out) {
   __shared__ double scratch[kAcceptThreads / kWave + 1];
-  __shared__ float lds[kChunk + kChunk / 32];
   __shared__ int64_t s_n;
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -392,7 +421,6 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
   // read and its values are not used
   const bool has_q = n < k;
   const float *qr = has_q ? q + b * q_bs + n * q_rs : pr;
-  const int tile = kAcceptThreads * kCdfPerThread;
   // Every load of both rows goes out before the first is used, with no
   // branch between them (elements past the vocab read as 0 through the
   // buffer descriptors): one memory round trip for the row pair instead of
@@ -401,8 +429,8 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
   float vals[kRegTiles][kCdfPerThread], qv[kRegTiles][kCdfPerThread];
 #pragma unroll
   for (int j = 0; j < kRegTiles; ++j) {
-    load_tile<VEC4>(pb, j, tid, vals[j]);
-    load_tile<VEC4>(qb, j, tid, qv[j]);
+    load_run<VEC4>(pb, j, tid, vals[j]);
+    load_run<VEC4>(qb, j, tid, qv[j]);
   }
   double local = 0.0;
 #pragma unroll
@@ -421,11 +449,11 @@ __global__ __launch_bounds__(kAcceptThreads) void accept_reject_regs_kernel(
   for (int j = 0; j < kRegTiles; ++j)
 #pragma unroll
     for (int e = 0; e < kCdfPerThread; ++e) {
-      const int64_t i = (int64_t)j * tile + kCdfPerThread * tid + e;
+      const int64_t i = run_elem(j, tid, e);
       if (use_residual) vals[j][e] = vals[j][e] / denom;
       else vals[j][e] = i < vocab ? pr[i] : 0.0f;  // p == q: fall back to p (rare: reloaded)
     }
-  const int64_t idx = inverse_cdf_regs(vals, vocab, u_residual[b], scratch, lds);
+  const int64_t idx = inverse_cdf_regs(vals, vocab, u_residual[b], scratch);
   if (tid == 0) out[batch + b] = idx;
 }
 
@@ -435,15 +463,13 @@ __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_regs_kernel
                                                                                  const float *__restrict__ u,
                                                                                  int64_t *__restrict__ out) {
   __shared__ double scratch[kAcceptThreads / kWave + 1];
-  __shared__ float lds[kChunk + kChunk / 32];
   const int64_t b = blockIdx.x;
   const float *row = probs + b * row_stride;
-  const int tile = kAcceptThreads * kCdfPerThread;
   float vals[kRegTiles][kCdfPerThread];
   const __amdgpu_buffer_rsrc_t rb = row_buffer(row, (unsigned)vocab);  // zeros past the vocab
 #pragma unroll
-  for (int j = 0; j < kRegTiles; ++j) load_tile<VEC4>(rb, j, threadIdx.x, vals[j]);
-  const int64_t idx = inverse_cdf_regs(vals, vocab, u[b], scratch, lds);
+  for (int j = 0; j < kRegTiles; ++j) load_run<VEC4>(rb, j, threadIdx.x, vals[j]);
+  const int64_t idx = inverse_cdf_regs(vals, vocab, u[b], scratch);
   if (threadIdx.x == 0) out[b] = idx;
 }
 
