@@ -65,7 +65,7 @@ __device__ __forceinline__ int block_argmax(float best, int best_i, float *red_f
   return red_i[0];
 }
 
-template <typename TIn>
+template <typename TIn, bool UNIT_T = false>
 __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
     const TIn *__restrict__ logits, int64_t row_stride, int64_t vocab, float temperature,
     float *__restrict__ out, int64_t out_stride, int64_t *__restrict__ index_out, int64_t index_stride) {
@@ -104,23 +104,40 @@ __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
   // softmax(logits.float() / T): exp(v - m) is evaluated as
   // 2^((v - m) * log2 e) on the hardware exp2 (about 1e-6 relative for the
   // shifts that matter)
+  // x / 1 is x exactly (NaN and infinities too), so the temperature-1
+  // instance (UNIT_T) skips the divisions
   if (fits) {
     const int last = (int)vocab - 1;
     float v[kSoftPer];
 #pragma unroll
     for (int k = 0; k < kSoftPer; ++k) v[k] = to_f32(x[min(k * kSoftmaxThreads + tid, last)]);
-    float m = -INFINITY;
+    float m = -INFINITY, sum = 0.0f;
+    if constexpr (UNIT_T) {
+      // positions past the vocab hold copies of its last element (the clamp
+      // above): they leave the max alone, and their terms are zeroed below
+      // (adding +0 to the sum changes no bit, as the exp2(-inf) = 0 of a
+      // masked score would not)
 #pragma unroll
-    for (int k = 0; k < kSoftPer; ++k) {
-      v[k] = (k * kSoftmaxThreads + tid < vocab) ? v[k] / temperature : -INFINITY;
-      m = fmaxf(m, v[k]);
-    }
-    const float mg = block_max(m, red_f);
-    float sum = 0.0f;
+      for (int k = 0; k < kSoftPer; ++k) m = fmaxf(m, v[k]);
+      const float mg = block_max(m, red_f);
 #pragma unroll
-    for (int k = 0; k < kSoftPer; ++k) {
-      v[k] = __builtin_amdgcn_exp2f((v[k] - mg) * kLog2e);
-      sum += v[k];
+      for (int k = 0; k < kSoftPer; ++k) {
+        const float e = __builtin_amdgcn_exp2f((v[k] - mg) * kLog2e);
+        v[k] = k * kSoftmaxThreads + tid < vocab ? e : 0.0f;
+        sum += v[k];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kSoftPer; ++k) {
+        v[k] = (k * kSoftmaxThreads + tid < vocab) ? v[k] / temperature : -INFINITY;
+        m = fmaxf(m, v[k]);
+      }
+      const float mg = block_max(m, red_f);
+#pragma unroll
+      for (int k = 0; k < kSoftPer; ++k) {
+        v[k] = __builtin_amdgcn_exp2f((v[k] - mg) * kLog2e);
+        sum += v[k];
+      }
     }
     const float inv = 1.0f / block_sum(sum, red_f);
 #pragma unroll
@@ -134,7 +151,7 @@ __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
   // then a second pass that writes
   float m = -INFINITY, sum = 0.0f;
   for (int64_t i = tid; i < vocab; i += blockDim.x) {
-    const float v = to_f32(x[i]) / temperature;
+    const float v = UNIT_T ? to_f32(x[i]) : to_f32(x[i]) / temperature;
     if (v > m) {
       sum = (m == -INFINITY) ? 0.0f : sum * __builtin_amdgcn_exp2f((m - v) * kLog2e);
       m = v;
@@ -145,7 +162,7 @@ __global__ __launch_bounds__(kSoftmaxThreads) void probabilities_kernel(
   sum = (m == -INFINITY) ? 0.0f : sum * __builtin_amdgcn_exp2f((m - mg) * kLog2e);
   const float inv = 1.0f / block_sum(sum, red_f);
   for (int64_t i = tid; i < vocab; i += blockDim.x)
-    y[i] = __builtin_amdgcn_exp2f((to_f32(x[i]) / temperature - mg) * kLog2e) * inv;
+    y[i] = __builtin_amdgcn_exp2f(((UNIT_T ? to_f32(x[i]) : to_f32(x[i]) / temperature) - mg) * kLog2e) * inv;
 }
 
 // ------------------------------------------- accept stage (per batch) ----
@@ -571,8 +588,13 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
   hipStream_t s = as_stream(stream);
   switch (dtype) {
     case SPECDEC_F32:
-      probabilities_kernel<float><<<grid, block, 0, s>>>((const float *)logits, row_stride, vocab,
-                                                        temperature, out, out_stride, index_out, index_stride);
+      if (temperature == 1.0f)
+        probabilities_kernel<float, true><<<grid, block, 0, s>>>((const float *)logits, row_stride, vocab,
+                                                                temperature, out, out_stride, index_out,
+                                                                index_stride);
+      else
+        probabilities_kernel<float><<<grid, block, 0, s>>>((const float *)logits, row_stride, vocab,
+                                                          temperature, out, out_stride, index_out, index_stride);
       break;
     case SPECDEC_F64:
       probabilities_kernel<double><<<grid, block, 0, s>>>((const double *)logits, row_stride, vocab,
