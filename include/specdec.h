@@ -50,7 +50,7 @@ extern "C" {
 #define SPECDEC_BF16 2
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 5). */
+ * below changes (currently 6). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -208,6 +208,18 @@ int specdec_add_rmsnorm(void *hidden, const void *delta, const void *weight, voi
 int specdec_silu_mul(const void *gate_up, void *out, int dtype, int64_t rows, int64_t inter,
                      void *stream);
 
+/* The post-attention RMSNorm and the MLP activation around a gate/up
+ * projection of the unnormalised residual stream (lm/forward.py:64-65, with
+ * transformers' LlamaRMSNorm and LlamaMLP).  gate_up [rows, 2*inter] holds
+ * hidden @ (W diag(norm weight))^T; per row, s = rsqrt(mean(hidden^2) + eps)
+ * over hidden [rows, dim], then gate = round(s * gate), up = round(s * up) and
+ * out [rows, inter] = round(round(silu(gate)) * up).  Algebraically the same
+ * as normalising before the projection; the rounding points differ.  The row
+ * sum of squares is reduced in one fixed order, so a row's result does not
+ * depend on the other rows of the call. */
+int specdec_rms_silu_mul(const void *gate_up, const void *hidden, void *out, int dtype, int64_t rows,
+                         int64_t inter, int64_t dim, float eps, void *stream);
+
 /* -------------------------------------------------------------- attention --- */
 
 /* Workspace needed by specdec_paged_attention for a call shape: `floats`
@@ -259,9 +271,18 @@ int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
  * tokens' rotated k and their v for its kv head and split into the paged
  * pools (identical values where workgroups overlap), so one launch per layer
  * replaces two.  Same rounding as the two separate kernels.
- * Replaces lm/forward.py:53,60-63 + cache/kv.py:101-112. */
+ * With `hidden` not null, the layer's input RMSNorm is finished here too:
+ * qkv is then a projection of hidden [batch, width, hidden_dim] bf16 (the
+ * unnormalised residual stream) with the norm weight folded into the
+ * projection, and every new token's q, k and v are multiplied by
+ * s = rsqrt(mean(hidden^2) + eps) of its row and rounded to bf16 before
+ * RoPE.  Needs bf16, block_size % 16 == 0 and width <= 16 (else
+ * SPECDEC_EUNSUPPORTED); hidden_dim % 8 == 0 and hidden 16-byte aligned.
+ * Replaces lm/forward.py:53,60-63 + cache/kv.py:101-112 (and the decoder
+ * layer's input_layernorm). */
 int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
                                  const float *cos_table, const float *sin_table,
+                                 const void *hidden, int64_t hidden_dim, float eps,
                                  void *k_pool, void *v_pool, const int32_t *tables,
                                  int64_t table_stride, const int32_t *meta, int32_t batch,
                                  int32_t width, int32_t n_heads, int32_t n_kv_heads,

@@ -3,13 +3,21 @@
 A forward is split in two:
   * host part: `cache.append` decides block growth (one block-plan launch)
     and uploads the per-row metadata (table row, past length, new tokens);
-  * device part, `forward_core`: eight launches per layer (nine when the
-    attention needs its split combine) -- fused residual add + RMSNorm, one
-    fused QKV GEMM (torch/hipBLASLt), the paged verify-attention kernel that
-    also applies RoPE and appends the new K/V to the paged pools and reads
-    K/V blocks in place (no gather copy, no materialised mask), o_proj, add
-    + RMSNorm, the gate/up GEMM, SiLU*up, the down GEMM -- then the fp32
-    output projection (lm/forward.py:71-84).
+  * device part, `forward_core`: six launches per layer for decode,
+    verification and draft steps (seven when the attention needs its split
+    combine): the fused QKV GEMM (torch/hipBLASLt) of the unnormalised
+    residual stream; the paged verify-attention kernel, which finishes the
+    input RMSNorm (each token's q/k/v scaled by its row's rsqrt(mean(x^2) +
+    eps)), applies RoPE, appends the new K/V to the paged pools and reads
+    K/V blocks in place (no gather copy, no materialised mask); o_proj
+    accumulated into the residual stream by the GEMM itself (beta = 1); the
+    gate/up GEMM of the unnormalised stream; one kernel that finishes the
+    post-attention norm and applies SiLU*up; the down GEMM, again
+    accumulated into the stream -- then the final norm and the fp32 output
+    projection (lm/forward.py:71-84).  The norm weights live in the
+    projections' columns (lm/model.py:Layer).  Prefill (more than 16 new
+    tokens) and fp32 models normalise in a kernel of their own instead,
+    without the weight.
 The device part reads everything it needs from device memory, so a fixed
 (batch, width) shape can be captured once in a HIP graph and replayed
 (lm/graphs.py).
@@ -41,6 +49,18 @@ def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool) -> torch.Tensor:
     return F.linear(x, w)
 
 
+def _project_add(hidden: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemv: bool) -> None:
+    """hidden += x @ w.T inside the GEMM (beta = 1, in place), rounded once:
+    a residual add without a kernel of its own.
+    A 5-row call's rows have the bits of the same rows projected alone, as
+    with `_project`."""
+    n, k = w.shape
+    if gemv and x.numel() == k:
+        hidden.view(n).addmv_(w, x.reshape(k))
+    else:
+        hidden.view(-1, n).addmm_(x.reshape(-1, k), w.t())
+
+
 def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Tensor, max_kv_len: int,
                  last: torch.Tensor | None = None, workspace: ops.AttentionWorkspace | None = None,
                  split_tokens: int = 0) -> torch.Tensor:
@@ -61,18 +81,26 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     layers = llama.layers
     hidden = F.embedding(ids, llama.embed)
     x = torch.empty_like(hidden)
-    ops.add_rmsnorm(hidden, None, layers[0].ln1, x, eps)
+    # the attention finishes the input norm for decode-sized calls; else a
+    # weightless norm kernel writes x and the projection reads that
+    in_attn = ops.norm_in_attention(hidden.dtype, cache.block_size, t)
+    if not in_attn:
+        ops.add_rmsnorm(hidden, None, llama.unit_norm, x, eps)
     attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
     act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
     for i, layer in enumerate(layers):
-        qkv = _project(x, layer.wqkv, gemv)
+        qkv = _project(hidden if in_attn else x, layer.wqkv, gemv)
         ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t, h,
                                  hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
-                                 split_tokens)
-        ops.add_rmsnorm(hidden, _project(attn, layer.wo, gemv), layer.ln2, x, eps)
-        ops.silu_mul(_project(x, layer.wgu, gemv), act)
-        nxt = layers[i + 1].ln1 if i + 1 < len(layers) else llama.norm
-        ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), nxt, x, eps)
+                                 split_tokens, norm_of=hidden if in_attn else None, eps=eps)
+        _project_add(hidden, attn, layer.wo, gemv)
+        ops.rms_silu_mul(_project(hidden, layer.wgu, gemv), hidden, act, eps)
+        if i + 1 == len(layers):
+            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.norm, x, eps)
+        elif in_attn:
+            _project_add(hidden, act, layer.wd, gemv)
+        else:
+            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.unit_norm, x, eps)
     if last is not None:
         x = x[torch.arange(b, device=x.device), last]
     return logits(llama, x)

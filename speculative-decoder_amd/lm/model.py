@@ -106,12 +106,25 @@ def perturbed_truncation(state: dict[str, torch.Tensor], shape: LlamaShape, n_la
 
 @dataclass
 class Layer:
+    """One decoder layer.  The two RMSNorm weights are folded into the
+    columns of the projections that read the norms' outputs (W diag(ln), one
+    rounding to the weight dtype; exact for the unit weights of a fresh
+    model), because the forward projects the unnormalised residual stream
+    and finishes each norm after the projection: RMSNorm(x) @ W^T =
+    rsqrt(mean(x^2) + eps) * (x @ (W diag(ln))^T)."""
     ln1: torch.Tensor
-    wqkv: torch.Tensor
+    wqkv: torch.Tensor  # q/k/v [(H + 2 Hkv) d, hidden], ln1 folded in
     wo: torch.Tensor
     ln2: torch.Tensor
-    wgu: torch.Tensor
+    wgu: torch.Tensor  # gate/up [2 * intermediate, hidden], ln2 folded in
     wd: torch.Tensor
+
+
+def fold_norm(w: torch.Tensor, ln: torch.Tensor) -> torch.Tensor:
+    """W diag(ln): the norm weight multiplied into W's columns, in fp32 or
+    wider, then rounded once to W's dtype."""
+    wide = torch.promote_types(w.dtype, torch.float32)
+    return (w.to(wide) * ln.to(wide)).to(w.dtype).contiguous()
 
 
 @dataclass
@@ -127,6 +140,13 @@ class Llama:
     head_wide: torch.Tensor
     rope_cos: torch.Tensor = field(repr=False)
     rope_sin: torch.Tensor = field(repr=False)
+    # a norm weight of ones: RMSNorm without its weight, for the calls whose
+    # projection (holding the folded weight) reads a normalised input
+    unit_norm: torch.Tensor = field(repr=False, default=None)
+
+    def __post_init__(self):
+        if self.unit_norm is None:
+            self.unit_norm = torch.ones(self.config.hidden_size, dtype=self.embed.dtype, device=self.embed.device)
 
     @property
     def device(self) -> torch.device:
@@ -158,11 +178,12 @@ class Llama:
         layers = []
         for n in range(shape.num_hidden_layers):
             p = f"model.layers.{n}."
+            ln1, ln2 = get(p + "input_layernorm.weight"), get(p + "post_attention_layernorm.weight")
             wqkv = torch.cat([get(p + "self_attn.q_proj.weight"), get(p + "self_attn.k_proj.weight"),
-                              get(p + "self_attn.v_proj.weight")], dim=0).contiguous()
-            wgu = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], dim=0).contiguous()
-            layers.append(Layer(get(p + "input_layernorm.weight"), wqkv, get(p + "self_attn.o_proj.weight"),
-                                get(p + "post_attention_layernorm.weight"), wgu, get(p + "mlp.down_proj.weight")))
+                              get(p + "self_attn.v_proj.weight")], dim=0)
+            wgu = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], dim=0)
+            layers.append(Layer(ln1, fold_norm(wqkv, ln1), get(p + "self_attn.o_proj.weight"), ln2,
+                                fold_norm(wgu, ln2), get(p + "mlp.down_proj.weight")))
         head = embed if shape.tie_word_embeddings else get("lm_head.weight")
         if head.is_cuda and head.dtype in (torch.bfloat16, torch.float16):
             wide = head

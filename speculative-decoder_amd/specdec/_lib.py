@@ -30,15 +30,16 @@ SIGNATURES: dict[str, list] = {
     "specdec_kv_gather": [P, P, c_int, I32, I32, P, I32, P, I64, I32, I32, P, P, P],
     "specdec_add_rmsnorm": [P, P, P, P, c_int, I64, I64, c_float, P],
     "specdec_silu_mul": [P, P, c_int, I64, I64, P],
+    "specdec_rms_silu_mul": [P, P, P, c_int, I64, I64, I64, c_float, P],
     "specdec_attention_workspace": [I32, I32, I32, I32, I32, I32, I32, P],
     "specdec_attention_split": [I32, I32, I32, I32, I32],
     "specdec_paged_attention": [P, c_int, I64, P, P, P, I64, P, I32, I32, I32, I32, I32, I32, c_float,
                                 I32, I32, P, I64, P, I64, P],
-    "specdec_rope_paged_attention": [P, c_int, I64, P, P, P, P, P, I64, P, I32, I32, I32, I32, I32, I32, c_float,
-                                     I32, I32, P, I64, P, I64, P],
+    "specdec_rope_paged_attention": [P, c_int, I64, P, P, P, I64, c_float, P, P, P, I64, P, I32, I32, I32, I32, I32,
+                                     I32, c_float, I32, I32, P, I64, P, I64, P],
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _lib: ctypes.CDLL | None = None
 
 

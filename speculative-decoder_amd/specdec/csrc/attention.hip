@@ -64,6 +64,12 @@ struct AttnArgs {
   int rope;
   const float *cos_t;
   const float *sin_t;
+  // input RMSNorm finished here (rope calls only; null: q/k/v are already
+  // normalised): hidden [batch, width, hdim] bf16 is the residual stream the
+  // q/k/v projection read, its norm weight folded into the projection
+  const void *hidden;
+  int hdim;
+  float eps;
   const void *k;
   const void *v;
   const int32_t *tables;
@@ -662,16 +668,60 @@ attention_bf16_kernel(
     }
     qop[0] = __builtin_bit_cast(bf16x8, raw[0]);
     qop[1] = __builtin_bit_cast(bf16x8, raw[1]);
-    if (a.rope && row_ok) {
-      const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
-      const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
+  }
+
+  // Input RMSNorm finished here (a.hidden): q, k and v come from a
+  // projection of the unnormalised residual stream, so each new token's
+  // values are scaled by s = rsqrt(mean(hidden^2) + eps) of its row, rounded
+  // to bf16 as a projection's output is, before RoPE.  Wave w reduces tokens
+  // w, w + NW, ... (the host allows at most kStage new tokens): lane l adds
+  // the row's 16-byte vectors l, l+64, ... in order, then a butterfly -- one
+  // fixed order, so every workgroup of every call gets the same s for a
+  // token, and the same s the MLP's norm kernel computes for a row.
+  __shared__ float s_tok[kStage];
+  const bool norm_in = MODE != 0 && a.hidden;  // the host sends no other
+  if (norm_in) {
+    const int nvec = a.hdim / 8;
+    const int ntok = min(min(ti.nnew, a.width), kStage);
+    for (int tk = tid >> 6; tk < ntok; tk += NW) {
+      const u32x4 *hr = reinterpret_cast<const u32x4 *>(a.hidden) + ((int64_t)ti.b * a.width + tk) * nvec;
+      float ss = 0.0f;
+      for (int base = 0; base < nvec; base += 4 * kWave) {
+        u32x4 hv[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float y1, y2;
-        rope_pair((float)qop[0][j], (float)qop[1][j], cs[j], sn[j], y1, y2);
-        qop[0][j] = (__bf16)y1;
-        qop[1][j] = (__bf16)y2;
+        for (int k = 0; k < 4; ++k) hv[k] = hr[min(base + lane + kWave * k, nvec - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const bool in = base + lane + kWave * k < nvec;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const unsigned w = hv[k][e >> 1];
+            const float x = __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+            ss += in ? x * x : 0.0f;
+          }
+        }
       }
+      ss = wave_sum(ss);
+      if (lane == 0) s_tok[tk] = rsqrtf(ss / (float)a.hdim + a.eps);
+    }
+    __syncthreads();
+  }
+  // v * s rounded to bf16 (raw bits in and out)
+  auto scaled_bits = [&](u16 bits, float sc) -> u16 {
+    return __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(sc * to_f32(__builtin_bit_cast(__hip_bfloat16, bits))));
+  };
+
+  if (a.rope && row_ok) {
+    const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
+    const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
+    const float sq = norm_in ? s_tok[t] : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float x1 = (float)qop[0][j], x2 = (float)qop[1][j], y1, y2;
+      if (norm_in) x1 = (float)(__bf16)(sq * x1), x2 = (float)(__bf16)(sq * x2);
+      rope_pair(x1, x2, cs[j], sn[j], y1, y2);
+      qop[0][j] = (__bf16)y1;
+      qop[1][j] = (__bf16)y2;
     }
   }
 
@@ -683,6 +733,11 @@ attention_bf16_kernel(
       const int task = tid + u * kThreads;
       if (task < n_in * (kD / 2)) {
         const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
+        if (norm_in) {
+          const float st = s_tok[pos - ti.past];
+          sk1[u] = scaled_bits(sk1[u], st);
+          sk2[u] = scaled_bits(sk2[u], st);
+        }
         float y1, y2;
         rope_pair(to_f32(__builtin_bit_cast(__hip_bfloat16, sk1[u])), to_f32(__builtin_bit_cast(__hip_bfloat16, sk2[u])),
                   scs[u], ssn[u], y1, y2);
@@ -700,6 +755,7 @@ attention_bf16_kernel(
       const int task = tid + u * kThreads;
       if (task < n_in * kD) {
         const int pos = p0 + task / kD, dd = task % kD;
+        if (norm_in) svv[u] = scaled_bits(svv[u], s_tok[pos - ti.past]);
         s_nv[pos - p0][dd] = svv[u];
         vpw[((int64_t)svb[u] * Hkv + ti.h) * tile_elems + (int64_t)dd * bs + pos % bs] = svv[u];
       }
@@ -1078,6 +1134,12 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
       block_size <= 0 || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (head_dim != kD) return SPECDEC_EUNSUPPORTED;
+  if (a.hidden) {
+    // the scales are computed in the staged prologue: bf16, whole 16-token
+    // block groups, every new token of a row staged in LDS
+    if (dtype != SPECDEC_BF16 || block_size % 16 != 0 || width > kStage) return SPECDEC_EUNSUPPORTED;
+    if (a.hdim <= 0 || a.hdim % 8 != 0 || ((uintptr_t)a.hidden & 15) != 0) return SPECDEC_EINVAL;
+  }
   if (batch == 0 || width == 0 || max_kv_len == 0) return SPECDEC_OK;
   if (!a.q || !a.k || !a.v || !a.tables || !a.meta || !a.out) return SPECDEC_EINVAL;
   a.batch = batch;
@@ -1184,6 +1246,7 @@ SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_toke
 
 SPECDEC_API int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
                                              const float *cos_table, const float *sin_table,
+                                             const void *hidden, int64_t hidden_dim, float eps,
                                              void *k_pool, void *v_pool, const int32_t *tables,
                                              int64_t table_stride, const int32_t *meta, int32_t batch,
                                              int32_t width, int32_t n_heads, int32_t n_kv_heads,
@@ -1198,6 +1261,10 @@ SPECDEC_API int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token
   a.rope = 1;
   a.cos_t = cos_table;
   a.sin_t = sin_table;
+  if (hidden && (hidden_dim <= 0 || hidden_dim > (1 << 20))) return SPECDEC_EINVAL;
+  a.hidden = hidden;
+  a.hdim = (int)hidden_dim;
+  a.eps = eps;
   a.k = k_pool;
   a.v = v_pool;
   a.tables = tables;

@@ -1,5 +1,6 @@
-// Elementwise layer glue of the Llama forward: residual add + RMSNorm, and
-// SiLU(gate) * up.
+// Elementwise layer glue of the Llama forward: residual add + RMSNorm,
+// SiLU(gate) * up, and SiLU(gate) * up with the post-attention RMSNorm's row
+// scale applied to a gate/up projection of the unnormalised residual stream.
 //
 // Numerics follow transformers' Llama modules as lm/forward.py:56,64-65
 // calls them: the residual add rounds to the activation type, RMSNorm
@@ -154,6 +155,85 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const T *__restrict__
   reinterpret_cast<u32x4 *>(out + r * inter)[i] = o;
 }
 
+// The post-attention RMSNorm finished after the gate/up projection instead of
+// before it.  With s = rsqrt(mean(x^2) + eps) and g the norm weight,
+//   (g * (x * s)) @ W^T = s * (x @ (W diag(g))^T),
+// so the projection reads the residual stream x itself, with g folded into
+// W's columns, and this kernel scales each gate and up value by its row's s
+// (rounded to T, as a projection's output is) before SiLU(gate) * up.
+//
+// Each wave reduces its row's sum of squares itself: lane l adds the row's
+// 16-byte vectors l, l+64, l+128, ... in order, then a butterfly across the
+// wave.  add_rmsnorm_wave_kernel uses the same order.  Every wave of every
+// call therefore computes the same s for the same row, whatever the grid and
+// the number of rows, with no LDS and no barrier.  NV vectors per lane are in
+// flight per pass over the row.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void rms_silu_mul_vec_kernel(const T *__restrict__ gu, const T *__restrict__ hidden,
+                                                                T *__restrict__ out, int64_t inter, int64_t dim,
+                                                                float eps) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t r = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = i < inter / E;
+  const int64_t ic = live ? i : 0;  // dead lanes still take part in the wave's reduction
+  const u32x4 g = reinterpret_cast<const u32x4 *>(gu + r * 2 * inter)[ic];
+  const u32x4 u = reinterpret_cast<const u32x4 *>(gu + r * 2 * inter + inter)[ic];
+  const u32x4 *h = reinterpret_cast<const u32x4 *>(hidden + r * dim);
+  const int nvec = (int)(dim / E);
+  float ss = 0.0f;
+  for (int base = 0; base < nvec; base += kWave * NV) {
+    u32x4 hv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) hv[k] = h[min(base + lane + kWave * k, nvec - 1)];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const bool in = base + lane + kWave * k < nvec;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float x = vec_elem<T>(hv[k], e);
+        ss += in ? x * x : 0.0f;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float s = rsqrtf(ss / (float)dim + eps);
+  if (!live) return;
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float x = to_f32(from_f32<T>(s * vec_elem<T>(g, e)));
+    const float up = to_f32(from_f32<T>(s * vec_elem<T>(u, e)));
+    const T a = from_f32<T>(x / (1.0f + expf(-x)));
+    vec_set<T>(o, e, from_f32<T>(to_f32(a) * up));
+  }
+  reinterpret_cast<u32x4 *>(out + r * inter)[i] = o;
+}
+
+// The same for any dim, inter and alignment, one element per thread: lane l
+// adds elements l, l+64, ... of the row.
+template <typename T>
+__global__ __launch_bounds__(256) void rms_silu_mul_kernel(const T *__restrict__ gu, const T *__restrict__ hidden,
+                                                           T *__restrict__ out, int64_t inter, int64_t dim,
+                                                           float eps) {
+  const int64_t r = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  float ss = 0.0f;
+  for (int64_t j = lane; j < dim; j += kWave) {
+    const float x = to_f32(hidden[r * dim + j]);
+    ss += x * x;
+  }
+  ss = wave_sum(ss);
+  const float s = rsqrtf(ss / (float)dim + eps);
+  if (c >= inter) return;
+  const float x = to_f32(from_f32<T>(s * to_f32(gu[r * 2 * inter + c])));
+  const float up = to_f32(from_f32<T>(s * to_f32(gu[r * 2 * inter + inter + c])));
+  const T a = from_f32<T>(x / (1.0f + expf(-x)));
+  out[r * inter + c] = from_f32<T>(to_f32(a) * up);
+}
+
 template <typename T>
 __global__ void silu_mul_kernel(const T *__restrict__ gu, T *__restrict__ out, int64_t rows, int64_t inter) {
   const int64_t total = rows * inter;
@@ -239,6 +319,46 @@ SPECDEC_API int specdec_silu_mul(const void *gate_up, void *out, int dtype, int6
   } else if (dtype == SPECDEC_F32) {
     silu_mul_kernel<float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>((const float *)gate_up, (float *)out, rows,
                                                                        inter);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+namespace specdec {
+
+template <typename T>
+static void launch_rms_silu_mul(const T *gate_up, const T *hidden, T *out, int64_t rows, int64_t inter, int64_t dim,
+                                float eps, hipStream_t s) {
+  constexpr int E = 16 / sizeof(T);
+  if (inter % E == 0 && dim % E == 0 && aligned16(gate_up) && aligned16(hidden) && aligned16(out)) {
+    const int64_t nvec = dim / E;
+    dim3 grid((unsigned)((inter / E + 255) / 256), (unsigned)rows), block(256);
+    if (nvec <= 2 * kWave)
+      rms_silu_mul_vec_kernel<T, 2><<<grid, block, 0, s>>>(gate_up, hidden, out, inter, dim, eps);
+    else if (nvec <= 4 * kWave)
+      rms_silu_mul_vec_kernel<T, 4><<<grid, block, 0, s>>>(gate_up, hidden, out, inter, dim, eps);
+    else
+      rms_silu_mul_vec_kernel<T, 8><<<grid, block, 0, s>>>(gate_up, hidden, out, inter, dim, eps);
+    return;
+  }
+  dim3 grid((unsigned)((inter + 255) / 256), (unsigned)rows), block(256);
+  rms_silu_mul_kernel<T><<<grid, block, 0, s>>>(gate_up, hidden, out, inter, dim, eps);
+}
+
+}  // namespace specdec
+
+SPECDEC_API int specdec_rms_silu_mul(const void *gate_up, const void *hidden, void *out, int dtype, int64_t rows,
+                                     int64_t inter, int64_t dim, float eps, void *stream) {
+  if (rows < 0 || inter <= 0 || dim <= 0 || rows > 65535 || inter > ((int64_t)1 << 30)) return SPECDEC_EINVAL;
+  if (rows == 0) return SPECDEC_OK;
+  if (!gate_up || !hidden || !out) return SPECDEC_EINVAL;
+  hipStream_t s = as_stream(stream);
+  if (dtype == SPECDEC_BF16) {
+    launch_rms_silu_mul<__hip_bfloat16>((const __hip_bfloat16 *)gate_up, (const __hip_bfloat16 *)hidden,
+                                        (__hip_bfloat16 *)out, rows, inter, dim, eps, s);
+  } else if (dtype == SPECDEC_F32) {
+    launch_rms_silu_mul<float>((const float *)gate_up, (const float *)hidden, (float *)out, rows, inter, dim, eps, s);
   } else {
     return SPECDEC_EINVAL;
   }

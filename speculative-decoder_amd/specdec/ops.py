@@ -317,6 +317,23 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def rms_silu_mul(gate_up: torch.Tensor, hidden: torch.Tensor, out: torch.Tensor, eps: float) -> torch.Tensor:
+    """out = round(silu(round(s * gate))) * round(s * up), s = rsqrt(mean(hidden^2)
+    + eps) per row: the post-attention RMSNorm finished after a gate/up
+    projection of the unnormalised hidden (whose weight carries the norm
+    weight in its columns).  Rows are the leading dims of all three."""
+    inter, dim = gate_up.shape[-1] // 2, hidden.shape[-1]
+    dev = gpu(gate_up, "gate_up").device
+    _on(dev, gate_up, "gate_up", contiguous=True)
+    rows = gate_up.numel() // (2 * inter)
+    _on(dev, hidden, "hidden", gate_up.dtype, True, rows * dim)
+    _on(dev, out, "out", gate_up.dtype, True, rows * inter)
+    st = lib().specdec_rms_silu_mul(gate_up.data_ptr(), hidden.data_ptr(), out.data_ptr(), dtype_code(gate_up), rows,
+                                    inter, dim, float(eps), stream())
+    _check(st, "rms_silu_mul")
+    return out
+
+
 # --------------------------------------------------------------- attention --
 class AttentionWorkspace:
     """Grow-only buffer of split-KV partials for one device.  Calls that
@@ -399,16 +416,39 @@ def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, widt
     return out
 
 
+# new tokens per row up to which the attention can finish the input RMSNorm
+# (every new token of a row is staged in the workgroup's LDS)
+NORM_IN_ATTENTION_MAX_WIDTH = 16
+
+
+def norm_in_attention(dtype: torch.dtype, block_size: int, width: int) -> bool:
+    """Whether rope_paged_attention accepts `norm_of` for this call shape."""
+    return dtype == torch.bfloat16 and block_size % 16 == 0 and width <= NORM_IN_ATTENTION_MAX_WIDTH
+
+
 def rope_paged_attention(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads, head_dim,
                          block_size, scale, max_kv_len, out, out_token_stride,
-                         workspace: AttentionWorkspace | None = None, split_tokens: int = 0):
+                         workspace: AttentionWorkspace | None = None, split_tokens: int = 0,
+                         norm_of: torch.Tensor | None = None, eps: float = 0.0):
     """RoPE + paged append + verify attention in one launch (plus the split
-    combine when needed).  qkv [B, T, (H + 2 Hkv) d] holds unrotated q/k/v."""
-    _qkv_side(gpu(qkv, "qkv").device, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool, out)
+    combine when needed).  qkv [B, T, (H + 2 Hkv) d] holds unrotated q/k/v.
+    With `norm_of` (the [B, T, hidden] residual stream that qkv projects, the
+    norm weight folded into the projection), each token's q/k/v are scaled by
+    its row's rsqrt(mean(norm_of^2) + eps) first: the input RMSNorm finished
+    after the projection (`norm_in_attention` tells which shapes allow it)."""
+    dev = gpu(qkv, "qkv").device
+    _qkv_side(dev, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool, out)
+    hidden_dim = 0
+    if norm_of is not None:
+        if not norm_in_attention(qkv.dtype, block_size, width):
+            raise ValueError(f"norm_of needs bf16, block_size % 16 == 0 and width <= {NORM_IN_ATTENTION_MAX_WIDTH}")
+        hidden_dim = norm_of.shape[-1]
+        _on(dev, norm_of, "norm_of", qkv.dtype, True, batch * width * hidden_dim)
     ws = workspace or workspace_for(qkv.device)
     ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
     st = lib().specdec_rope_paged_attention(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), cos.data_ptr(),
-                                            sin.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), tables.data_ptr(),
+                                            sin.data_ptr(), ptr(norm_of), hidden_dim, float(eps), k_pool.data_ptr(),
+                                            v_pool.data_ptr(), tables.data_ptr(),
                                             tables.stride(0), meta.data_ptr(), batch, width, n_heads, n_kv_heads,
                                             head_dim, block_size, float(scale), max_kv_len, split_tokens,
                                             ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(), out_token_stride,

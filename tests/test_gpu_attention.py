@@ -433,3 +433,68 @@ def test_tiled_fused_rope_append_equals_separate_kernels(bs):
         outs.append((out, k_all, v_all))
     for x, y in zip(outs[0], outs[1]):
         assert torch.equal(x, y)
+
+
+def _norm_case(batch, lengths, h, hkv, hidden_dim, split_tokens, t_new=5, seed=0):
+    """Two identical caches; rope_paged_attention on q/k/v pre-scaled by each
+    token's RMS factor vs on the raw projection with norm_of = the residual
+    rows.  Each token's residual row is +-2^e_t (random signs, e_t in
+    -2..2), so its mean square is exactly 4^e_t and the factor (eps = 0) is
+    exactly 2^-e_t in any summation order: the two calls must agree bit for
+    bit, and a scale applied to the wrong token, or missing from q, k or v,
+    cannot."""
+    from lm.model import LlamaShape, rope_tables
+
+    d, bs = 64, 16
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=10000.0)
+    cos, sin = (x.cuda() for x in rope_tables(shape, max(lengths) + 64))
+    g = torch.Generator().manual_seed(seed)
+    expo = torch.randint(-2, 3, (batch, t_new, 1), generator=g).float()
+    signs = torch.randint(0, 2, (batch, t_new, hidden_dim), generator=g).float() * 2 - 1
+    hidden = (signs * torch.exp2(expo)).to(torch.bfloat16).cuda()
+    factor = torch.exp2(-expo).to(torch.bfloat16).cuda()
+    qkv = torch.randn(batch, t_new, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16).cuda()
+    blocks = sum((n + t_new) // bs + 2 for n in lengths) + 8
+    hist = [torch.randn(batch, hkv, max(lengths), d, generator=g).to(torch.bfloat16).cuda() for _ in range(2)]
+    ids = list(range(batch))
+    outs = []
+    for which in range(2):
+        cache = make_cache(1, hkv, d, blocks, bs, torch.bfloat16, 3)
+        for s in ids:
+            cache.add(s)
+        step = cache.append(ids, lengths)
+        cache.write(0, step, hist[0], hist[1])
+        step = cache.append(ids, [t_new] * batch)
+        out = torch.zeros(batch, t_new, h * d, dtype=torch.bfloat16, device="cuda")
+        x = qkv * factor if which == 0 else qkv.clone()
+        ops.rope_paged_attention(x, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, t_new, h,
+                                 hkv, d, bs, 0.125, step.max_total, out, out.stride(1), split_tokens=split_tokens,
+                                 norm_of=None if which == 0 else hidden, eps=0.0)
+        k_all, v_all = cache.gather(0, step)
+        outs.append((out, k_all, v_all))
+    return outs
+
+
+@pytest.mark.parametrize(("batch", "lengths", "heads", "hidden_dim", "split"), [
+    (2, [300, 37], (32, 32), 2048, 0),  # one 16-wave workgroup per tile, grouped splits
+    (2, [300, 37], (9, 3), 576, -1),  # the draft's flat split
+    (1, [3000], (32, 32), 2048, 0),  # few 4-wave split workgroups, loads paired
+    (3, [2600, 700, 4500], (32, 32), 2048, 0),  # 4-wave splits + combine
+    (8, [4000 - 300 * b for b in range(8)], (32, 32), 2048, 0),  # tiled
+])
+def test_input_norm_in_attention_equals_prescaled_qkv(batch, lengths, heads, hidden_dim, split):
+    ref, got = _norm_case(batch, lengths, heads[0], heads[1], hidden_dim, split)
+    for a, b in zip(ref, got):
+        assert torch.equal(a, b)
+
+
+def test_input_norm_in_attention_rejects_other_shapes():
+    cache, step, q = _filled(1, [40], 0)
+    h = torch.zeros(1, 20, 64, dtype=torch.bfloat16, device="cuda")
+    qkv = torch.zeros(1, 20, 96 * 64, dtype=torch.bfloat16, device="cuda")
+    cos = sin = torch.zeros(128, 32, device="cuda")
+    out = torch.zeros(1, 20, 32 * 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="width"):
+        ops.rope_paged_attention(qkv, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, 1, 20, 32, 32,
+                                 64, 16, 0.125, step.max_total, out, out.stride(1), norm_of=h, eps=1e-5)

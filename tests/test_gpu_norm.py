@@ -1,6 +1,7 @@
-"""Layer glue kernels (residual add + RMSNorm, SiLU(gate) * up) against a
-torch fp32 statement of transformers' Llama modules, at the decode sizes of
-both models and at sizes that take the general kernels."""
+"""Layer glue kernels (residual add + RMSNorm, SiLU(gate) * up, and SiLU * up
+after a projection of the unnormalised stream) against a torch fp32
+statement of transformers' Llama modules, at the decode sizes of both
+models and at sizes that take the general kernels."""
 import pytest
 import torch
 
@@ -55,3 +56,69 @@ def test_silu_mul_matches_torch(dtype, rows, inter):
         assert (out != want).float().mean().item() < 0.01
     else:
         assert torch.allclose(out, want, rtol=2e-6, atol=1e-7), (out - want).abs().max()
+
+
+def rms_silu_ref(gu, hidden, eps):
+    """torch fp32 statement of the kernel's contract: s per row, the scaled
+    gate and up rounded to the activation dtype, then SiLU(gate) * up."""
+    dtype, inter = gu.dtype, gu.shape[-1] // 2
+    s = torch.rsqrt(hidden.float().pow(2).mean(-1, keepdim=True) + eps)
+    gate = (gu[..., :inter].float() * s).to(dtype).float()
+    up = (gu[..., inter:].float() * s).to(dtype).float()
+    return ((gate / (1 + torch.exp(-gate))).to(dtype).float() * up).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize(("rows", "dim", "inter"), [(1, 576, 1536), (5, 2048, 8192), (3, 64, 256), (2, 100, 12),
+                                                   (4, 4096, 1024), (1, 8192, 64)])
+def test_rms_silu_mul_matches_torch(dtype, rows, dim, inter):
+    g = torch.Generator(device="cuda").manual_seed(rows * 31 + dim + inter)
+    hidden = (4 * torch.randn(rows, dim, generator=g, device="cuda")).to(dtype)
+    gu = (3 * torch.randn(rows, 2 * inter, generator=g, device="cuda")).to(dtype)
+    out = torch.empty(rows, inter, dtype=dtype, device="cuda")
+    ops.rms_silu_mul(gu, hidden, out, 1e-5)
+    want = rms_silu_ref(gu, hidden, 1e-5)
+    # s may differ from torch's in its last bit (another summation order)
+    if dtype == torch.bfloat16:
+        assert torch.allclose(out.float(), want.float(), rtol=2 ** -6, atol=1e-5)
+        assert (out != want).float().mean().item() < 0.02
+    else:
+        assert torch.allclose(out, want, rtol=1e-5, atol=1e-6), (out - want).abs().max()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_norm_after_projection_equals_norm_before(dtype):
+    """The identity the forward relies on: projecting the unnormalised stream
+    with the norm weight folded into W's columns, then this kernel, gives
+    what RMSNorm -> projection -> SiLU*up gives, up to rounding.  A wrong
+    fold (rows instead of columns, a missing weight) or a wrong scale is far
+    outside the bound."""
+    g = torch.Generator(device="cuda").manual_seed(5)
+    rows, dim, inter = 5, 2048, 1024
+    hidden = (4 * torch.randn(rows, dim, generator=g, device="cuda")).to(dtype)
+    weight = (1 + 0.3 * torch.randn(dim, generator=g, device="cuda")).to(dtype)
+    w = (0.02 * torch.randn(2 * inter, dim, generator=g, device="cuda")).to(dtype)
+    x = torch.empty_like(hidden)
+    ops.add_rmsnorm(hidden.clone(), None, weight, x, 1e-5)
+    before = torch.empty(rows, inter, dtype=dtype, device="cuda")
+    ops.silu_mul(torch.nn.functional.linear(x, w), before)
+    folded = (w.float() * weight.float()).to(dtype)
+    after = torch.empty_like(before)
+    ops.rms_silu_mul(torch.nn.functional.linear(hidden, folded), hidden, after, 1e-5)
+    tol = 3e-2 if dtype == torch.bfloat16 else 1e-4
+    scale = before.float().abs().max().item()
+    assert (after.float() - before.float()).abs().max().item() < tol * scale
+    if dtype == torch.float32:
+        assert torch.allclose(after, before, rtol=1e-4, atol=1e-6)
+
+
+def test_rms_silu_rows_do_not_depend_on_the_call():
+    """Each row's result is the same whether it comes with 5 rows or alone."""
+    g = torch.Generator(device="cuda").manual_seed(9)
+    hidden = torch.randn(5, 2048, generator=g, device="cuda").to(torch.bfloat16)
+    gu = torch.randn(5, 16384, generator=g, device="cuda").to(torch.bfloat16)
+    all_rows = ops.rms_silu_mul(gu, hidden, torch.empty(5, 8192, dtype=torch.bfloat16, device="cuda"), 1e-5)
+    for r in range(5):
+        one = ops.rms_silu_mul(gu[r:r + 1], hidden[r:r + 1], torch.empty(1, 8192, dtype=torch.bfloat16, device="cuda"),
+                               1e-5)
+        assert torch.equal(one, all_rows[r:r + 1])

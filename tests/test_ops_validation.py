@@ -30,6 +30,8 @@ def test_cpu_inputs_are_rejected_before_launch():
         ops.add_rmsnorm(torch.randn(2, 8), None, torch.ones(8), torch.empty(2, 8), 1e-5)
     with pytest.raises(RuntimeError, match="GPU"):
         ops.silu_mul(torch.randn(2, 8), torch.empty(2, 4))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.rms_silu_mul(torch.randn(2, 8), torch.randn(2, 6), torch.empty(2, 4), 1e-5)
 
 
 def test_checker_names_device_dtype_and_size():
