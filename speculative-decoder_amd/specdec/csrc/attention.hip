@@ -669,13 +669,21 @@ attention_bf16_kernel(
     qop[0] = __builtin_bit_cast(bf16x8, raw[0]);
     qop[1] = __builtin_bit_cast(bf16x8, raw[1]);
   }
+  // the rotation's cos/sin, loaded before the norm's barrier below
+  float qcs[8], qsn[8];
+  if (a.rope && row_ok) {
+    const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
+    const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qcs[j] = cs[j], qsn[j] = sn[j];
+  }
 
   // Input RMSNorm finished here (a.hidden): q, k and v come from a
   // projection of the unnormalised residual stream, so each new token's
   // values are scaled by s = rsqrt(mean(hidden^2) + eps) of its row, rounded
   // to bf16 as a projection's output is, before RoPE.  Wave w reduces tokens
   // w, w + NW, ... (the host allows at most kStage new tokens): lane l adds
-  // the row's 16-byte vectors l, l+64, ... in order, then a butterfly -- one
+  // the row's 16-byte vectors l, l+64, ... in order, then wave_sum_dpp -- one
   // fixed order, so every workgroup of every call gets the same s for a
   // token, and the same s the MLP's norm kernel computes for a row.
   __shared__ float s_tok[kStage];
@@ -701,7 +709,7 @@ attention_bf16_kernel(
           }
         }
       }
-      ss = wave_sum(ss);
+      ss = wave_sum_dpp(ss);
       if (lane == 0) s_tok[tk] = rsqrtf(ss / (float)a.hdim + a.eps);
     }
     __syncthreads();
@@ -712,14 +720,12 @@ attention_bf16_kernel(
   };
 
   if (a.rope && row_ok) {
-    const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
-    const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
     const float sq = norm_in ? s_tok[t] : 1.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float x1 = (float)qop[0][j], x2 = (float)qop[1][j], y1, y2;
       if (norm_in) x1 = (float)(__bf16)(sq * x1), x2 = (float)(__bf16)(sq * x2);
-      rope_pair(x1, x2, cs[j], sn[j], y1, y2);
+      rope_pair(x1, x2, qcs[j], qsn[j], y1, y2);
       qop[0][j] = (__bf16)y1;
       qop[1][j] = (__bf16)y2;
     }

@@ -39,6 +39,27 @@ template <typename T> __device__ __forceinline__ T wave_sum(T v) {
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+// The same sum through DPP lane moves instead of LDS permutes: within each
+// row of 16 lanes, partners at xor 1, xor 2 (quad permutes), then the mirror
+// in 8 and in 16 lanes, so every lane of a row holds the row's sum; then the
+// four row sums are read into scalar registers and added as (r0 + r1) +
+// (r2 + r3).  Each step adds a pair of equal-bit operands in both lanes, so
+// every lane returns the same bits, in an order fixed by the lane layout.
+template <int CTRL> __device__ __forceinline__ float dpp_partner_add(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true);
+  return v + __int_as_float(moved);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_partner_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]: xor 1
+  v = dpp_partner_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]: xor 2
+  v = dpp_partner_add<0x141>(v);  // row_half_mirror: lane i <-> 7 - i
+  v = dpp_partner_add<0x140>(v);  // row_mirror: lane i <-> 15 - i
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
 template <typename T> __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, kWave));

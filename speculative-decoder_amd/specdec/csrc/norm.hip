@@ -163,11 +163,10 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const T *__restrict__
 // (rounded to T, as a projection's output is) before SiLU(gate) * up.
 //
 // Each wave reduces its row's sum of squares itself: lane l adds the row's
-// 16-byte vectors l, l+64, l+128, ... in order, then a butterfly across the
-// wave.  add_rmsnorm_wave_kernel uses the same order.  Every wave of every
-// call therefore computes the same s for the same row, whatever the grid and
-// the number of rows, with no LDS and no barrier.  NV vectors per lane are in
-// flight per pass over the row.
+// 16-byte vectors l, l+64, l+128, ... in order, then wave_sum_dpp (lane moves
+// in a fixed pattern, no LDS).  Every wave of every call therefore computes
+// the same s for the same row, whatever the grid and the number of rows,
+// with no barrier.  NV vectors per lane are in flight per pass over the row.
 template <typename T, int NV>
 __global__ __launch_bounds__(256) void rms_silu_mul_vec_kernel(const T *__restrict__ gu, const T *__restrict__ hidden,
                                                                 T *__restrict__ out, int64_t inter, int64_t dim,
@@ -197,7 +196,7 @@ __global__ __launch_bounds__(256) void rms_silu_mul_vec_kernel(const T *__restri
       }
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float s = rsqrtf(ss / (float)dim + eps);
   if (!live) return;
   u32x4 o;
@@ -225,7 +224,7 @@ __global__ __launch_bounds__(256) void rms_silu_mul_kernel(const T *__restrict__
     const float x = to_f32(hidden[r * dim + j]);
     ss += x * x;
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float s = rsqrtf(ss / (float)dim + eps);
   if (c >= inter) return;
   const float x = to_f32(from_f32<T>(s * to_f32(gu[r * 2 * inter + c])));
