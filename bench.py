@@ -527,7 +527,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--only", choices=["all", "e2e", "attention", "kernels", "small", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "e2e", "batched", "attention", "kernels", "small", "copy"], default="all",
                     help="small: the kernels of configs 1-3 without the attention grid (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
@@ -563,6 +563,10 @@ def main():
     if args.only == "e2e":
         e2e, _ = bench_e2e(args.steps, args.warmup)
         print(json.dumps({"e2e": e2e}))
+        return
+    if args.only == "batched":
+        target, draft, _, _ = build_models()
+        print(json.dumps({"batched_sampled": bench_batched(target, draft)}))
         return
 
     e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
