@@ -170,18 +170,19 @@ __device__ void append_new_kv(const AttnArgs &a, const TileInfo &ti, int lo, int
 // scale * log2(e).  Waves hand them over in LDS as s_m/s_l [wave][query] and
 // s_o [wave][query][dim].
 
-// Fold of waves w0 .. w0+N-1 for query row qq, dims d0 .. d0+3 (R rows
-// per wave in LDS).
+// Fold of waves w0 .. w0+n-1 (n = N unless given) for query row qq, dims
+// d0 .. d0+3 (R rows per wave in LDS).  A wave that saw no key holds
+// (-inf, 0, 0) and adds nothing: leaving it out of n changes no bit.
 template <int N = 4, int R = kRows>
 __device__ __forceinline__ void fold_waves(const float (*s_m)[R], const float (*s_l)[R],
                                            const float (*s_o)[R][kD + 4], int w0, int qq, int d0, float &M,
-                                           float &L, float (&O)[4]) {
+                                           float &L, float (&O)[4], int n = N) {
   M = s_m[w0][qq];
-  for (int w = 1; w < N; ++w) M = fmaxf(M, s_m[w0 + w][qq]);
+  for (int w = 1; w < n; ++w) M = fmaxf(M, s_m[w0 + w][qq]);
   L = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) O[i] = 0.0f;
-  for (int w = 0; w < N; ++w) {
+  for (int w = 0; w < n; ++w) {
     const float mw = s_m[w0 + w][qq];
     const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
     L = __builtin_fmaf(f, s_l[w0 + w][qq], L);
@@ -403,7 +404,9 @@ __device__ void finish_grouped(const AttnArgs &a, const TileInfo &ti, float m, f
   float M, L, O[4];
   if (a.flat) {
     if (grp == 0 && qq < nq) {
-      fold_waves<16>(s_m, s_l, s_o, 0, qq, d0, M, L, O);
+      // wave w's first step starts at key 64 w: the waves past the tile's
+      // keys saw none
+      fold_waves<16>(s_m, s_l, s_o, 0, qq, d0, M, L, O, max(1, min(16, (ti.kv_len + 63) / 64)));
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
