@@ -43,17 +43,19 @@ def test_probabilities_match_torch_softmax(temperature):
         assert (got.double().sum(-1) - 1).abs().max() < 1e-5
 
 
-@pytest.mark.parametrize("vocab", [V, 1000, 70000])
+@pytest.mark.parametrize("vocab", [V, 1000, 1001, 49151, 70000])
 def test_probabilities_into_strided_rows_with_argmax(vocab):
     """Writing into a row-strided view (the draft chain's q[:, i]) gives the
     same rows; at temperature 0 index_out holds each row's argmax, which is
-    what an inverse-CDF draw from the one-hot row returns.  70000 exceeds the
-    register-resident row size and takes the streaming loop."""
+    what an inverse-CDF draw from the one-hot row returns.  Vocabularies that
+    are a multiple of 4 move as 16-byte vectors, 1001 and 49151 element by
+    element; 70000 exceeds the register-resident row size and takes the
+    streaming loop."""
     from specdec import ops
 
     g = torch.Generator().manual_seed(vocab)
     x = (torch.randn(3, vocab, generator=g) * 3).cuda()
-    for temperature in (0.0, 0.7):
+    for temperature in (0.0, 0.7, 1.0):
         want = osamp.probabilities(x.cpu(), temperature)
         q = torch.full((3, 2, vocab), -1.0, device="cuda")
         idx = torch.full((3, 2), -1, dtype=torch.int64, device="cuda")
