@@ -69,3 +69,25 @@ def test_bf16_spec_equals_plain():
         out, _ = generate(target, tc, ModelDraft(draft, dc), [p], 40, k=4)
         plain = cached_autoregressive.generate(target, KVCache.for_model(ts, 64, 16, torch.bfloat16, "cuda"), p, 40)
         assert out[0] == plain
+
+
+def test_bf16_spec_equals_plain_with_norm_weights():
+    """The same identity with non-unit RMSNorm weights in both models: the
+    weights folded into the projections (rounded once into bf16 weights)
+    serve the verify and plain decoding alike, so the outputs still agree."""
+    ts, ds = shapes()
+
+    def perturbed(shape, seed):
+        state = random_state_dict(shape, seed, "cuda", torch.bfloat16)
+        g = torch.Generator(device="cuda").manual_seed(seed + 100)
+        for name, w in state.items():
+            if name.endswith("norm.weight"):
+                w.copy_((0.5 + torch.rand(w.shape, generator=g, device="cuda")).to(w.dtype))
+        return Llama.from_state_dict(shape, state)
+
+    target, draft = perturbed(ts, 0), perturbed(ds, 1)
+    for p in prompts(2, 96):
+        tc, dc = caches(ts, ds, torch.bfloat16)
+        out, _ = generate(target, tc, ModelDraft(draft, dc), [p], 40, k=4)
+        plain = cached_autoregressive.generate(target, KVCache.for_model(ts, 64, 16, torch.bfloat16, "cuda"), p, 40)
+        assert out[0] == plain
