@@ -5,10 +5,11 @@ with k = 4 and paged KV (block size 16), target with SmolLM2-1.7B shapes and
 draft with SmolLM2-135M shapes, random-init bf16 weights, a 256-token seeded
 prompt and 128 new tokens.  One step = one `generate` call.
 
-`roofline`: the verify paged-attention kernel at B = 1, context 4096, 32/32
-heads of 64, 5 query tokens, shuffled block table: algorithmic bytes per
-launch (K+V of 4101 positions + Q in + O out + block table) over the mean
-launch time measured with HIP events on the stream it runs on.
+`roofline`: the verify paged-attention kernel at B = 8, context 4096, 32/32
+heads of 64, 5 query tokens, shuffled block table (config 2's largest
+batch): algorithmic bytes per launch (K+V of 8 x 4101 positions + Q in + O
+out + block tables) over the mean launch time measured with HIP events on
+the stream it runs on.  B = 1 sits beside it in the line.
 
 `cpu_baseline`: the oracle's CPU restatement of the reference loop
 (gather + SDPA forward, host accept-reject) on the same weights, timed on a
@@ -161,7 +162,7 @@ def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 
     attention kernel time at that batch and context (graph-replayed)."""
     import spec.loop as loop_mod
     from cache.kv import KVCache
-    from make_golden import planted_rows
+    from specdec.workloads import planted_rows
     from spec.draft import ModelDraft
     from spec.loop import generate
     from spec.ngram import NGramDraft
@@ -334,7 +335,7 @@ def time_fn(fn, iters=100, graph=False):
 
 
 def bench_kernels(attention_grid=True):
-    from make_golden import planted_rows
+    from specdec.workloads import planted_rows
     from specdec import ops
 
     res = {}
@@ -469,7 +470,7 @@ def cpu_kernel_baselines(seconds=1.0):
     import oracle.kv as okv
     import oracle.ngram as on
     import oracle.sampling as osamp
-    from make_golden import planted_rows
+    from specdec.workloads import planted_rows
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -542,7 +543,6 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     sys.path.insert(0, str(ROOT))
-    sys.path.insert(0, str(ROOT / "tests" / "golden"))
 
     if args.only == "attention":
         r = time_attention(args.batch, 4096, iters=max(args.steps, 1) * 100, rotate=not args.one_pool)

@@ -50,7 +50,7 @@ extern "C" {
 #define SPECDEC_BF16 2
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 6). */
+ * below changes (currently 7). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -73,7 +73,8 @@ int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t v
  * p [batch, k+1, vocab], q [batch, k, vocab] (dtype F32 or F64, strides in
  * elements), draft int64 [batch, k], u_accept [batch, k] and u_residual [batch]
  * of the same dtype as p.  out int64 [3, batch]: n_accepted, next_token, and
- * a flag that is 1 when a drafted token had q(x) <= 0.
+ * a flag that is 1 when a drafted token had q(x) <= 0 or an id outside
+ * [0, vocab).
  * Replaces spec/accept.py:44-79 `accept_reject` with the default residual
  * (spec/accept.py:18-26) and spec/accept.py:29-35 `sample_inverse_cdf`. */
 int specdec_accept_reject(const void *p, const void *q, int dtype,
@@ -84,13 +85,15 @@ int specdec_accept_reject(const void *p, const void *q, int dtype,
                           int64_t vocab, int64_t *out, void *stream);
 
 /* First stage of accept-reject alone (for a caller-supplied residual):
- * out int64 [2, batch]: n_accepted and the zero-q flag.
+ * out int64 [2, batch]: n_accepted and a flag that is 1 when a drafted token
+ * had q(x) <= 0 or an id outside [0, vocab) (such an id is never read
+ * through; it counts as the first rejection).
  * Replaces spec/accept.py:65-71. */
 int specdec_accept_count(const void *p, const void *q, int dtype,
                          int64_t p_batch_stride, int64_t p_row_stride,
                          int64_t q_batch_stride, int64_t q_row_stride,
                          const int64_t *draft, const void *u_accept, int64_t batch,
-                         int64_t k, int64_t *out, void *stream);
+                         int64_t k, int64_t vocab, int64_t *out, void *stream);
 
 /* Inverse-CDF sampling: token i is chosen iff u*total lies in
  * [cdf[i-1], cdf[i]) with the prefix sums accumulated in fp64 and rounded to

@@ -209,9 +209,25 @@ def rope_tables(shape: LlamaShape, n_positions: int) -> tuple[torch.Tensor, torc
 
 
 def shape_from_hf_config(config) -> LlamaShape:
+    """The Llama shape of a transformers config.  Architectures whose math
+    this forward does not carry are refused rather than run with wrong
+    logits: projection biases (Qwen2's q/k/v biases, `attention_bias`,
+    `mlp_bias`), scaled RoPE (`rope_scaling` other than the default) and
+    sliding-window attention."""
     head_dim = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
-    if config.model_type not in ("llama", "qwen2"):
-        raise NotImplementedError(f"cached forward supports llama and qwen2, got {config.model_type}")
+    if config.model_type != "llama":
+        raise NotImplementedError(f"the forward implements the Llama architecture; got {config.model_type} "
+                                  "(Qwen2's q/k/v projection biases are not implemented)")
+    if getattr(config, "attention_bias", False) or getattr(config, "mlp_bias", False):
+        raise NotImplementedError("projection biases (attention_bias / mlp_bias) are not implemented")
+    scaling = getattr(config, "rope_scaling", None)
+    params = getattr(config, "rope_parameters", None)
+    kind = None
+    for source in (scaling, params):
+        if isinstance(source, dict):
+            kind = source.get("rope_type", source.get("type")) or kind
+    if kind not in (None, "default"):
+        raise NotImplementedError(f"RoPE scaling {kind!r} is not implemented (only the default rotary tables)")
     if getattr(config, "use_sliding_window", False):
         raise NotImplementedError("sliding-window attention is not implemented")
     return LlamaShape(

@@ -59,6 +59,10 @@ class Verdict:
     next_token: torch.Tensor  # [B] residual sample at the first rejection, or the bonus token
 
 
+_BAD_DRAFT = ("a drafted token has zero draft probability or lies outside the vocabulary; q is not what it "
+              "was sampled from")
+
+
 def _uniforms(shape: tuple[int, ...], generator: torch.Generator | None, dtype: torch.dtype) -> torch.Tensor:
     device = generator.device if generator is not None else torch.device("cpu")
     return torch.rand(*shape, generator=generator, dtype=dtype, device=device)
@@ -78,7 +82,8 @@ def accept_reject(
     sampled from, draft [B, k].  Returns the Verdict with host (CPU) int64
     tensors: the loop reads them element by element.
 
-    Raises ValueError if a drafted token has zero draft probability."""
+    Raises ValueError if a drafted token has zero draft probability (or is
+    not a token id of the vocabulary)."""
     b, k = draft.shape
     if u_accept is None:
         u_accept = _uniforms((b, k), generator, p.dtype)
@@ -92,12 +97,12 @@ def accept_reject(
     if residual is residual_distribution:
         out = ops.accept_reject(p, q, draft_d, ua, ur).cpu()
         if bool(out[2].any()):
-            raise ValueError("a drafted token has zero draft probability; q is not what it was sampled from")
+            raise ValueError(_BAD_DRAFT)
         return Verdict(out[0].clone(), out[1].clone())
     stage = ops.accept_count(p, q, draft_d, ua)
     n_host = stage.cpu()
     if bool(n_host[1].any()):
-        raise ValueError("a drafted token has zero draft probability; q is not what it was sampled from")
+        raise ValueError(_BAD_DRAFT)
     n = stage[0]
     rows = torch.arange(b, device=p.device)
     q_padded = torch.cat([q, torch.zeros_like(q[:, :1])], dim=1)

@@ -17,7 +17,7 @@ SIGNATURES: dict[str, list] = {
     "specdec_abi_version": [],
     "specdec_probabilities": [P, c_int, I64, I64, I64, c_float, P, I64, P, I64, P],
     "specdec_accept_reject": [P, P, c_int, I64, I64, I64, I64, P, P, P, I64, I64, I64, P, P],
-    "specdec_accept_count": [P, P, c_int, I64, I64, I64, I64, P, P, I64, I64, P, P],
+    "specdec_accept_count": [P, P, c_int, I64, I64, I64, I64, P, P, I64, I64, I64, P, P],
     "specdec_sample_inverse_cdf": [P, c_int, I64, I64, I64, P, P, P],
     "specdec_one_hot": [P, I64, I64, P, P],
     "specdec_ngram_lookup": [P, I64, P, I64, I32, I32, P, P, P],
@@ -39,7 +39,7 @@ SIGNATURES: dict[str, list] = {
                                      I32, c_float, I32, I32, P, I64, P, I64, P],
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _lib: ctypes.CDLL | None = None
 
 

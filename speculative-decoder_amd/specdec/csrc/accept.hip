@@ -613,7 +613,7 @@ __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64
 
 using namespace specdec;
 
-SPECDEC_API int specdec_abi_version(void) { return 6; }
+SPECDEC_API int specdec_abi_version(void) { return 7; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,
@@ -701,12 +701,12 @@ SPECDEC_API int specdec_accept_count(const void *p, const void *q, int dtype,
                                      int64_t p_batch_stride, int64_t p_row_stride,
                                      int64_t q_batch_stride, int64_t q_row_stride,
                                      const int64_t *draft, const void *u_accept, int64_t batch,
-                                     int64_t k, int64_t *out, void *stream) {
-  if (batch < 0 || k < 0) return SPECDEC_EINVAL;
+                                     int64_t k, int64_t vocab, int64_t *out, void *stream) {
+  if (batch < 0 || k < 0 || vocab <= 0) return SPECDEC_EINVAL;
   if (batch == 0) return SPECDEC_OK;
   if (!p || !out || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
-  // vocab is only used to range-check draft ids; the caller validated them
-  const int64_t vocab = INT64_MAX;
+  // a draft id outside [0, vocab) is never read through: it sets the flag
+  // (out[batch + b]) and counts as the first rejection
   dim3 block(64), grid((unsigned)((batch + 63) / 64));
   hipStream_t s = as_stream(stream);
   if (dtype == SPECDEC_F32) {

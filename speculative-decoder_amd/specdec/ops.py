@@ -133,13 +133,14 @@ def accept_reject(p, q, draft, u_accept, u_residual) -> torch.Tensor:
 
 
 def accept_count(p, q, draft, u_accept) -> torch.Tensor:
-    """Accept stage alone; int64 [2, B]: n_accepted, zero-q flag."""
+    """Accept stage alone; int64 [2, B]: n_accepted, and a flag for a zero
+    q(x) or a draft id outside the vocabulary."""
     p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
     b, k = _accept_inputs(p, q, draft, u_accept)
     out = torch.empty(2, b, dtype=torch.int64, device=p.device)
     st = lib().specdec_accept_count(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
                                     q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(), b, k,
-                                    out.data_ptr(), stream())
+                                    p.shape[-1], out.data_ptr(), stream())
     _check(st, "accept_count")
     return out
 

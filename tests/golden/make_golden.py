@@ -23,6 +23,9 @@ from pathlib import Path
 
 import torch
 
+sys.path.insert(0, str(Path(__file__).resolve().parents[2] / "speculative-decoder_amd"))
+from specdec.workloads import accept_inputs, planted_rows  # noqa: E402
+
 REF = Path("/root/reference")
 OUT = Path(__file__).resolve().parent
 
@@ -35,37 +38,6 @@ def ref_import():
     import cache.kv as kv  # noqa: E402
 
     return accept, ngram, kv
-
-
-def planted_rows(n_rows: int, length: int, vocab: int, seed: int, cover: float = 0.3):
-    """int histories with ~cover of positions overwritten by copies of earlier
-    spans (lengths 8..64), as in the n-gram benchmark workload."""
-    rng = random.Random(seed)
-    rows = []
-    for _ in range(n_rows):
-        row = [rng.randrange(vocab) for _ in range(length)]
-        covered = 0
-        while covered < cover * length:
-            span = rng.randint(8, 64)
-            if length < 2 * span + 2:
-                break
-            src = rng.randrange(0, length - 2 * span)
-            dst = rng.randrange(src + span, length - span + 1)
-            row[dst:dst + span] = row[src:src + span]
-            covered += span
-        rows.append(row)
-    return rows
-
-
-def accept_inputs(dtype, b, k, v, noise, seed):
-    """Seeded target/draft probabilities and draft tokens sampled from q."""
-    g = torch.Generator().manual_seed(seed)
-    tl = torch.randn(b, k + 1, v, generator=g, dtype=torch.float64) * 2.0
-    dl = tl[:, :k] + torch.randn(b, k, v, generator=g, dtype=torch.float64) * noise
-    p = torch.softmax(tl, -1).to(dtype)
-    q = torch.softmax(dl, -1).to(dtype)
-    draft = torch.multinomial(q.reshape(-1, v).double(), 1, generator=g).view(b, k)
-    return p, q, draft
 
 
 def make_accept(accept) -> dict:

@@ -152,8 +152,23 @@ def test_zero_draft_probability_raises():
         accept_reject(p, q, torch.tensor([[3]]), generator=torch.Generator().manual_seed(0))
 
 
+@pytest.mark.parametrize("custom", [False, True])
+@pytest.mark.parametrize("bad_id", [5, 6, -1])
+def test_draft_id_outside_vocab_raises(custom, bad_id):
+    """A draft id outside [0, V) is range-checked on the device (it is never
+    used as an index) and raises ValueError on the fused path and on the
+    custom-residual path alike; the reference's gather raises too."""
+    p = t64(P).expand(1, 3, 5).contiguous()
+    q = t64(Q).expand(1, 2, 5).contiguous()
+    draft = torch.tensor([[2, bad_id]])
+    kw = {"residual": lambda pp, qq: torch.clamp(pp - qq, min=0.0)} if custom else {}
+    with pytest.raises(ValueError, match="vocabulary"):
+        accept_reject(p, q, draft, generator=torch.Generator().manual_seed(0), **kw)
+    torch.cuda.synchronize()
+
+
 def _golden_inputs(case):
-    from make_golden import accept_inputs
+    from specdec.workloads import accept_inputs
 
     dtype = getattr(torch, case["dtype"])
     if case["p"] is not None:
