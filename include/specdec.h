@@ -11,6 +11,8 @@
  *   SPECDEC_EINVAL       1  a size, stride or pointer argument is out of range
  *   SPECDEC_EHIP         2  the HIP launch failed (hipGetLastError)
  *   SPECDEC_EUNSUPPORTED 3  a shape the kernels do not implement (e.g. head_dim != 64)
+ *   SPECDEC_ENOSCRATCH   4  the call needs more scratch than the library's static
+ *                           buffer holds (specdec_paged_attention_static only)
  *
  * Data-dependent conditions that the reference raises on (a drafted token
  * with zero draft probability, a double free) are reported through status
@@ -44,6 +46,7 @@ extern "C" {
 #define SPECDEC_EINVAL 1
 #define SPECDEC_EHIP 2
 #define SPECDEC_EUNSUPPORTED 3
+#define SPECDEC_ENOSCRATCH 4
 
 #define SPECDEC_F32 0
 #define SPECDEC_F64 1
@@ -293,6 +296,36 @@ int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
                                  int32_t max_kv_len, int32_t split_tokens,
                                  float *workspace, int64_t workspace_floats, void *out,
                                  int64_t out_token_stride, void *stream);
+
+/* fp32 split partials the library holds per GPU for
+ * specdec_paged_attention_static (8 MiB). */
+#define SPECDEC_STATIC_PARTIAL_FLOATS (2 * 1024 * 1024)
+
+/* specdec_paged_attention without a workspace argument: the split partials
+ * of calls that need them live in a file-scope device array of the library
+ * (SPECDEC_STATIC_PARTIAL_FLOATS floats, one copy per GPU, held until the
+ * process ends), so the call allocates nothing and takes no buffer beyond
+ * its inputs and outputs.  A call whose partials would not fit returns
+ * SPECDEC_ENOSCRATCH before anything is launched (specdec_attention_workspace
+ * bounds the need from above; calls answered by one workgroup per tile, as
+ * at most four 512-token splits, or the tiled grid, need none).  Every call
+ * on a GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two threads) race, so order them.  The array needs no clearing:
+ * each call writes every partial it reads.  The first call on a device
+ * looks the array's address up (hipGetSymbolAddress) with that device
+ * current.
+ * No counterpart in the reference (whose attention is
+ * lm/forward.py:44-49,62-63 on torch): it is for callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation. */
+int specdec_paged_attention_static(const void *q, int dtype, int64_t q_token_stride,
+                                   const void *k_pool, const void *v_pool,
+                                   const int32_t *tables, int64_t table_stride,
+                                   const int32_t *meta, int32_t batch, int32_t width,
+                                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t block_size, float scale, int32_t max_kv_len,
+                                   int32_t split_tokens, void *out,
+                                   int64_t out_token_stride, void *stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace specdec {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -1136,9 +1138,18 @@ static int cu_count() {
   return counts[dev];
 }
 
-static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width, int32_t n_heads,
-                            int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_kv_len,
-                            int32_t split_tokens, float *workspace, int64_t workspace_floats, void *stream) {
+// Grid of one call: the split, the kernel family and how many split
+// partials per unit the workspace must hold.
+struct AttnPlan {
+  int64_t units = 0;       // (row, kv head, query tile) workgroups
+  int64_t need_floats = 0; // workspace floats this call reads and writes
+  bool single = false;     // one 16-wave workgroup per unit, no combine
+  bool nothing = false;    // no work: the call returns at once
+};
+
+static int plan_attention(AttnArgs &a, AttnPlan &plan, int dtype, int32_t batch, int32_t width, int32_t n_heads,
+                          int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_kv_len,
+                          int32_t split_tokens) {
   if (batch < 0 || width < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads ||
       block_size <= 0 || max_kv_len < 0)
     return SPECDEC_EINVAL;
@@ -1149,7 +1160,11 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
     if (dtype != SPECDEC_BF16 || block_size % 16 != 0 || width > kStage) return SPECDEC_EUNSUPPORTED;
     if (a.hdim <= 0 || a.hdim % 8 != 0 || ((uintptr_t)a.hidden & 15) != 0) return SPECDEC_EINVAL;
   }
-  if (batch == 0 || width == 0 || max_kv_len == 0) return SPECDEC_OK;
+  if (dtype != SPECDEC_BF16 && dtype != SPECDEC_F32) return SPECDEC_EINVAL;
+  if (batch == 0 || width == 0 || max_kv_len == 0) {
+    plan.nothing = true;
+    return SPECDEC_OK;
+  }
   if (!a.q || !a.k || !a.v || !a.tables || !a.meta || !a.out) return SPECDEC_EINVAL;
   a.batch = batch;
   a.width = width;
@@ -1163,7 +1178,6 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
                                : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
-  a.ws = workspace;
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
   // bf16 tiles with more than four splits (at most kTSplits), when every CU
   // gets a tile and a tile's live rows fit kTRows, run tiled: one 16-wave
@@ -1174,21 +1188,24 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
   // bf16 tiles with at most four splits (or one flat split, or tiled) run
   // in one 16-wave workgroup; otherwise one 4-wave workgroup per split +
   // combine
-  const bool single = dtype == SPECDEC_BF16 && (a.flat || a.tiled || a.max_splits <= 4);
-  a.parts = single ? 1 : a.max_splits;
-  if (a.parts > 1) {
-    if (!workspace) return SPECDEC_EINVAL;
-    if (workspace_floats < units * a.parts * kPart) return SPECDEC_EINVAL;
-  }
+  plan.single = dtype == SPECDEC_BF16 && (a.flat || a.tiled || a.max_splits <= 4);
+  a.parts = plan.single ? 1 : a.max_splits;
   if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
+  plan.units = units;
+  plan.need_floats = a.parts > 1 ? units * a.parts * kPart : 0;
+  return SPECDEC_OK;
+}
+
+static int run_attention(AttnArgs &a, const AttnPlan &plan, int dtype, int32_t block_size, void *stream) {
   hipStream_t s = as_stream(stream);
   const bool bs16 = (block_size % 16) == 0;
+  const int64_t units = plan.units;
   dim3 grid((unsigned)units, (unsigned)a.parts);
   if (a.tiled) {
     dim3 block(16 * kWave);
     if (block_size == 16) attention_bf16_kernel<1, 16, true><<<grid, block, 0, s>>>(a);
     else attention_bf16_kernel<2, 16, true><<<grid, block, 0, s>>>(a);
-  } else if (single) {
+  } else if (plan.single) {
     dim3 block(16 * kWave);
     if (block_size == 16) attention_bf16_kernel<1, 16><<<grid, block, 0, s>>>(a);
     else if (bs16) attention_bf16_kernel<2, 16><<<grid, block, 0, s>>>(a);
@@ -1205,12 +1222,10 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
     if (block_size == 16) attention_bf16_kernel<1, 4><<<grid, block, 0, s>>>(a);
     else if (bs16) attention_bf16_kernel<2, 4><<<grid, block, 0, s>>>(a);
     else attention_bf16_kernel<0, 4><<<grid, block, 0, s>>>(a);
-  } else if (dtype == SPECDEC_F32) {
+  } else {
     dim3 block(kAttnThreads);
     if (bs16) attention_f32_kernel<true><<<grid, block, 0, s>>>(a);
     else attention_f32_kernel<false><<<grid, block, 0, s>>>(a);
-  } else {
-    return SPECDEC_EINVAL;
   }
   if (a.parts > 1) {
     dim3 cg((unsigned)units), cb(kAttnThreads);
@@ -1226,6 +1241,48 @@ static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width
     }
   }
   return launch_status();
+}
+
+static int launch_attention(AttnArgs &a, int dtype, int32_t batch, int32_t width, int32_t n_heads,
+                            int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_kv_len,
+                            int32_t split_tokens, float *workspace, int64_t workspace_floats, void *stream) {
+  AttnPlan plan;
+  const int st = plan_attention(a, plan, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size,
+                                max_kv_len, split_tokens);
+  if (st != SPECDEC_OK || plan.nothing) return st;
+  if (plan.need_floats > 0 && (!workspace || workspace_floats < plan.need_floats)) return SPECDEC_EINVAL;
+  a.ws = workspace;
+  return run_attention(a, plan, dtype, block_size, stream);
+}
+
+// ---- split partials held by the library ---------------------------------
+// specdec_paged_attention_static's workspace: one array per GPU the library
+// runs on (each device holds its own copy, at its own address, until the
+// process ends).  In host code `static_partials` names a host-side stand-in,
+// not device memory: its device address on the current device comes from
+// hipGetSymbolAddress, looked up once per device and kept in
+// static_partials_ptr[].  Partials need no initialisation (every slot the
+// combine reads was written by the same call's split kernel), so a call
+// clears nothing; calls that overlap on one GPU race for the array.
+constexpr int64_t kStaticPartialFloats = SPECDEC_STATIC_PARTIAL_FLOATS;
+static __device__ __align__(256) float static_partials[kStaticPartialFloats];
+
+constexpr int kMaxDevices = 64;
+static float *static_partials_ptr[kMaxDevices];
+static std::mutex static_partials_lock;
+
+// Device address of this device's static_partials (the device must be
+// current), or null if HIP cannot provide it.
+static float *static_partials_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> hold(static_partials_lock);
+  if (!static_partials_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(static_partials)) != hipSuccess || !p) return nullptr;
+    static_partials_ptr[dev] = static_cast<float *>(p);
+  }
+  return static_partials_ptr[dev];
 }
 
 SPECDEC_API int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
@@ -1284,4 +1341,36 @@ SPECDEC_API int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token
   a.out_stride = out_token_stride;
   return launch_attention(a, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size, max_kv_len,
                           split_tokens, workspace, workspace_floats, stream);
+}
+
+SPECDEC_API int specdec_paged_attention_static(const void *q, int dtype, int64_t q_token_stride,
+                                               const void *k_pool, const void *v_pool,
+                                               const int32_t *tables, int64_t table_stride,
+                                               const int32_t *meta, int32_t batch, int32_t width,
+                                               int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                               int32_t block_size, float scale, int32_t max_kv_len,
+                                               int32_t split_tokens, void *out, int64_t out_token_stride,
+                                               void *stream) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_stride = q_token_stride;
+  a.rope = 0;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.meta = meta;
+  a.scale = scale;
+  a.out = out;
+  a.out_stride = out_token_stride;
+  AttnPlan plan;
+  const int st = plan_attention(a, plan, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size,
+                                max_kv_len, split_tokens);
+  if (st != SPECDEC_OK || plan.nothing) return st;
+  if (plan.need_floats > kStaticPartialFloats) return SPECDEC_ENOSCRATCH;
+  if (plan.need_floats > 0) {
+    a.ws = static_partials_on_current_device();
+    if (!a.ws) return SPECDEC_EHIP;
+  }
+  return run_attention(a, plan, dtype, block_size, stream);
 }

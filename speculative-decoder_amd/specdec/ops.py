@@ -10,7 +10,7 @@ import torch
 
 from specdec._lib import lib
 
-OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
+OK, EINVAL, EHIP, EUNSUPPORTED, ENOSCRATCH = 0, 1, 2, 3, 4
 F32, F64, BF16 = 0, 1, 2
 
 _DTYPES = {torch.float32: F32, torch.float64: F64, torch.bfloat16: BF16}
@@ -23,7 +23,8 @@ class KernelError(RuntimeError):
 def _check(status: int, name: str) -> None:
     if status == OK:
         return
-    what = {EINVAL: "invalid argument", EHIP: "HIP launch failed", EUNSUPPORTED: "unsupported shape"}
+    what = {EINVAL: "invalid argument", EHIP: "HIP launch failed", EUNSUPPORTED: "unsupported shape",
+            ENOSCRATCH: "needs more split partials than the library's static buffer holds"}
     err = NotImplementedError if status == EUNSUPPORTED else KernelError
     raise err(f"{name}: {what.get(status, 'error')} (status {status})")
 
@@ -414,6 +415,22 @@ def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, widt
                                        split_tokens, ws.floats.data_ptr(), ws.floats.numel(), out.data_ptr(),
                                        out_token_stride, stream())
     _check(st, "paged_attention")
+    return out
+
+
+def paged_attention_static(q, q_token_stride, k_pool, v_pool, tables, meta, batch, width, n_heads, n_kv_heads,
+                           head_dim, block_size, scale, max_kv_len, out, out_token_stride, split_tokens: int = 0):
+    """paged_attention with no workspace: split partials live in the
+    library's own per-GPU buffer (specdec_paged_attention_static), so the
+    call allocates nothing.  Raises KernelError if the call needs more
+    partials than that buffer holds; calls overlapping on one GPU race."""
+    _qkv_side(gpu(q, "q").device, q, None, None, meta, batch, width, tables, k_pool, v_pool, out)
+    st = lib().specdec_paged_attention_static(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
+                                              v_pool.data_ptr(), tables.data_ptr(), tables.stride(0),
+                                              meta.data_ptr(), batch, width, n_heads, n_kv_heads, head_dim,
+                                              block_size, float(scale), max_kv_len, split_tokens, out.data_ptr(),
+                                              out_token_stride, stream())
+    _check(st, "paged_attention_static")
     return out
 
 
