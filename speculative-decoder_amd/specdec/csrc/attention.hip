@@ -127,13 +127,6 @@ __device__ __forceinline__ int64_t block_of(const AttnArgs &a, const TileInfo &t
   return a.tables[(int64_t)ti.row * a.table_stride + pos / a.bs];
 }
 
-// RoPE of one (x1, x2) pair exactly as the append kernel computes it: each
-// product and the sum rounded on their own (no fused multiply-add).
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &y1, float &y2) {
-  y1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
-}
-
 // Fused append: this workgroup writes kv head h of every new token whose
 // position lies in [lo, hi) -- its own split -- rotated k and plain v, into
 // the paged pools, before it reads any key.  Workgroups whose ranges

@@ -120,10 +120,9 @@ __global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, in
     float x1 = to_f32(x[i]), x2 = to_f32(x[i + half]);
     if (head < H + Hkv) {
       // q*cos + rotate_half(q)*sin, each product and the sum rounded
-      // separately (no fused multiply-add), cos/sin in fp32
-      const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
-      const float y1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-      const float y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+      // separately (rope_pair), cos/sin in fp32
+      float y1, y2;
+      rope_pair(x1, x2, cos_t[pos * half + i], sin_t[pos * half + i], y1, y2);
       x1 = y1;
       x2 = y2;
       if (head < H) {

@@ -33,6 +33,20 @@ template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(f
   return __float2bfloat16(x);  // round to nearest even
 }
 
+// ---- RoPE -----------------------------------------------------------------
+// transformers' q * cos + rotate_half(q) * sin for one (x1, x2) pair, with
+// each product and each sum rounded on its own, as the separate elementwise
+// ops of the reference round them.  hipcc contracts a * b - c * d into a
+// fused multiply-add by default (one rounding fewer, so a nearly cancelling
+// pair can land one bf16 step away once rounded), so contraction is
+// switched off for these four products and two sums.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &y1, float &y2) {
+#pragma clang fp contract(off)
+  const float x1c = x1 * c, x2s = x2 * s, x2c = x2 * c, x1s = x1 * s;
+  y1 = x1c - x2s;
+  y2 = x2c + x1s;
+}
+
 // ---- wavefront reductions (all 64 lanes participate) --------------------
 template <typename T> __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll

@@ -28,7 +28,21 @@ def make_cache(layers, hkv, d, num_blocks, bs, dtype, seed):
     return cache
 
 
+def padded(rows: list[torch.Tensor], width: int) -> torch.Tensor:
+    """Per-row [Hkv, n_b, d] host tensors -> [B, Hkv, width, d] fp32, zeros past n_b."""
+    hkv, d = rows[0].shape[0], rows[0].shape[2]
+    out = torch.zeros(len(rows), hkv, width, d)
+    for b, r in enumerate(rows):
+        out[b, :, : r.shape[1]] = r.float()
+    return out
+
+
 def run_case(batch, lengths, h, hkv, bs, dtype, t_new, seed, rollback=True):
+    """Two verify rounds over a shuffled pool, each followed by a rollback of
+    a seeded number of rejected positions.  The expected output is SDPA over
+    the K/V the test wrote, kept on the host (appends concatenated, rollbacks
+    cut), never read back from the device; the device copy (cache.gather)
+    must equal that host copy bit for bit."""
     d = 64
     g = torch.Generator().manual_seed(seed)
     nb = sum((L + 2 * t_new + 2 * bs) // bs + 1 for L in lengths) + 8
@@ -41,6 +55,8 @@ def run_case(batch, lengths, h, hkv, bs, dtype, t_new, seed, rollback=True):
     kh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(dtype)
     vh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(dtype)
     cache.write(0, step, kh.cuda(), vh.cuda())
+    host_k = [kh[b, :, : lengths[b]] for b in range(batch)]
+    host_v = [vh[b, :, : lengths[b]] for b in range(batch)]
     outs = []
     for rnd in range(2):
         step = cache.append(ids, [t_new] * batch)
@@ -48,20 +64,25 @@ def run_case(batch, lengths, h, hkv, bs, dtype, t_new, seed, rollback=True):
         kn = torch.randn(batch, hkv, t_new, d, generator=g).to(dtype)
         vn = torch.randn(batch, hkv, t_new, d, generator=g).to(dtype)
         cache.write(0, step, kn.cuda(), vn.cuda())
+        host_k = [torch.cat([host_k[b], kn[b]], dim=1) for b in range(batch)]
+        host_v = [torch.cat([host_v[b], vn[b]], dim=1) for b in range(batch)]
         out = torch.zeros(batch, t_new, h * d, dtype=dtype, device="cuda")
         qd = q.reshape(batch, t_new, h * d).cuda()
         ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch,
                             t_new, h, hkv, d, bs, d ** -0.5, step.max_total, out, out.stride(1))
-        k_all, v_all = cache.gather(0, step)
-        want = of.attention(q.transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
-                            torch.tensor(step.past), torch.tensor(step.total), d ** -0.5)
+        k_all, v_all = padded(host_k, step.max_total), padded(host_v, step.max_total)
+        dev_k, dev_v = cache.gather(0, step)
+        assert torch.equal(dev_k.cpu().float(), k_all) and torch.equal(dev_v.cpu().float(), v_all)
+        want = of.attention(q.transpose(1, 2).float(), k_all, v_all, torch.tensor(step.past), torch.tensor(step.total),
+                            d ** -0.5)
         got = out.view(batch, t_new, h, d).transpose(1, 2).float().cpu()
         outs.append((got, want))
         if rollback:
             rng = random.Random(seed * 7 + rnd)
-            for s in ids:
-                a = rng.randint(0, t_new - 1)
-                cache.truncate(s, step.past[ids.index(s)] + 1 + a)
+            for b, s in enumerate(ids):
+                keep = step.past[b] + 1 + rng.randint(0, t_new - 1)
+                cache.truncate(s, keep)
+                host_k[b], host_v[b] = host_k[b][:, :keep], host_v[b][:, :keep]
     return outs
 
 
@@ -165,31 +186,17 @@ def test_prefill_many_query_tiles():
 def test_repeated_split_combines_stay_exact():
     """Many back-to-back launches over the same workspace (every call splits
     9 ways and combines in a second kernel): each result is compared with
-    SDPA, so a stale or overwritten partial shows."""
-    d, h, hkv, bs, L = 64, 32, 32, 16, 4096
+    SDPA over the host K/V, so a stale or overwritten partial shows."""
+    h = 32
+    cache, step, _, host = _filled(1, [4096], seed=11)
     g = torch.Generator().manual_seed(11)
-    cache = make_cache(1, hkv, d, 300, bs, torch.bfloat16, 4)
-    cache.add(0)
-    step = cache.append([0], [L])
-    cache.write(0, step, torch.randn(1, hkv, L, d, generator=g).to(torch.bfloat16).cuda(),
-                torch.randn(1, hkv, L, d, generator=g).to(torch.bfloat16).cuda())
-    step = cache.append([0], [5])
-    cache.write(0, step, torch.randn(1, hkv, 5, d, generator=g).to(torch.bfloat16).cuda(),
-                torch.randn(1, hkv, 5, d, generator=g).to(torch.bfloat16).cuda())
-    k_all, v_all = cache.gather(0, step)
     outs, qs = [], []
     for i in range(40):
-        q = torch.randn(1, 5, h * d, generator=g).to(torch.bfloat16)
-        qd = q.cuda()
-        out = torch.empty(1, 5, h * d, dtype=torch.bfloat16, device="cuda")
-        ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 1, 5, h, hkv,
-                            d, bs, 0.125, step.max_total, out, out.stride(1))
-        outs.append(out)
-        qs.append(q)
-    for q, out in zip(qs, outs):
-        want = of.attention(q.view(1, 5, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
-                            torch.tensor([L]), torch.tensor([L + 5]), 0.125)
-        assert (out.view(1, 5, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
+        qd = torch.randn(1, 5, h * 64, generator=g).to(torch.bfloat16).cuda()
+        outs.append(_attend(cache, step, qd, None))
+        qs.append(qd)
+    for qd, out in zip(qs, outs):
+        assert (_got(out) - _want(qd, step, host)).abs().max().item() < 2e-2
 
 
 @pytest.mark.parametrize("split", [256, 512, 2048, -1])
@@ -198,28 +205,11 @@ def test_explicit_split_sizes(split, heads):
     """Caller-chosen splits against SDPA; -1 is the draft's flat policy (one
     16-wave workgroup striding every key)."""
     h, hkv = heads
-    d, bs = 64, 16
-    g = torch.Generator().manual_seed(split + h)
-    cache = make_cache(1, hkv, d, 400, bs, torch.bfloat16, 9)
-    ids = [0, 1]
-    for s in ids:
-        cache.add(s)
-    lengths = [1500, 333]
-    step = cache.append(ids, lengths)
-    cache.write(0, step, torch.randn(2, hkv, 1500, d, generator=g).to(torch.bfloat16).cuda(),
-                torch.randn(2, hkv, 1500, d, generator=g).to(torch.bfloat16).cuda())
-    step = cache.append(ids, [1, 1])
-    cache.write(0, step, torch.randn(2, hkv, 1, d, generator=g).to(torch.bfloat16).cuda(),
-                torch.randn(2, hkv, 1, d, generator=g).to(torch.bfloat16).cuda())
-    q = torch.randn(2, 1, h * d, generator=g).to(torch.bfloat16)
-    qd = q.cuda()
-    out = torch.zeros(2, 1, h * d, dtype=torch.bfloat16, device="cuda")
-    ops.paged_attention(qd, qd.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, 1, h, hkv, d, bs,
-                        0.125, step.max_total, out, out.stride(1), ops.AttentionWorkspace(qd.device), split)
-    k_all, v_all = cache.gather(0, step)
-    want = of.attention(q.view(2, 1, h, d).transpose(1, 2).float(), k_all.cpu().float(), v_all.cpu().float(),
-                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
-    assert (out.view(2, 1, h, d).transpose(1, 2).float().cpu() - want).abs().max().item() < 2e-2
+    cache, step, q, host = _filled(2, [1500, 333], seed=split + h, h=h, hkv=hkv, t_new=1)
+    out = torch.zeros(2, 1, h * 64, dtype=torch.bfloat16, device="cuda")
+    ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, 1, h, hkv, 64, 16,
+                        0.125, step.max_total, out, out.stride(1), ops.AttentionWorkspace(q.device), split)
+    assert (_got(out, h) - _want(q, step, host, h)).abs().max().item() < 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -263,26 +253,44 @@ def test_fused_rope_append_equals_separate_kernels(dtype, bs, t_new, lengths):
 
 def _filled(batch, lengths, seed, h=32, hkv=32, t_new=5):
     """A bf16 cache of `batch` rows with lengths[b] cached keys each (random
-    K/V, shuffled blocks, block 16), t_new more appended, and q for them."""
+    K/V, shuffled blocks, block 16), t_new more appended, and q for them.
+    The K/V written are kept on the host: returns (cache, step, q, host)
+    with host = (K, V) [B, Hkv, max_total, d] fp32, zeros past each row."""
     d, bs = 64, 16
     g = torch.Generator().manual_seed(seed)
     cache = make_cache(1, hkv, d, sum((n + t_new) // bs + 2 for n in lengths) + 8, bs, torch.bfloat16, seed)
     ids = list(range(batch))
     for s in ids:
         cache.add(s)
-    step = cache.append(ids, [n + t_new for n in lengths])
-    t_max = max(lengths) + t_new
-    cache.write(0, step, torch.randn(batch, hkv, t_max, d, generator=g).to(torch.bfloat16).cuda(),
-                torch.randn(batch, hkv, t_max, d, generator=g).to(torch.bfloat16).cuda())
-    for s, n in zip(ids, lengths):
-        cache.truncate(s, n)
+    step = cache.append(ids, list(lengths))
+    kh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(torch.bfloat16)
+    vh = torch.randn(batch, hkv, max(lengths), d, generator=g).to(torch.bfloat16)
+    cache.write(0, step, kh.cuda(), vh.cuda())
     step = cache.append(ids, [t_new] * batch)
+    kn = torch.randn(batch, hkv, t_new, d, generator=g).to(torch.bfloat16)
+    vn = torch.randn(batch, hkv, t_new, d, generator=g).to(torch.bfloat16)
+    cache.write(0, step, kn.cuda(), vn.cuda())
     q = torch.randn(batch, t_new, h * d, generator=g).to(torch.bfloat16).cuda()
-    return cache, step, q
+    host = tuple(padded([torch.cat([x[b, :, :n], y[b]], dim=1) for b, n in enumerate(lengths)], step.max_total)
+                 for x, y in ((kh, kn), (vh, vn)))
+    return cache, step, q, host
+
+
+def _want(q, step, host, h=32):
+    """SDPA over the host K/V for q [B, T, h*64] (the reference's attention step)."""
+    b, t_new = q.shape[0], q.shape[1]
+    return of.attention(q.view(b, t_new, h, 64).transpose(1, 2).float().cpu(), host[0], host[1],
+                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
+
+
+def _got(out, h=32):
+    b, t_new = out.shape[0], out.shape[1]
+    return out.view(b, t_new, h, 64).transpose(1, 2).float().cpu()
 
 
 def _attend(cache, step, q, ws, out=None, h=32, hkv=32):
     batch, t_new = q.shape[0], q.shape[1]
+    ws = ws if ws is not None else ops.workspace_for(q.device)
     if out is None:
         out = torch.zeros(batch, t_new, h * 64, dtype=torch.bfloat16, device="cuda")
     ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, t_new, h, hkv,
@@ -305,17 +313,13 @@ def test_split_workspace_shared_across_shapes():
     built = [_filled(b, lengths, seed=40 + i) for i, (b, lengths) in enumerate(_SPLIT_SHAPES)]
     shared = ops.AttentionWorkspace(torch.device("cuda"))
     for rep in range(2):
-        for i, (cache, step, q) in enumerate(built):
+        for i, (cache, step, q, host) in enumerate(built):
             got = _attend(cache, step, q, shared)
             fresh = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
             torch.cuda.synchronize()
             assert torch.equal(got, fresh), (rep, i)
             if rep == 0:
-                b, t_new = q.shape[0], q.shape[1]
-                k_all, v_all = cache.gather(0, step)
-                want = of.attention(q.view(b, t_new, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(),
-                                    v_all.cpu().float(), torch.tensor(step.past), torch.tensor(step.total), 0.125)
-                err = (got.view(b, t_new, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+                err = (_got(got) - _want(q, step, host)).abs().max().item()
                 assert err < 2e-2, (i, err)
 
 
@@ -328,10 +332,10 @@ def test_split_graph_replays_match_eager(shape):
     from lm.graphs import _capture
 
     if shape == "split":
-        cache, step, q = _filled(2, [5000, 2600], seed=61)
+        cache, step, q, _ = _filled(2, [5000, 2600], seed=61)
     else:
-        cache, step, q = _filled(8, [3000 + 100 * b for b in range(8)], seed=63)
-    other = _filled(3, [2600, 700, 4500], seed=62)
+        cache, step, q, _ = _filled(8, [3000 + 100 * b for b in range(8)], seed=63)
+    other = _filled(3, [2600, 700, 4500], seed=62)[:3]
     ws = ops.AttentionWorkspace(torch.device("cuda"))
     ws.reserve(1 << 24)  # no growth inside the capture
     want = _attend(cache, step, q, ws)
@@ -353,12 +357,9 @@ def test_ragged_batch8_rows_equal_rows_verified_alone_bitwise():
     the same split path; either way the bits are the same, and the batch
     result matches SDPA."""
     lengths = [7900, 100, 2500, 4100, 600, 7000, 3000, 1500]
-    cache, step, q = _filled(8, lengths, seed=71)
+    cache, step, q, host = _filled(8, lengths, seed=71)
     out8 = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
-    k_all, v_all = cache.gather(0, step)
-    want = of.attention(q.view(8, 5, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(), v_all.cpu().float(),
-                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
-    err = (out8.view(8, 5, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+    err = (_got(out8) - _want(q, step, host)).abs().max().item()
     assert err < 2e-2, err
     for row, n in enumerate(lengths):
         cache.truncate(row, n)
@@ -377,12 +378,9 @@ def test_tiled_batch8_rows_equal_rows_verified_alone_bitwise():
     batch 1 (16-wave or split + combine path) gives the same bits, and the
     batch result matches SDPA."""
     lengths = [6100, 100, 2500, 4100, 600, 5000, 3000, 1500]
-    cache, step, q = _filled(8, lengths, seed=81)
+    cache, step, q, host = _filled(8, lengths, seed=81)
     out8 = _attend(cache, step, q, ops.AttentionWorkspace(torch.device("cuda")))
-    k_all, v_all = cache.gather(0, step)
-    want = of.attention(q.view(8, 5, 32, 64).transpose(1, 2).float().cpu(), k_all.cpu().float(), v_all.cpu().float(),
-                        torch.tensor(step.past), torch.tensor(step.total), 0.125)
-    err = (out8.view(8, 5, 32, 64).transpose(1, 2).float().cpu() - want).abs().max().item()
+    err = (_got(out8) - _want(q, step, host)).abs().max().item()
     assert err < 2e-2, err
     for row, n in enumerate(lengths):
         cache.truncate(row, n)
@@ -490,7 +488,7 @@ def test_input_norm_in_attention_equals_prescaled_qkv(batch, lengths, heads, hid
 
 
 def test_input_norm_in_attention_rejects_other_shapes():
-    cache, step, q = _filled(1, [40], 0)
+    cache, step, q, _ = _filled(1, [40], 0)
     h = torch.zeros(1, 20, 64, dtype=torch.bfloat16, device="cuda")
     qkv = torch.zeros(1, 20, 96 * 64, dtype=torch.bfloat16, device="cuda")
     cos = sin = torch.zeros(128, 32, device="cuda")
@@ -498,3 +496,71 @@ def test_input_norm_in_attention_rejects_other_shapes():
     with pytest.raises(ValueError, match="width"):
         ops.rope_paged_attention(qkv, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, 1, 20, 32, 32,
                                  64, 16, 0.125, step.max_total, out, out.stride(1), norm_of=h, eps=1e-5)
+
+
+def _rope_host(x: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """transformers' rotate_half RoPE of x [..., T, 64] (bf16) at positions
+    pos [T], in fp32 with every product and sum rounded on its own, then
+    rounded to bf16 -- where the kernel rounds a rotated q or k."""
+    x = x.float()
+    c, s = cos[pos], sin[pos]  # [T, 32]
+    x1, x2 = x[..., :32], x[..., 32:]
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("width", [256, 1024])
+@pytest.mark.parametrize("heads", [(32, 32), (9, 3)])
+@pytest.mark.parametrize("past", [[0, 0], [100, 0]])
+def test_bf16_prefill_matches_oracle(width, heads, past):
+    """A prompt-sized append (256 or 1024 new tokens, right-padded rows of
+    different lengths, from an empty cache or after a cached chunk) through
+    the fused RoPE + append + attention launch, in bf16, against the
+    reference's prefill step restated on the host (lm/forward.py:40-49,
+    53, 60-63): RoPE of q and k, the new K/V appended after the cached
+    ones, causal SDPA.  The pool must hold the host's rotated k and v bit
+    for bit."""
+    from lm.model import LlamaShape, rope_tables
+
+    h, hkv = heads
+    d, bs, batch = 64, 16, 2
+    n_new = [width, width - 37]
+    theta = 130000.0 if h == 32 else 100000.0
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=theta)
+    cos_h, sin_h = rope_tables(shape, 2048)
+    cos, sin = cos_h.cuda(), sin_h.cuda()
+    g = torch.Generator().manual_seed(width + h + past[0])
+    cache = make_cache(1, hkv, d, sum((p + n) // bs + 2 for p, n in zip(past, n_new)) + 8, bs, torch.bfloat16, 5)
+    ids = list(range(batch))
+    for s in ids:
+        cache.add(s)
+    hist_k = [torch.randn(hkv, p, d, generator=g).to(torch.bfloat16) for p in past]
+    hist_v = [torch.randn(hkv, p, d, generator=g).to(torch.bfloat16) for p in past]
+    if max(past) > 0:
+        step = cache.append(ids, past)
+        cache.write(0, step, padded(hist_k, max(past)).to(torch.bfloat16).cuda(),
+                    padded(hist_v, max(past)).to(torch.bfloat16).cuda())
+    step = cache.append(ids, n_new)
+    qkv = torch.randn(batch, width, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16)
+    out = torch.zeros(batch, width, h * d, dtype=torch.bfloat16, device="cuda")
+    x = qkv.cuda()
+    ops.rope_paged_attention(x, cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, width, h, hkv,
+                             d, bs, 0.125, step.max_total, out, out.stride(1))
+    # host: rotated q/k of the real tokens, K/V after the cached chunk
+    q_all = qkv[..., : h * d].view(batch, width, h, d).transpose(1, 2)
+    k_new = qkv[..., h * d:(h + hkv) * d].view(batch, width, hkv, d).transpose(1, 2)
+    v_new = qkv[..., (h + hkv) * d:].view(batch, width, hkv, d).transpose(1, 2)
+    host_k, host_v, q_rot = [], [], torch.zeros(batch, h, width, d)
+    for b in range(batch):
+        pos = torch.arange(past[b], past[b] + n_new[b])
+        q_rot[b, :, : n_new[b]] = _rope_host(q_all[b, :, : n_new[b]], pos, cos_h, sin_h).float()
+        host_k.append(torch.cat([hist_k[b], _rope_host(k_new[b, :, : n_new[b]], pos, cos_h, sin_h)], dim=1))
+        host_v.append(torch.cat([hist_v[b], v_new[b, :, : n_new[b]]], dim=1))
+    k_all, v_all = padded(host_k, step.max_total), padded(host_v, step.max_total)
+    dev_k, dev_v = cache.gather(0, step)
+    assert torch.equal(dev_k.cpu().float(), k_all) and torch.equal(dev_v.cpu().float(), v_all)
+    want = of.attention(q_rot, k_all, v_all, torch.tensor(past), torch.tensor(step.total), 0.125)
+    got = out.view(batch, width, h, d).transpose(1, 2).float().cpu()
+    for b in range(batch):
+        err = (got[b, :, : n_new[b]] - want[b, :, : n_new[b]]).abs()
+        assert err.max().item() < 2e-2 and err.mean().item() < 2e-3, (b, err.max().item(), err.mean().item())
