@@ -1,32 +1,43 @@
 """Benchmark of the speculative-decoding hot path on one MI355X.
 
 Headline (`value`): emitted tokens/s of greedy speculative decoding at batch 1
-with k = 4 and paged KV (block size 16), target with SmolLM2-1.7B shapes and
-draft with SmolLM2-135M shapes, random-init bf16 weights, a 256-token seeded
-prompt and 128 new tokens.  One step = one `generate` call.
+with k = 4 and paged KV (block size 16); target with SmolLM2-1.7B shapes, draft
+with SmolLM2-135M shapes, random-init bf16 weights, a 256-token seeded prompt,
+128 new tokens.  One step = one `generate` call.  The line's `e2e` object adds
+the request's roofline fraction (algorithmic bytes of every forward of the
+request -- weights read as stored, K/V read and written -- over its wall time),
+plain greedy decoding on the same GPU, per-round p50/p99 latencies, a
+truncated-target draft sweep and a copy draft (acceptance 1).
 
 `roofline`: the verify paged-attention kernel at B = 8, context 4096, 32/32
-heads of 64, 5 query tokens, shuffled block table (config 2's largest
-batch): algorithmic bytes per launch (K+V of 8 x 4101 positions + Q in + O
-out + block tables) over the mean launch time measured with HIP events on
-the stream it runs on.  B = 1 sits beside it in the line.
+heads of 64, 5 query tokens, shuffled block table (config 2's largest batch):
+algorithmic bytes per launch (K+V of 8 x 4101 positions + Q in + O out + block
+tables) over the mean launch time, from HIP events on the launching stream
+around graph replays of back-to-back launches.  B = 1 sits beside it.
 
-`cpu_baseline`: the oracle's CPU restatement of the reference loop
-(gather + SDPA forward, host accept-reject) on the same weights, timed on a
-bounded sample of the same request.
+`cpu_baseline`: the oracle's CPU restatement of the reference loop (gather +
+SDPA forward, host accept-reject) on the same weights and prompt, its rounds
+interleaved one for one with the GPU loop's rounds, warm-up rounds excluded,
+p50/p99 per round.
 
-`kernels`: per-kernel times for the other workloads (accept-reject at
-V = 49152, n-gram lookup at batch 16, cache append/rollback, attention over
+`batched_sampled`: config 5 -- batches of 8 and 32, T = 0.8, k = 4 and 8,
+1024-token prompts with planted repetition decoded to a 4096-token context,
+model and n-gram drafters -- with in-loop accept-kernel, verify and attention
+times.  `kernels`: per-kernel times for configs 1-3 and 2' (accept-reject at
+V = 49152, n-gram lookup at batch 16, cache append and rollback, attention over
 the batch x context grid), each with its algorithmic bytes and GB/s.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only e2e|attention|kernels]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only ...]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
+import subprocess
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -51,6 +62,11 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def pct(xs: list[float], q: float) -> float:
+    s = sorted(xs)
+    return s[min(len(s) - 1, max(0, round(q / 100 * (len(s) - 1))))]
+
+
 # ----------------------------------------------------------------- models ---
 def build_models(dtype=torch.bfloat16, seed=0):
     from lm.model import SMOLLM2_135M, SMOLLM2_1_7B, Llama, random_state_dict
@@ -62,40 +78,72 @@ def build_models(dtype=torch.bfloat16, seed=0):
             t_state, d_state)
 
 
-def mean_accept_len(stats):
-    """Accepted draft tokens per (sequence, round)."""
-    return stats.accepted / max(len(stats.emitted_per_round), 1)
-
-
 def prompt_ids(seed=0):
     g = torch.Generator().manual_seed(seed)
     return torch.randint(0, V, (PROMPT,), generator=g).tolist()
 
 
-def make_caches(target, draft, new_tokens=NEW_TOKENS):
-    """Target and draft caches sized for one request; reused across requests
-    (sequences are freed at the end of each), as a server would."""
+def caches_for(target, draft, batch=1, context=PROMPT + NEW_TOKENS, k=K):
+    """Target and draft caches sized for `batch` rows of `context` tokens
+    (+ the verify window); reused across requests, as a server would."""
     from cache.kv import KVCache
 
-    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
-    return (KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda"),
-            KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda"))
+    blocks = batch * ((context + 2 * k + 2 * BLOCK) // BLOCK + 2) + 8
+    return (KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda", ),
+            KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda") if draft is not None else None)
 
 
-def run_e2e(target, draft, prompt, caches, new_tokens=NEW_TOKENS):
+def mean_accept_len(stats):
+    """Accepted draft tokens per (sequence, round)."""
+    return stats.accepted / max(len(stats.emitted_per_round), 1)
+
+
+# ------------------------------------------------------ algorithmic bytes ---
+def weight_bytes(llama) -> int:
+    """Bytes of weights one forward reads as stored: every projection of every
+    layer and the output head (embedding rows and norm vectors are noise)."""
+    n = sum(t.numel() * t.element_size() for layer in llama.layers for t in (layer.wqkv, layer.wo, layer.wgu, layer.wd))
+    return n + llama.head_wide.numel() * llama.head_wide.element_size()
+
+
+def kv_bytes_per_position(llama) -> int:
+    """K and V of one token position over every layer."""
+    c = llama.config
+    return c.num_hidden_layers * c.num_key_value_heads * c.head_dim * 2 * llama.embed.element_size()
+
+
+def request_bytes(target, draft, prompt_len: int, stats, k: int) -> int:
+    """Algorithmic HBM bytes of one batch-1 speculative request: the target's
+    and the draft's prefill (weights once, K/V of the prompt written), then per
+    round the k draft steps (weights + K/V read up to each step's position +
+    its write) and the verify (weights + K/V read + k+1 written).  Contexts
+    follow the request's own emitted_per_round."""
+    tw, dw = weight_bytes(target), (weight_bytes(draft) if draft is not None else 0)
+    tkv, dkv = kv_bytes_per_position(target), (kv_bytes_per_position(draft) if draft is not None else 0)
+    total = tw + dw + prompt_len * (tkv + dkv)
+    ctx = prompt_len + 1  # the first token comes from the target's prefill
+    for emitted in stats.emitted_per_round:
+        total += k * dw + sum(ctx + j for j in range(k)) * dkv + k * dkv
+        total += tw + (ctx + k) * tkv
+        ctx += emitted
+    return total
+
+
+# ------------------------------------------------------------------- e2e ---
+def run_e2e(target, draft, prompt, caches, new_tokens=NEW_TOKENS, k=K, drafter=None):
     from spec.draft import ModelDraft
     from spec.loop import generate
 
     tc, dc = caches
-    out, stats = generate(target, tc, ModelDraft(draft, dc), [prompt], new_tokens, k=K,
-                          generator=torch.Generator().manual_seed(0))
+    drafter = drafter if drafter is not None else ModelDraft(draft, dc)
+    out, stats = generate(target, tc, drafter, [prompt], new_tokens, k=k, generator=torch.Generator().manual_seed(0))
     return out[0], stats
 
 
 def bench_e2e(steps, warmup):
     target, draft, t_state, d_state = build_models()
     prompt = prompt_ids()
-    caches = make_caches(target, draft)
+    caches = caches_for(target, draft)
     log("e2e warmup")
     for _ in range(warmup):
         run_e2e(target, draft, prompt, caches)
@@ -108,17 +156,23 @@ def bench_e2e(steps, warmup):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     emitted = sum(len(o) for o in outs)
+    nbytes = request_bytes(target, draft, PROMPT, stats, K)
+    gbs = nbytes * steps / dt / 1e9
     result = {"tokens_per_s": emitted / dt, "ms_per_step": 1000 * dt / steps, "emitted_per_step": len(outs[0]),
               "rounds": stats.rounds, "mean_accept_len": mean_accept_len(stats),
-              "acceptance": stats.accepted / max(stats.drafted, 1)}
+              "acceptance": stats.accepted / max(stats.drafted, 1),
+              "roofline": {"bound": "hbm", "bytes_per_request": nbytes, "achieved": gbs, "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                           "bytes": "target + draft weights as stored (bf16 head read as bf16) per forward, K/V read "
+                                    "and written per position, over the request's own rounds"}}
     # identity check of this output against plain greedy decoding of the target
     from baselines.cached_autoregressive import generate as plain
-    from cache.kv import KVCache
 
-    blocks = (PROMPT + NEW_TOKENS + 2 * BLOCK) // BLOCK + 4
+    plain_cache = caches_for(target, None)[0]
+    plain(target, plain_cache, prompt, NEW_TOKENS)  # warm
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    want = plain(target, KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda"), prompt, NEW_TOKENS)
+    want = plain(target, plain_cache, prompt, NEW_TOKENS)
     torch.cuda.synchronize()
     result["plain_greedy_tokens_per_s"] = NEW_TOKENS / (time.perf_counter() - t1)
     result["identical_to_plain_greedy"] = want == outs[0]
@@ -126,92 +180,60 @@ def bench_e2e(steps, warmup):
     return result, (target, draft, t_state, d_state, prompt, outs[0])
 
 
-def bench_variant_b(target, t_state, prompt, steps=1, n_layers=4, noise=0.002):
-    """Config 4, second variant: the draft is the target's first `n_layers`
-    layers (embeddings, final norm and head shared) plus N(0, noise^2) on
-    every matrix of those layers."""
-    from cache.kv import KVCache
+def bench_truncated_drafts(target, t_state, prompt, depths=(4, 12, 18, 22), noise=0.002):
+    """Config 4's second variant: the draft is the target's first n layers
+    (embeddings, final norm and head shared) plus N(0, noise^2) on every matrix
+    of those layers, swept over the truncation depth."""
     from lm.model import SMOLLM2_1_7B, Llama, perturbed_truncation
-    from spec.draft import ModelDraft
-    from spec.loop import generate
 
-    state, shape = perturbed_truncation(t_state, SMOLLM2_1_7B, n_layers, noise, seed=7)
-    draft = Llama.from_state_dict(shape, state)
-    blocks = (PROMPT + NEW_TOKENS + 2 * K + 2 * BLOCK) // BLOCK + 4
-    tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda")
-    dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda")
-    generate(target, tc, ModelDraft(draft, dc), [prompt], NEW_TOKENS, k=K, generator=torch.Generator().manual_seed(0))
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        out, stats = generate(target, tc, ModelDraft(draft, dc), [prompt], NEW_TOKENS, k=K,
-                              generator=torch.Generator().manual_seed(0))
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    return {"draft": f"target layers 0..{n_layers - 1} + N(0, {noise}^2)", "tokens_per_s": len(out[0]) / dt,
-            "acceptance": stats.accepted / max(stats.drafted, 1),
-            "mean_accept_len": mean_accept_len(stats), "rounds": stats.rounds}
-
-
-def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 8, "model"), (32, 8, "ngram")),
-                  prompt_len=1024, new_tokens=32, temperature=0.8):
-    """Config 5, bounded: batched sampled speculative decoding on seeded
-    1024-token prompts with ~30% planted repetition, `new_tokens` per row.
-    Reports emitted tokens/s, mean accept length, and per round the accept
-    kernel time (HIP events around the call the loop makes) and the verify
-    attention kernel time at that batch and context (graph-replayed)."""
-    import spec.loop as loop_mod
-    from cache.kv import KVCache
-    from specdec.workloads import planted_rows
-    from spec.draft import ModelDraft
-    from spec.loop import generate
-    from spec.ngram import NGramDraft
-
-    results = {}
-    for batch, k, kind in combos:
-        prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
-        blocks = batch * ((prompt_len + new_tokens + 2 * k + 2 * BLOCK) // BLOCK + 2) + 8
-        tc = KVCache.for_model(target.config, blocks, BLOCK, target.dtype, "cuda", )
-        dc = KVCache.for_model(draft.config, blocks, BLOCK, draft.dtype, "cuda") if kind == "model" else None
-        accept_us = []
-        real_accept = loop_mod.accept_reject
-
-        def timed_accept(*a, **kw):
-            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            st.record()
-            v = real_accept(*a, **kw)
-            en.record()
-            en.synchronize()
-            accept_us.append(st.elapsed_time(en) * 1000)
-            return v
-
-        def run():
-            drafter = ModelDraft(draft, dc) if kind == "model" else NGramDraft(V)
-            return generate(target, tc, drafter, prompts, new_tokens, k=k, temperature=temperature,
-                            generator=torch.Generator().manual_seed(5))
-
-        run()  # warm-up: captures the graphs of this shape
-        loop_mod.accept_reject = timed_accept
-        try:
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            outs, stats = run()
-            torch.cuda.synchronize()
-            dt = time.perf_counter() - t0
-        finally:
-            loop_mod.accept_reject = real_accept
-        attn = time_attention(batch, prompt_len + new_tokens // 2, iters=40, t_new=k + 1)
-        results[f"b{batch}_k{k}_{kind}"] = {
-            "tokens_per_s": sum(len(o) for o in outs) / dt, "mean_accept_len": mean_accept_len(stats),
-            "acceptance": stats.accepted / max(stats.drafted, 1),
-            "rounds": stats.rounds, "accept_call_us_per_round": sum(accept_us) / max(len(accept_us), 1),
-            "verify_attention_us_per_layer": attn["us"], "verify_attention_gbs": attn["gbs"],
-            "sample": f"{batch} rows, {prompt_len}-token prompts (~30% planted repetition), {new_tokens} new tokens, "
-                      f"T={temperature}, k={k}"}
-        log(f"batched {batch} {k} {kind}: {results[f'b{batch}_k{k}_{kind}']}")
-        del tc, dc
+    out = {}
+    for n in depths:
+        state, shape = perturbed_truncation(t_state, SMOLLM2_1_7B, n, noise, seed=7)
+        draft = Llama.from_state_dict(shape, state)
+        caches = caches_for(target, draft)
+        run_e2e(target, draft, prompt, caches)  # warm (graph captures)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tokens, stats = run_e2e(target, draft, prompt, caches)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        gbs = request_bytes(target, draft, PROMPT, stats, K) / dt / 1e9
+        out[f"layers_{n}"] = {"draft": f"target layers 0..{n - 1} + N(0, {noise}^2)", "tokens_per_s": len(tokens) / dt,
+                              "acceptance": stats.accepted / max(stats.drafted, 1),
+                              "mean_accept_len": mean_accept_len(stats), "rounds": stats.rounds,
+                              "roofline_frac": gbs / HBM_PEAK_GBS}
+        log(f"truncated draft {n}: {out[f'layers_{n}']}")
+        del draft, caches
         torch.cuda.empty_cache()
-    return results
+    return out
+
+
+def bench_copy_draft(target, prompt, want):
+    """The target as its own draft.  Computing as the verify does
+    (ModelDraft(exact=True)), every drafted token is the target's own greedy
+    choice: every round accepts all k and emits the bonus token -- the
+    accept, bonus and rollback paths at full shapes.  Computing for latency
+    (the default draft arithmetic), near-ties of the bf16 forward break the
+    other way now and then, and acceptance shows how often."""
+    from spec.draft import ModelDraft
+
+    out = {}
+    for name, exact in (("exact", True), ("latency", False)):
+        caches = caches_for(target, target)
+        run_e2e(target, None, prompt, caches, drafter=ModelDraft(target, caches[1], exact=exact))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tokens, stats = run_e2e(target, None, prompt, caches, drafter=ModelDraft(target, caches[1], exact=exact))
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        gbs = request_bytes(target, target, PROMPT, stats, K) / dt / 1e9
+        out[name] = {"tokens_per_s": len(tokens) / dt, "acceptance": stats.accepted / max(stats.drafted, 1),
+                     "mean_accept_len": mean_accept_len(stats), "rounds": stats.rounds,
+                     "emitted_per_round": sorted(set(stats.emitted_per_round)),
+                     "identical_to_plain_greedy": tokens == want, "roofline_frac": gbs / HBM_PEAK_GBS}
+        del caches
+        torch.cuda.empty_cache()
+    return out
 
 
 # ------------------------------------------------------------ attention -----
@@ -241,7 +263,7 @@ def setup_attention(batch, length, seed=0, h=32, hkv=32, d=64, t_new=5, num_bloc
     for s in ids:
         cache.add(s)
     g = torch.Generator(device="cuda").manual_seed(seed)
-    step = cache.append(ids, [length] * batch)
+    cache.append(ids, [length] * batch)
     cache.k.normal_(generator=g)
     cache.v.normal_(generator=g)
     step = cache.append(ids, [t_new] * batch)
@@ -335,8 +357,8 @@ def time_fn(fn, iters=100, graph=False):
 
 
 def bench_kernels(attention_grid=True):
-    from specdec.workloads import planted_rows
     from specdec import ops
+    from specdec.workloads import planted_rows
 
     res = {}
     # config 1: accept-reject, B=1, k=4, V=49152, fp32, T=1
@@ -361,7 +383,10 @@ def bench_kernels(attention_grid=True):
                                     "softmax_gbs": 2 * logit_bytes / us_soft / 1e3,
                                     "softmax_frac_of_peak": 2 * logit_bytes / us_soft / 1e3 / HBM_PEAK_GBS,
                                     "accept_bytes": accept_bytes, "accept_gbs": accept_bytes / us_acc / 1e3,
-                                    "accept_frac_of_peak": accept_bytes / us_acc / 1e3 / HBM_PEAK_GBS}
+                                    "accept_frac_of_peak": accept_bytes / us_acc / 1e3 / HBM_PEAK_GBS,
+                                    "round_us": us_soft + us_acc,
+                                    "round_frac_of_peak": (2 * logit_bytes + accept_bytes) / (us_soft + us_acc) / 1e3
+                                    / HBM_PEAK_GBS}
     # config 3: n-gram, B=16
     for length in (2048, 4096, 8192):
         rows = planted_rows(16, length, V, seed=length)
@@ -382,19 +407,8 @@ def bench_kernels(attention_grid=True):
     app_bytes = 5 * 96 * 64 * 2 + 5 * 64 * 64 * 2
     res["append_b1_t5"] = {"us": us_app, "bytes": app_bytes, "gbs": app_bytes / us_app / 1e3,
                            "frac_of_peak": app_bytes / us_app / 1e3 / HBM_PEAK_GBS}
-    # config 2': one round's rollback of 8 rows (a rejected tail each) and the
-    # regrowth for the next verify: the block plan the cache launches
-    ids = list(range(8))
-    cache8, _, _, _ = setup_attention(8, 1005)  # 1010 cached: the rollback frees a block, the regrowth takes one
-    lens = [cache8.length(s) for s in ids]
-
-    def rollback_and_grow():
-        for s, n in zip(ids, lens):
-            cache8.truncate(s, n - 5 + 1)
-        cache8.append(ids, [4] * 8)
-
-    res["rollback_grow_b8"] = {"us_host_inclusive": time_fn(rollback_and_grow, iters=50)}
-    del cache8
+    del cache
+    res["rollback_grow_b8"] = bench_rollback()
     if not attention_grid:
         return res
     # attention over the config-2 grid
@@ -404,35 +418,330 @@ def bench_kernels(attention_grid=True):
     return res
 
 
-# ------------------------------------------------------------ CPU side ------
-def cpu_baseline(t_state, d_state, prompt, new_tokens=64):
-    """Oracle loop on the host cores: same weights (bf16), same prompt, a
-    bounded number of new tokens."""
-    import oracle.forward as of
-    import oracle.kv as okv
-    from lm.model import SMOLLM2_135M, SMOLLM2_1_7B
-    from oracle.draft import ModelDraft
-    from oracle.loop import generate
+def bench_rollback(batch=8, length=1010):
+    """Config 2': one round's cache bookkeeping at batch 8 as the device sees
+    it -- every row rolls back its rejected tail block (a push) and regrows
+    one block for the next verify (a pop) -- i.e. one block-plan launch.
+    Timed as graph replays of that launch (its pushes and pops balance, so a
+    replay leaves the free stack's depth where it was); plus the host-side
+    round trip of truncate + append that the round loop issues."""
+    from specdec import ops
 
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
+    cache, _, _, _ = setup_attention(batch, length - 5)
+    ids = list(range(batch))
+    lens = [cache.length(s) for s in ids]
+    alloc = cache.allocator
+    rows = [cache.tables[s].row for s in ids]
+    cols = [len(cache.tables[s]) - 1 for s in ids]
+    entries = []
+    for i, (r, c) in enumerate(zip(rows, cols)):
+        entries += [r, c, 1, i]
+    for i, (r, c) in enumerate(zip(rows, cols)):
+        entries += [r, c, 1, i]
+    ent = torch.tensor(entries, dtype=torch.int32, device="cuda")
+    top = alloc._dev_top
+    us = time_fn(lambda: ops.block_plan(cache.table_tensor, alloc._stack, alloc._used, top, ent, batch, batch),
+                 graph=True)
+    # entries read + per block: table read, stack write, mark write (push);
+    # stack read, table write, mark write (pop)
+    nbytes = ent.numel() * 4 + batch * (4 + 4 + 1) * 2
+
+    def host_round():
+        for s, n in zip(ids, lens):
+            cache.truncate(s, n - 5 + 1)
+        cache.append(ids, [4] * batch)
+
+    res = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3, "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS,
+           "host_round_trip_us": time_fn(host_round, iters=50),
+           "what": "block-plan launch: 8 rows push their tail block and pop one (rollback + regrowth)"}
+    del cache
+    return res
+
+
+# ---------------------------------------------------------- config 5 -------
+class LoopTimer:
+    """In-loop kernel timing without a synchronisation in the timed region:
+    HIP events recorded around each accept-reject launch and each verify
+    graph replay on the launching stream, read after the run; and, every
+    `every` rounds, the verify attention replayed over that round's cache
+    state (the round's row metadata and block tables, every layer's pools,
+    read-only: the cache is not changed) as one batch of back-to-back launches
+    between two events."""
+
+    def __init__(self, every: int = 32):
+        self.every = every
+        self.accept, self.verify, self.attention = [], [], []
+        # wall time spent outside the loop's own work: one-time graph
+        # captures of new shapes, and the sampled attention replays
+        self.excluded = 0.0
+        self._round = 0
+
+    def __enter__(self):
+        import lm.graphs as graphs
+        from specdec import ops
+
+        self._ops, self._graphs = ops, graphs
+        self._real_accept = ops.accept_reject
+        self._real_run = graphs.VerifyGraph.run
+        self._real_capture = graphs._capture
+        timer = self
+
+        def accept(*a, **kw):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record()
+            out = timer._real_accept(*a, **kw)
+            en.record()
+            timer.accept.append((st, en))
+            return out
+
+        def verify_run(runner, ids, meta):
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record()
+            out = timer._real_run(runner, ids, meta)
+            en.record()
+            timer.verify.append((st, en))
+            timer._round += 1
+            if timer._round % timer.every == 0:
+                timer._attention_replay(runner, meta)
+            return out
+
+        def capture(run):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = timer._real_capture(run)
+            torch.cuda.synchronize()
+            timer.excluded += time.perf_counter() - t0
+            return out
+
+        ops.accept_reject = accept
+        graphs.VerifyGraph.run = verify_run
+        graphs._capture = capture
+        return self
+
+    def _attention_replay(self, runner, meta):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self._replay_layers(runner, meta)
+        torch.cuda.synchronize()
+        self.excluded += time.perf_counter() - t0
+
+    def _replay_layers(self, runner, meta):
+        ops, cache, llama = self._ops, runner.cache, runner.llama
+        cfg = llama.config
+        b, width = meta.shape[1], runner.ids.shape[1]
+        h, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        q = torch.zeros(b, width, h * d, dtype=llama.dtype, device=cache.device)
+        out = torch.empty_like(q)
+        layers = len(llama.layers)
+        ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, meta, b, width, h, hkv, d,
+                            cache.block_size, llama.scaling, runner.bucket, out, out.stride(1), runner.ws)  # warm
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for i in range(layers):
+            ops.paged_attention(q, q.stride(1), cache.k[i], cache.v[i], cache.table_tensor, meta, b, width, h, hkv,
+                                d, cache.block_size, llama.scaling, runner.bucket, out, out.stride(1), runner.ws)
+        en.record()
+        past = meta[1].tolist()
+        self.attention.append((st, en, layers, attention_bytes(b, past, t_new=width, h=h, hkv=hkv, d=d)))
+
+    def __exit__(self, *exc):
+        self._ops.accept_reject = self._real_accept
+        self._graphs.VerifyGraph.run = self._real_run
+        self._graphs._capture = self._real_capture
+        return False
+
+    def summary(self):
+        torch.cuda.synchronize()
+        acc = [s.elapsed_time(e) * 1000 for s, e in self.accept]
+        ver = [s.elapsed_time(e) * 1000 for s, e in self.verify]
+        att = [(s.elapsed_time(e) * 1000 / n, nbytes) for s, e, n, nbytes in self.attention]
+        out = {"accept_kernel_us_per_round": {"mean": statistics.fmean(acc), "p50": pct(acc, 50), "p99": pct(acc, 99)},
+               "verify_us_per_round": {"mean": statistics.fmean(ver), "p50": pct(ver, 50), "p99": pct(ver, 99)}}
+        if att:
+            us = statistics.fmean(a for a, _ in att)
+            nbytes = statistics.fmean(b for _, b in att)
+            out["verify_attention_us_per_layer"] = us
+            out["verify_attention_gbs"] = nbytes / us / 1e3
+            out["verify_attention_frac_of_peak"] = nbytes / us / 1e3 / HBM_PEAK_GBS
+            out["verify_attention_sampled_rounds"] = len(att)
+        return out
+
+
+def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 8, "model"), (32, 8, "ngram")),
+                  prompt_len=1024, context=4096, temperature=0.8):
+    """Config 5: batched sampled speculative decoding on seeded 1024-token
+    prompts with ~30% planted repetition, each row decoded to a 4096-token
+    context.  Reports emitted tokens/s -- without the one-time HIP graph
+    captures of new shapes (new context buckets, the smaller batches left as
+    rows finish) and the sampled attention replays, and with them -- mean
+    accept length, and in-loop kernel times (LoopTimer)."""
+    from spec.draft import ModelDraft
+    from spec.loop import generate
+    from spec.ngram import NGramDraft
+    from specdec.workloads import planted_rows
+
+    results = {}
+    new_tokens = context - prompt_len
+    for batch, k, kind in combos:
+        prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
+        tc, dc = caches_for(target, draft if kind == "model" else None, batch, context, k)
+
+        def drafter():
+            return ModelDraft(draft, dc) if kind == "model" else NGramDraft(V)
+
+        # warm-up: the first context bucket's graphs at this batch
+        generate(target, tc, drafter(), prompts, 16, k=k, temperature=temperature,
+                 generator=torch.Generator().manual_seed(1))
+        with LoopTimer() as timer:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            outs, stats = generate(target, tc, drafter(), prompts, new_tokens, k=k, temperature=temperature,
+                                   generator=torch.Generator().manual_seed(5))
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        emitted = sum(len(o) for o in outs)
+        key = f"b{batch}_k{k}_{kind}"
+        results[key] = {"tokens_per_s": emitted / (dt - timer.excluded), "tokens_per_s_wall": emitted / dt,
+                        "excluded_s": timer.excluded, "seconds": dt, "emitted": emitted,
+                        "context": prompt_len + min(len(o) for o in outs),
+                        "mean_accept_len": mean_accept_len(stats), "acceptance": stats.accepted / max(stats.drafted, 1),
+                        "rounds": stats.rounds, **timer.summary(),
+                        "sample": f"{batch} rows, {prompt_len}-token prompts (~30% planted repetition) decoded to "
+                                  f"{context} tokens, T={temperature}, k={k}"}
+        log(f"batched {key}: {results[key]}")
+        del tc, dc
+        torch.cuda.empty_cache()
+    return results
+
+
+# ------------------------------------------------------------ CPU side ------
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return "unknown"
+
+
+def oracle_models(t_state, d_state):
+    import oracle.forward as of
+    from lm.model import SMOLLM2_135M, SMOLLM2_1_7B
 
     def cfg(s):
         return of.Config(s.vocab_size, s.hidden_size, s.num_hidden_layers, s.num_attention_heads,
                          s.num_key_value_heads, s.intermediate_size, s.head_dim, s.rms_norm_eps, s.rope_theta, True)
 
-    tm = of.Model(cfg(SMOLLM2_1_7B), {k: v.cpu() for k, v in t_state.items()})
-    dm = of.Model(cfg(SMOLLM2_135M), {k: v.cpu() for k, v in d_state.items()})
-    blocks = (PROMPT + new_tokens + 2 * K + 2 * BLOCK) // BLOCK + 4
-    t0 = time.perf_counter()
-    out, stats = generate(tm, okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16),
-                          ModelDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16)),
-                          [prompt], new_tokens, K, generator=torch.Generator().manual_seed(0))
-    dt = time.perf_counter() - t0
-    return {"value": len(out[0]) / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle loop (gather+SDPA forward, CPU accept-reject), 256-token prompt, "
-                      f"{new_tokens} new tokens, bf16, torch threads={threads}",
-            "seconds": dt, "tokens": out[0]}
+    return (of.Model(cfg(SMOLLM2_1_7B), {k: v.cpu() for k, v in t_state.items()}),
+            of.Model(cfg(SMOLLM2_135M), {k: v.cpu() for k, v in d_state.items()}))
+
+
+class _Turns:
+    """Strict alternation of two loops' rounds (one thread each): a loop
+    hands the turn over at the end of every round (its accept-reject call)
+    and waits for it back.  Each side's round time runs from getting the turn
+    to its next hand-over, so the other side's rounds are never counted."""
+
+    def __init__(self, sides=("gpu", "cpu")):
+        self.cv = threading.Condition()
+        self.turn = sides[0]
+        self.other = {sides[0]: sides[1], sides[1]: sides[0]}
+        self.done = set()
+        self.resumed = {s: None for s in sides}
+        self.rounds = {s: [] for s in sides}
+
+    def start(self, side):
+        with self.cv:
+            self.cv.wait_for(lambda: self.turn == side or self.other[side] in self.done, timeout=600)
+            self.resumed[side] = time.perf_counter()
+
+    def hand_over(self, side):
+        now = time.perf_counter()
+        with self.cv:
+            self.rounds[side].append(now - self.resumed[side])
+            if self.other[side] not in self.done:
+                self.turn = self.other[side]
+                self.cv.notify_all()
+                self.cv.wait_for(lambda: self.turn == side or self.other[side] in self.done, timeout=600)
+            self.resumed[side] = time.perf_counter()
+
+    def finish(self, side):
+        with self.cv:
+            self.done.add(side)
+            self.turn = self.other[side]
+            self.cv.notify_all()
+
+
+def cpu_e2e_interleaved(target, draft, t_state, d_state, prompt, warmup_rounds=3, rounds=20):
+    """The oracle loop (bf16, host cores) and the GPU loop on the same request,
+    their rounds alternating one for one.  The CPU request is a bounded sample
+    (prompt + warmup_rounds + rounds + 1 tokens: one token per round at this
+    draft's acceptance); the GPU request is the headline's.  Per side: p50 and
+    p99 of the measured rounds and emitted tokens/s over them."""
+    import oracle.kv as okv
+    import oracle.loop as ol
+    import spec.loop as loop
+    from oracle.draft import ModelDraft as OModelDraft
+    from spec.draft import ModelDraft
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    tm, dm = oracle_models(t_state, d_state)
+    cpu_tokens = warmup_rounds + rounds + 1
+    blocks = (PROMPT + NEW_TOKENS + 2 * K + 2 * BLOCK) // BLOCK + 4
+    turns = _Turns()
+    emitted = {"gpu": [], "cpu": []}
+    real = {"gpu": loop.accept_reject, "cpu": ol.accept_reject}
+
+    def hooked(side):
+        def accept(p, q, draft_ids, generator=None, **kw):
+            v = real[side](p, q, draft_ids, generator=generator, **kw)
+            emitted[side].append(int(v.n_accepted.sum()) + len(v.n_accepted))
+            turns.hand_over(side)
+            return v
+        return accept
+
+    results, errors = {}, []
+
+    def cpu_side():
+        try:
+            turns.start("cpu")
+            t0 = time.perf_counter()
+            out, stats = ol.generate(tm, okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16),
+                                     OModelDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16)),
+                                     [prompt], cpu_tokens, K, generator=torch.Generator().manual_seed(0))
+            results["cpu"] = (out[0], stats, time.perf_counter() - t0)
+        except BaseException as e:  # surfaced in the main thread
+            errors.append(e)
+        finally:
+            turns.finish("cpu")
+
+    loop.accept_reject, ol.accept_reject = hooked("gpu"), hooked("cpu")
+    worker = threading.Thread(target=cpu_side, daemon=True)
+    try:
+        tc, dc = caches_for(target, draft)
+        turns.start("gpu")
+        worker.start()
+        out, stats = loop.generate(target, tc, ModelDraft(draft, dc), [prompt], NEW_TOKENS, k=K,
+                                   generator=torch.Generator().manual_seed(0))
+        turns.finish("gpu")
+        worker.join(timeout=900)
+    finally:
+        loop.accept_reject, ol.accept_reject = real["gpu"], real["cpu"]
+    if errors:
+        raise errors[0]
+    cpu_out, cpu_stats, cpu_seconds = results["cpu"]
+    summary = {}
+    for side in ("gpu", "cpu"):
+        measured = turns.rounds[side][warmup_rounds:warmup_rounds + rounds]
+        toks = emitted[side][warmup_rounds:warmup_rounds + rounds]
+        summary[side] = {"rounds": len(measured), "round_ms_p50": 1000 * pct(measured, 50),
+                         "round_ms_p99": 1000 * pct(measured, 99), "tokens_per_s": sum(toks) / sum(measured)}
+    first_div = next((i for i, (a, b) in enumerate(zip(cpu_out, out[0])) if a != b), None)
+    return summary, {"cpu_request_seconds": cpu_seconds, "cpu_tokens": len(cpu_out), "threads": threads,
+                     "bf16_first_divergence_from_gpu": first_div}
 
 
 def cpu_attention_baseline(length=4096, batch=1, seconds=3.0):
@@ -523,6 +832,48 @@ def cpu_kernel_baselines(seconds=1.0):
     return res
 
 
+def cpu_batched_baseline(tm, dm, batch=8, prompt_len=128, new_tokens=8, k=4, temperature=0.8):
+    """Config 5 on the host cores, bounded: the oracle loop at batch 8, k = 4,
+    T = 0.8, model drafter, on 128-token planted prompts for 8 new tokens."""
+    import oracle.kv as okv
+    import oracle.loop as ol
+    from oracle.draft import ModelDraft as OModelDraft
+    from specdec.workloads import planted_rows
+
+    prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
+    blocks = batch * ((prompt_len + new_tokens + 2 * k + 2 * BLOCK) // BLOCK + 2)
+    t0 = time.perf_counter()
+    outs, stats = ol.generate(tm, okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16),
+                              OModelDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16)),
+                              prompts, new_tokens, k, temperature=temperature,
+                              generator=torch.Generator().manual_seed(5))
+    dt = time.perf_counter() - t0
+    return {"tokens_per_s": sum(len(o) for o in outs) / dt, "seconds": dt, "rounds": stats.rounds,
+            "mean_accept_len": mean_accept_len(stats),
+            "sample": f"{batch} rows, {prompt_len}-token planted prompts, {new_tokens} new tokens, T={temperature}, "
+                      f"k={k}, model drafter, bf16"}
+
+
+def kernel_speedups(kernels, ck, attn8, attn1, cpu_attn1, cpu_attn8):
+    """Host-oracle time over GPU time for each kernel timed on both sides."""
+    pairs = {"attention_b1_L4096": (cpu_attn1["us"], attn1["us"]), "attention_b8_L4096": (cpu_attn8["us"], attn8["us"])}
+    for b, k in ((1, 4), (8, 4)):
+        g = kernels.get(f"accept_b{b}_k{k}")
+        if g:
+            pairs[f"softmax_b{b}_k{k}"] = (ck[f"softmax_b{b}_k{k}_us"], g["softmax_us"])
+            pairs[f"accept_b{b}_k{k}"] = (ck[f"accept_b{b}_k{k}_us"], g["accept_us"])
+    for length in (2048, 4096, 8192):
+        g = kernels.get(f"ngram_b16_L{length}")
+        if g:
+            pairs[f"ngram_b16_L{length}"] = (ck[f"ngram_b16_L{length}_us"], g["us"])
+    if "append_b1_t5" in kernels:
+        pairs["append_b1_t5"] = (ck["append_b1_t5_us"], kernels["append_b1_t5"]["us"])
+    if "rollback_grow_b8" in kernels:
+        pairs["rollback_grow_b8_host_round_trip"] = (ck["rollback_grow_b8_us"],
+                                                     kernels["rollback_grow_b8"]["host_round_trip_us"])
+    return {name: c / g for name, (c, g) in pairs.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -534,6 +885,7 @@ def main():
     ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--batch", type=int, default=8, help="batch of the --only attention run")
     ap.add_argument("--one-pool", action="store_true", help="--only attention: re-read one layer pool")
+    ap.add_argument("--context", type=int, default=4096, help="--only batched: context the rows decode to")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (the path is built and "
@@ -566,35 +918,44 @@ def main():
         return
     if args.only == "batched":
         target, draft, _, _ = build_models()
-        print(json.dumps({"batched_sampled": bench_batched(target, draft)}))
+        print(json.dumps({"batched_sampled": bench_batched(target, draft, context=args.context)}))
         return
 
     e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
     log(f"e2e {e2e}")
+    e2e["truncated_drafts"] = bench_truncated_drafts(target, t_state, prompt)
+    e2e["copy_draft"] = bench_copy_draft(target, prompt, gpu_tokens)
+    log(f"copy draft {e2e['copy_draft']}")
     attn = time_attention(8, 4096, iters=120)
     log(f"attention b8 {attn}")
     attn1 = time_attention(1, 4096, iters=300)
     log(f"attention b1 {attn1}")
     attn1_pool = time_attention(1, 4096, iters=300, rotate=False)
     log(f"attention b1 one pool {attn1_pool}")
-    kernels = {} if args.only == "e2e" else bench_kernels()
-    variant_b = bench_variant_b(target, t_state, prompt)
-    log(f"variant B {variant_b}")
+    kernels = bench_kernels()
     batched = {} if args.no_batched else bench_batched(target, draft)
     cpu = None
     if not args.no_cpu:
+        log("cpu baseline (rounds interleaved with the GPU loop)")
+        rounds, extra = cpu_e2e_interleaved(target, draft, t_state, d_state, prompt)
+        log(f"cpu rounds {rounds} {extra}")
         del target, draft
         torch.cuda.empty_cache()
-        log("cpu baseline")
-        cpu = cpu_baseline(t_state, d_state, prompt)
-        cpu_tokens = cpu.pop("tokens")
-        # bf16 GEMMs round differently on the host and the GPU, so the two bf16
-        # token streams may part; the fp32 identity against the oracle is a test
-        cpu["bf16_first_divergence_from_gpu"] = next(
-            (i for i, (x, y) in enumerate(zip(cpu_tokens, gpu_tokens)) if x != y), None)
-        cpu["attention_b1_L4096"] = cpu_attention_baseline()
-        cpu["attention_b8_L4096"] = cpu_attention_baseline(batch=8)
-        cpu["kernels"] = cpu_kernel_baselines()
+        tm, dm = oracle_models(t_state, d_state)
+        ck = cpu_kernel_baselines()
+        log("cpu kernels done")
+        cpu_attn1, cpu_attn8 = cpu_attention_baseline(), cpu_attention_baseline(batch=8)
+        cpu = {"value": rounds["cpu"]["tokens_per_s"], "unit": "tokens/s", "cores": extra["threads"], "kind": "port",
+               "cpu_model": cpu_model(),
+               "sample": f"oracle loop (gather+SDPA forward, host accept-reject), bf16, 256-token prompt, "
+                         f"{extra['cpu_tokens']} new tokens; rounds interleaved one for one with the GPU loop's, "
+                         f"3 warm-up rounds excluded, 20 measured; torch threads={extra['threads']}",
+               "rounds": rounds, **extra,
+               "steady_state_speedup": rounds["gpu"]["tokens_per_s"] / rounds["cpu"]["tokens_per_s"],
+               "attention_b1_L4096": cpu_attn1, "attention_b8_L4096": cpu_attn8, "kernels": ck,
+               "batched_b8_k4_model": cpu_batched_baseline(tm, dm)}
+        cpu["kernel_speedups"] = kernel_speedups(kernels, ck, attn, attn1, cpu_attn1, cpu_attn8)
+        cpu["speedup"] = e2e["tokens_per_s"] / cpu["value"]
     line = {
         "metric": "spec-decode accepted tokens/s, 1.7B/135M k=4 b=1; verify-attn HBM GB/s",
         "value": e2e["tokens_per_s"],
@@ -619,37 +980,12 @@ def main():
                      "us_per_launch": attn["us"], "bytes_per_launch": attn["bytes"]},
         "cpu_baseline": cpu,
         "e2e": e2e,
-        "e2e_variant_b": variant_b,
         "attention_b1_ctx4096": attn1,
         "attention_b1_ctx4096_one_pool": attn1_pool,
         "batched_sampled": batched,
         "kernels": kernels,
     }
-    if cpu:
-        line["cpu_baseline"]["speedup"] = e2e["tokens_per_s"] / cpu["value"]
-        line["cpu_baseline"]["kernel_speedups"] = kernel_speedups(kernels, cpu, attn, attn1)
     print(json.dumps(line))
-
-
-def kernel_speedups(kernels, cpu, attn8, attn1):
-    """Host-oracle time over GPU time for each kernel timed on both sides."""
-    ck = cpu.get("kernels", {})
-    pairs = {"attention_b1_L4096": (cpu["attention_b1_L4096"]["us"], attn1["us"]),
-             "attention_b8_L4096": (cpu["attention_b8_L4096"]["us"], attn8["us"])}
-    for b, k in ((1, 4), (8, 4)):
-        g = kernels.get(f"accept_b{b}_k{k}")
-        if g:
-            pairs[f"softmax_b{b}_k{k}"] = (ck[f"softmax_b{b}_k{k}_us"], g["softmax_us"])
-            pairs[f"accept_b{b}_k{k}"] = (ck[f"accept_b{b}_k{k}_us"], g["accept_us"])
-    for length in (2048, 4096, 8192):
-        g = kernels.get(f"ngram_b16_L{length}")
-        if g:
-            pairs[f"ngram_b16_L{length}"] = (ck[f"ngram_b16_L{length}_us"], g["us"])
-    if "append_b1_t5" in kernels:
-        pairs["append_b1_t5"] = (ck["append_b1_t5_us"], kernels["append_b1_t5"]["us"])
-    if "rollback_grow_b8" in kernels:
-        pairs["rollback_grow_b8"] = (ck["rollback_grow_b8_us"], kernels["rollback_grow_b8"]["us_host_inclusive"])
-    return {name: c / g for name, (c, g) in pairs.items()}
 
 
 if __name__ == "__main__":

@@ -133,8 +133,8 @@ class DraftStepGraph(_Captured):
     """One draft step over right-padded [B, width] ids: forward of each row's
     last real token, probabilities, and an inverse-CDF sample with u[B]."""
 
-    def __init__(self, llama, cache, batch, width, temperature, bucket):
-        super().__init__(llama, cache, batch, bucket, width, latency=True)
+    def __init__(self, llama, cache, batch, width, temperature, bucket, latency=True):
+        super().__init__(llama, cache, batch, bucket, width, latency=latency)
         dev = cache.device
         self.temperature = temperature
         self.ids = torch.zeros(batch, width, dtype=torch.int64, device=dev)
@@ -163,8 +163,8 @@ class DraftChainGraph(_Captured):
     """`steps` consecutive one-token draft steps, each sampled token feeding
     the next step on the device.  Outputs q [B, steps, V] and tokens [B, steps]."""
 
-    def __init__(self, llama, cache, batch, steps, temperature, bucket):
-        super().__init__(llama, cache, batch, bucket, 1, latency=True)
+    def __init__(self, llama, cache, batch, steps, temperature, bucket, latency=True):
+        super().__init__(llama, cache, batch, bucket, 1, latency=latency)
         dev = cache.device
         self.temperature, self.steps = temperature, steps
         v = llama.config.vocab_size

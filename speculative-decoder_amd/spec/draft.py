@@ -44,9 +44,18 @@ def sample(probs: torch.Tensor, generator: torch.Generator) -> torch.Tensor:
 
 
 class ModelDraft:
-    def __init__(self, model, cache: KVCache) -> None:
+    """k sequential draft forwards per round (spec/draft.py:32-62).  By
+    default the draft computes for latency: single-row projections as
+    matrix-vector products and an attention split chosen for speed, whose
+    bits need not match the target's verify.  With exact=True it computes as
+    the verify and plain decoding do (same GEMMs, the fixed split), so a
+    draft that is the target itself proposes exactly the target's greedy
+    tokens."""
+
+    def __init__(self, model, cache: KVCache, exact: bool = False) -> None:
         self.model = model
         self.cache = cache
+        self.exact = exact
 
     def prefill(self, seq_ids: list[int], prompts: list[list[int]]) -> None:
         for seq_id in seq_ids:
@@ -63,7 +72,7 @@ class ModelDraft:
             return self._propose_graphs(seq_ids, pending, k, temperature, generator)
         tokens, qs = [], []
         for _ in range(k):
-            q = probabilities(run(self.model, self.cache, seq_ids, pending, latency_split=True), temperature)
+            q = probabilities(run(self.model, self.cache, seq_ids, pending, latency_split=not self.exact), temperature)
             token = sample(q, generator)
             tokens.append(token)
             qs.append(q)
@@ -88,11 +97,12 @@ class ModelDraft:
         u = torch.stack([torch.rand(b, generator=generator, dtype=torch.float32, device=dev) for _ in range(k)])
         u = u.to(cache.device, non_blocking=True)
         ids = torch.tensor([p + [0] * (width - len(p)) for p in pending], dtype=torch.int64)
-        first = graphs.get(cache, graphs.DraftStepGraph, llama, b, width, float(temperature), bucket)
+        latency = not self.exact
+        first = graphs.get(cache, graphs.DraftStepGraph, llama, b, width, float(temperature), bucket, latency)
         q0, t0 = first.run(ids, metas[0], u[0])
         if k == 1:
             return t0.clone().view(b, 1), q0.clone().view(b, 1, -1)
-        chain = graphs.get(cache, graphs.DraftChainGraph, llama, b, k - 1, float(temperature), bucket)
+        chain = graphs.get(cache, graphs.DraftChainGraph, llama, b, k - 1, float(temperature), bucket, latency)
         qs, toks = chain.run(t0, metas[1:], u[1:])
         return torch.cat([t0.view(b, 1), toks], dim=1), torch.cat([q0.view(b, 1, -1), qs], dim=1)
 

@@ -91,3 +91,18 @@ def test_bf16_spec_equals_plain_with_norm_weights():
         out, _ = generate(target, tc, ModelDraft(draft, dc), [p], 40, k=4)
         plain = cached_autoregressive.generate(target, KVCache.for_model(ts, 64, 16, torch.bfloat16, "cuda"), p, 40)
         assert out[0] == plain
+
+
+def test_bf16_exact_copy_draft_accepts_every_token():
+    """The target as its own draft, computing as the verify does: every
+    round accepts all k drafts and emits the bonus token (k + 1 tokens), and
+    the output is plain greedy decoding's (reference tests/test_greedy_identity.py:58-61)."""
+    ts, _ = shapes()
+    target = Llama.random(ts, 0, "cuda", torch.bfloat16)
+    p = prompts(1, 96)[0]
+    tc, dc = caches(ts, ts, torch.bfloat16)
+    out, stats = generate(target, tc, ModelDraft(target, dc, exact=True), [p], 41, k=4)
+    plain = cached_autoregressive.generate(target, KVCache.for_model(ts, 64, 16, torch.bfloat16, "cuda"), p, 41)
+    assert out[0] == plain
+    assert stats.accepted == stats.drafted == 4 * stats.rounds
+    assert stats.emitted_per_round == [5] * 8 and stats.rounds == 8
