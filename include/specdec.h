@@ -53,7 +53,7 @@ extern "C" {
 #define SPECDEC_BF16 2
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 7). */
+ * below changes (currently 8). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -69,6 +69,12 @@ int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t v
                           int64_t out_stride, int64_t *index_out, int64_t index_stride,
                           void *stream);
 
+/* Bytes of the workspace specdec_accept_reject uses for `batch` rows
+ * (chunk sums and barrier counters).  It must be zeroed once before its
+ * first use (and again after a call reports flag 2, below); calls leave it
+ * zeroed for the next. */
+int specdec_accept_workspace(int64_t batch, int64_t *bytes);
+
 /* Fused accept-reject for a batch: gather p(x), q(x) of the drafted tokens,
  * test u*q(x) < p(x), count the leading accepts n, build the residual
  * norm(max(0, p[n] - q[n])) (q[k] is the implicit zero row, so n == k is the
@@ -78,6 +84,11 @@ int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t v
  * of the same dtype as p.  out int64 [3, batch]: n_accepted, next_token, and
  * a flag that is 1 when a drafted token had q(x) <= 0 or an id outside
  * [0, vocab).
+ * With a workspace (fp32, and batch * chunks within one workgroup per
+ * compute unit) each row is spread over many workgroups of one launch that
+ * meet at two barriers; the flag is 2 if a barrier timed out (the workspace
+ * must then be zeroed again; next_token is not valid).  Calls sharing a
+ * workspace must be ordered.  Without one, one workgroup runs each row.
  * Replaces spec/accept.py:44-79 `accept_reject` with the default residual
  * (spec/accept.py:18-26) and spec/accept.py:29-35 `sample_inverse_cdf`. */
 int specdec_accept_reject(const void *p, const void *q, int dtype,
@@ -85,7 +96,8 @@ int specdec_accept_reject(const void *p, const void *q, int dtype,
                           int64_t q_batch_stride, int64_t q_row_stride,
                           const int64_t *draft, const void *u_accept,
                           const void *u_residual, int64_t batch, int64_t k,
-                          int64_t vocab, int64_t *out, void *stream);
+                          int64_t vocab, int64_t *out, void *workspace,
+                          int64_t workspace_bytes, void *stream);
 
 /* First stage of accept-reject alone (for a caller-supplied residual):
  * out int64 [2, batch]: n_accepted and a flag that is 1 when a drafted token

@@ -96,6 +96,7 @@ def accept_reject(
     ur = _cuda(u_residual.to(p.dtype)).contiguous()
     if residual is residual_distribution:
         out = ops.accept_reject(p, q, draft_d, ua, ur).cpu()
+        ops.check_accept_flags(out[2], p.device)
         if bool(out[2].any()):
             raise ValueError(_BAD_DRAFT)
         return Verdict(out[0].clone(), out[1].clone())

@@ -599,6 +599,254 @@ __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_kernel(
   if (threadIdx.x == 0) out[b] = idx;
 }
 
+// ----------------------------------------- accept-reject over many CUs ----
+// fp32 accept-reject with each batch row spread over G workgroups of 256
+// threads -- chunk g of the row, E consecutive elements per thread -- in
+// one launch whose workgroups meet twice per row:
+//   0. each workgroup finds the accept count n itself with scalar loads (the
+//      drafted ids, then p(x) and q(x)) and loads its chunk of p[n] and q[n]
+//      (q[k] is the zero row: the bonus samples p[k]);
+//   1. it publishes the fp64 sum of its chunk of the residual
+//      r = max(0, p[n] - q[n]);
+//   2. once every chunk sum of its row is published, each adds them in chunk
+//      order (the residual total, rounded to fp32), divides its elements by
+//      it (or takes p's row when the total is 0) and publishes L_g, the fp64
+//      inclusive prefix sum of its chunk at the chunk's last element;
+//   3. once every L_g is published, each forms C_j = L_0 + ... + L_{j-1} in
+//      chunk order and the target u * fp32(C_G); the one workgroup whose
+//      chunk holds the first prefix above the target -- fp32(C_g) <= target
+//      < fp32(C_{g+1}) -- counts its prefixes that do not exceed it.
+// An element's prefix is C_g + its chunk-local inclusive prefix (fp64, the
+// thread's run after a fixed-order workgroup scan), so a chunk's last
+// prefix is C_{g+1} exactly and the chunk test agrees with the count.
+// Accumulation in fp64 with a rounding per prefix is the CPU cumsum's rule;
+// only the order of the fp64 additions differs from a sequential sum.
+//
+// Meetings: a value is published with a device-scope atomic store, encoded
+// as the complement of the fp64 bits, so that it is never 0; a reader polls
+// the slots it needs until none reads 0 (bounded: a timeout flags the row
+// with 2 in out[2B + b]).  Slots go back to 0 without a counter: a
+// workgroup clears its L slot first thing (the clear is acknowledged before
+// its first publish, so no reader can pass the first meeting and still see
+// the last call's L), and clears its chunk-sum slot once every L is
+// published (every reader of the chunk sums has then finished with them).
+// The workspace needs zeroing once, not per call.  The grid never exceeds
+// one workgroup per compute unit, so every workgroup of a row is resident
+// together.  At B = 1 and 8 twelve chunks of 16 elements per thread
+// measured fastest (8.7 us against 9.7 with 24 chunks, 10.9 with 48, and
+// 13.1 for a variant loading every candidate row before n was known).
+constexpr int kMwThreads = 256;
+constexpr int kMwMaxG = 64;     // chunks per row
+constexpr int kMwSpin = 1 << 20;
+// per-row workspace, in uint64 words: chunk sums [G], then L [G]
+constexpr int64_t kMwL = kMwMaxG;
+constexpr int64_t kMwRowWords = 2 * kMwMaxG;
+constexpr int kMwUnroll = 8;  // drafted positions whose scalar loads go out together
+
+// the E elements of one thread from a row buffer (zeros past the row)
+template <int E, bool VEC4>
+__device__ __forceinline__ void load_elems(__amdgpu_buffer_rsrc_t rb, unsigned first, float (&v)[E]) {
+  if constexpr (VEC4) {
+#pragma unroll
+    for (int j = 0; j < E / 4; ++j) {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rb, (first + 4u * j) * 4u, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * j + e] = __builtin_bit_cast(float, (unsigned)w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, (first + e) * 4u, 0, 0));
+  }
+}
+
+__device__ __forceinline__ void publish(uint64_t *slot, uint64_t encoded) {
+  __hip_atomic_store(slot, encoded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t enc64(double v) { return ~__builtin_bit_cast(uint64_t, v); }
+__device__ __forceinline__ double dec64(uint64_t w) { return __builtin_bit_cast(double, ~w); }
+
+// Poll slots[0..n) (this workgroup's threads share them) until each is
+// published; their raw words land in dst.  False on timeout.
+__device__ bool await_slots(uint64_t *slots, int n, uint64_t *dst) {
+  __shared__ int s_late;
+  if (threadIdx.x == 0) s_late = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    uint64_t w = 0;
+    for (int spin = 0; spin < kMwSpin; ++spin) {
+      w = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (w != 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (w == 0) s_late = 1;
+    dst[i] = w;
+  }
+  __syncthreads();
+  return s_late == 0;
+}
+
+// Sequential fp64 sum of the decoded words w[0..n) (n >= 1), in index
+// order, with the reads issued 16 at a time so their latencies overlap;
+// also the running sum before and after element j (when 0 <= j < n).
+struct Chain {
+  double total, before, after;
+};
+__device__ __forceinline__ Chain chain_sum(const uint64_t *w, int n, int j) {
+  Chain r{0.0, 0.0, 0.0};
+  double acc = 0.0;
+  for (int i0 = 0; i0 < n; i0 += 16) {
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = dec64(w[min(i0 + i, n - 1)]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double next = i0 + i < n ? acc + v[i] : acc;
+      if (i0 + i == j) r.before = acc, r.after = next;
+      acc = next;
+    }
+  }
+  r.total = acc;
+  return r;
+}
+
+template <int E, bool VEC4>
+__global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(
+    const float *__restrict__ p, const float *__restrict__ q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
+    int64_t q_rs, const int64_t *__restrict__ draft, const float *__restrict__ u_accept,
+    const float *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab, int G,
+    int64_t *__restrict__ out, uint64_t *__restrict__ ws) {
+  __shared__ double scratch[kMwThreads / kWave + 1];
+  __shared__ uint64_t s_words[kMwMaxG];
+  __shared__ double s_last;
+  const int64_t b = blockIdx.x / G;
+  const int g = (int)(blockIdx.x % G);
+  const int tid = threadIdx.x;
+  constexpr int kChunk = kMwThreads * E;
+  const unsigned first = (unsigned)g * kChunk + (unsigned)tid * E;  // this thread's first element
+  uint64_t *row_ws = ws + b * kMwRowWords;
+  const float *p_b = p + b * p_bs;
+  const float *q_b = q + b * q_bs;
+  auto flag_late = [&]() {
+    if (tid == 0) __hip_atomic_store(reinterpret_cast<uint64_t *>(out + 2 * batch + b), 2ull, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+  };
+  // the last call's L of this chunk goes back to 0 before anything is published
+  if (tid == 0) publish(row_ws + kMwL + g, 0);
+  const float ur = u_residual[b];
+  __asm__ volatile("" ::"s"(ur));  // loaded now, not after a meeting
+
+  // 0. the accept count n and the bad-draft flag, the same in every thread
+  // (accept_stage's test, u * q(x) < p(x) as a product; an id outside the
+  // vocabulary is never read through)
+  int64_t n = k, bad = 0;
+  for (int64_t t0 = 0; t0 < k; t0 += kMwUnroll) {
+    int64_t xs[kMwUnroll];
+    float pxs[kMwUnroll], qxs[kMwUnroll], us[kMwUnroll];
+#pragma unroll
+    for (int j = 0; j < kMwUnroll; ++j) {
+      xs[j] = -1;
+      if (t0 + j < k) xs[j] = draft[b * k + t0 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < kMwUnroll; ++j) {
+      const int64_t t = t0 + j, x = xs[j];
+      pxs[j] = qxs[j] = us[j] = 0.0f;
+      if (t < k) us[j] = u_accept[b * k + t];
+      if (t < k && x >= 0 && x < vocab) {
+        pxs[j] = p_b[t * p_rs + x];
+        qxs[j] = q_b[t * q_rs + x];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kMwUnroll; ++j) {
+      const int64_t t = t0 + j, x = xs[j];
+      if (t >= k) break;
+      if (x < 0 || x >= vocab) {
+        bad = 1;
+        if (n == k) n = t;
+        continue;
+      }
+      if (!(qxs[j] > 0.0f)) bad = 1;
+      if (n == k && !(us[j] * qxs[j] < pxs[j])) n = t;
+    }
+  }
+  if (g == 0 && tid == 0) {
+    out[b] = n;
+    out[2 * batch + b] = bad;
+  }
+  float pr[E], qr[E];  // this thread's elements of p[n] and q[n]
+  load_elems<E, VEC4>(row_buffer(p_b + n * p_rs, (unsigned)vocab), first, pr);
+  if (n < k) load_elems<E, VEC4>(row_buffer(q_b + n * q_rs, (unsigned)vocab), first, qr);
+  else
+#pragma unroll
+    for (int e = 0; e < E; ++e) qr[e] = 0.0f;
+
+  // 1. the chunk's residual sum
+  float x[E];
+  double run = 0.0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float r = pr[e] - qr[e];
+    x[e] = r > 0.0f ? r : 0.0f;
+    run += (double)x[e];
+  }
+  const double chunk_sum = block_sum(run, scratch);
+  if (tid == 0) {
+    __builtin_amdgcn_s_waitcnt(0);  // the L clear is acknowledged before any publish
+    publish(row_ws + g, enc64(chunk_sum));
+  }
+  if (!await_slots(row_ws, G, s_words)) {
+    flag_late();
+    return;
+  }
+
+  // 2. the total in chunk order, the quotients, L_g
+  const float total = (float)chain_sum(s_words, G, -1).total;
+  const float denom = total > FLT_MIN ? total : FLT_MIN;
+  const bool use_residual = total > 0.0f;
+  run = 0.0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x[e] = use_residual ? x[e] / denom : pr[e];  // p == q: p itself
+    run += (double)x[e];
+  }
+  double unused;
+  const double excl = block_exclusive_scan(run, scratch, &unused);
+  if (tid == kMwThreads - 1) {
+    double acc = excl;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc += (double)x[e];
+    s_last = acc;
+  }
+  __syncthreads();
+  if (tid == 0) publish(row_ws + kMwL + g, enc64(s_last));
+  if (!await_slots(row_ws + kMwL, G, s_words)) {
+    flag_late();
+    return;
+  }
+  // every reader of the chunk sums is past them: clear this chunk's
+  if (tid == 0) publish(row_ws + g, 0);
+
+  // 3. chunk bases, the target, the count in the chunk that holds it
+  const Chain chain = chain_sum(s_words, G, g);
+  const double c_lo = chain.before, c_hi = chain.after, c = chain.total;
+  const float target = ur * (float)c;
+  if ((float)c_lo <= target && target < (float)c_hi) {
+    int cnt_le = 0;
+    double acc = excl;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      acc += (double)x[e];
+      if ((float)(c_lo + acc) <= target) ++cnt_le;
+    }
+    const int64_t idx = (int64_t)g * kChunk + (int64_t)block_sum((double)cnt_le, scratch);
+    if (tid == 0) out[batch + b] = idx < vocab - 1 ? idx : vocab - 1;
+  } else if (g == G - 1 && !(target < (float)c)) {
+    if (tid == 0) out[batch + b] = vocab - 1;  // no prefix exceeds the target
+  }
+}
+
 __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64_t vocab,
                                float *__restrict__ out) {
   const int64_t total = n * vocab;
@@ -613,7 +861,7 @@ __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64
 
 using namespace specdec;
 
-SPECDEC_API int specdec_abi_version(void) { return 7; }
+SPECDEC_API int specdec_abi_version(void) { return 8; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,
@@ -658,18 +906,78 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
   return launch_status();
 }
 
+// Grid of the many-CU accept-reject: E elements per thread, preferring 16
+// (12 chunks of a 49152 vocabulary, the fastest measured), then the next E
+// whose G chunks per row keep the grid within one workgroup per compute
+// unit; false when none fits (then one workgroup runs each row).
+struct MwPlan {
+  int E = 0, G = 0;
+};
+
+static bool plan_mw(int64_t batch, int64_t vocab, MwPlan &pl) {
+  const int cus = cu_count();
+  if (cus <= 0) return false;
+  for (int E : {16, 24, 32, 48}) {
+    const int64_t G = (vocab + (int64_t)kMwThreads * E - 1) / ((int64_t)kMwThreads * E);
+    if (G > kMwMaxG || batch * G > cus) continue;
+    pl.E = E;
+    pl.G = (int)G;
+    return true;
+  }
+  return false;
+}
+
+template <int E>
+static void launch_mw_e(bool vec4, int64_t batch, int G, hipStream_t s, const float *p, const float *q, int64_t p_bs,
+                        int64_t p_rs, int64_t q_bs, int64_t q_rs, const int64_t *draft, const float *ua,
+                        const float *ur, int64_t k, int64_t vocab, int64_t *out, uint64_t *ws) {
+  dim3 grid((unsigned)(batch * G)), block(kMwThreads);
+  if (vec4)
+    accept_reject_mw_kernel<E, true><<<grid, block, 0, s>>>(p, q, p_bs, p_rs, q_bs, q_rs, draft, ua, ur, batch, k,
+                                                             vocab, G, out, ws);
+  else
+    accept_reject_mw_kernel<E, false><<<grid, block, 0, s>>>(p, q, p_bs, p_rs, q_bs, q_rs, draft, ua, ur, batch, k,
+                                                              vocab, G, out, ws);
+}
+
+SPECDEC_API int specdec_accept_workspace(int64_t batch, int64_t *bytes) {
+  if (batch < 0 || !bytes) return SPECDEC_EINVAL;
+  *bytes = batch * kMwRowWords * (int64_t)sizeof(uint64_t);
+  return SPECDEC_OK;
+}
+
 SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
                                       int64_t p_batch_stride, int64_t p_row_stride,
                                       int64_t q_batch_stride, int64_t q_row_stride,
                                       const int64_t *draft, const void *u_accept,
                                       const void *u_residual, int64_t batch, int64_t k,
-                                      int64_t vocab, int64_t *out, void *stream) {
+                                      int64_t vocab, int64_t *out, void *workspace,
+                                      int64_t workspace_bytes, void *stream) {
   if (batch < 0 || k < 0 || vocab <= 0) return SPECDEC_EINVAL;
   if (vocab > (int64_t)kMaxTiles * kCdfPerThread * kAcceptThreads) return SPECDEC_EUNSUPPORTED;
   if (batch == 0) return SPECDEC_OK;
   if (!p || !out || !u_residual || (k > 0 && (!q || !draft || !u_accept))) return SPECDEC_EINVAL;
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
+  MwPlan pl;
+  if (workspace && dtype == SPECDEC_F32 && plan_mw(batch, vocab, pl)) {
+    if (workspace_bytes < batch * kMwRowWords * (int64_t)sizeof(uint64_t) || ((uintptr_t)workspace & 7) != 0)
+      return SPECDEC_EINVAL;
+    const bool vec4 = vocab % 4 == 0 && p_batch_stride % 4 == 0 && p_row_stride % 4 == 0 &&
+                      (k == 0 || (q_batch_stride % 4 == 0 && q_row_stride % 4 == 0 && ((uintptr_t)q & 15) == 0)) &&
+                      ((uintptr_t)p & 15) == 0;
+    const float *fp = (const float *)p, *fq = (const float *)q;
+    const float *ua = (const float *)u_accept, *ur = (const float *)u_residual;
+    uint64_t *ws = (uint64_t *)workspace;
+    const int64_t pb = p_batch_stride, pr = p_row_stride, qb = q_batch_stride, qr = q_row_stride;
+    switch (pl.E) {
+      case 16: launch_mw_e<16>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
+      case 24: launch_mw_e<24>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
+      case 32: launch_mw_e<32>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
+      default: launch_mw_e<48>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
+    }
+    return launch_status();
+  }
   if (dtype == SPECDEC_F32 && vocab <= (int64_t)kRegTiles * kCdfPerThread * kAcceptThreads) {
     if (vocab % 4 == 0)
       accept_reject_regs_kernel<true><<<grid, block, 0, s>>>((const float *)p, (const float *)q, p_batch_stride,

@@ -1117,20 +1117,6 @@ SPECDEC_API int specdec_attention_workspace(int32_t batch, int32_t width, int32_
   return SPECDEC_OK;
 }
 
-// Compute units of the current device (0 if it cannot be read), looked up
-// once per device.
-static int cu_count() {
-  static int counts[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (counts[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    counts[dev] = n;
-  }
-  return counts[dev];
-}
-
 // Grid of one call: the split, the kernel family and how many split
 // partials per unit the workspace must hold.
 struct AttnPlan {

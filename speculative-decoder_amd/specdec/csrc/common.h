@@ -21,6 +21,20 @@ inline int launch_status() {
   return e == hipSuccess ? SPECDEC_OK : SPECDEC_EHIP;
 }
 
+// Compute units of the current device (0 if it cannot be read), looked up
+// once per device.
+inline int cu_count() {
+  static int counts[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
+
 // ---- element conversion -------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(double x) { return static_cast<float>(x); }

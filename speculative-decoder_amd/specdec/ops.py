@@ -119,18 +119,73 @@ def _accept_inputs(p, q, draft, u_accept) -> tuple[int, int]:
     return b, k
 
 
-def accept_reject(p, q, draft, u_accept, u_residual) -> torch.Tensor:
+class AcceptWorkspace:
+    """Zero-initialised, grow-only workspace of the many-CU accept-reject
+    (chunk sums and barrier counters; every call leaves it zeroed).  Calls
+    sharing one must be ordered on one stream."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.buf = torch.zeros(0, dtype=torch.uint8, device=device)
+
+    def reserve(self, batch: int) -> torch.Tensor:
+        import ctypes
+
+        nbytes = ctypes.c_int64()
+        _check(lib().specdec_accept_workspace(batch, ctypes.byref(nbytes)), "accept_workspace")
+        if nbytes.value > self.buf.numel():
+            self.buf = torch.zeros(max(nbytes.value, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+    def reset(self) -> None:
+        self.buf.zero_()
+
+
+_accept_workspaces: dict[torch.device, AcceptWorkspace] = {}
+
+
+def accept_workspace_for(device: torch.device) -> AcceptWorkspace:
+    ws = _accept_workspaces.get(device)
+    if ws is None:
+        ws = _accept_workspaces[device] = AcceptWorkspace(device)
+    return ws
+
+
+# out[2] flag bit: a barrier of the many-CU accept kernel timed out
+ACCEPT_TIMEOUT = 2
+
+
+def accept_reject(p, q, draft, u_accept, u_residual, workspace: AcceptWorkspace | None = None,
+                  single: bool = False) -> torch.Tensor:
     """Fused accept + residual + inverse CDF; returns int64 [3, B] on the GPU:
-    n_accepted, next_token, zero-q flag."""
+    n_accepted, next_token, and a flag (1: a drafted token with zero q(x) or
+    outside the vocabulary; 2: a barrier of the many-CU kernel timed out --
+    see check_accept_flags).  `single` asks for the one-workgroup-per-row
+    kernel (no workspace)."""
     p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
     b, k = _accept_inputs(p, q, draft, u_accept)
     _on(p.device, u_residual, "u_residual", p.dtype, True, b)
     out = torch.empty(3, b, dtype=torch.int64, device=p.device)
+    ws_ptr, ws_bytes = None, 0
+    if not single:
+        buf = (workspace or accept_workspace_for(p.device)).reserve(b)
+        ws_ptr, ws_bytes = buf.data_ptr(), buf.numel()
     st = lib().specdec_accept_reject(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
                                      q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(),
-                                     u_residual.data_ptr(), b, k, p.shape[-1], out.data_ptr(), stream())
+                                     u_residual.data_ptr(), b, k, p.shape[-1], out.data_ptr(), ws_ptr, ws_bytes,
+                                     stream())
     _check(st, "accept_reject")
     return out
+
+
+def check_accept_flags(flags: torch.Tensor, device: torch.device, workspace: AcceptWorkspace | None = None) -> None:
+    """Raise for the flags of an accept_reject call read back to the host: a
+    timed-out barrier (the workspace is zeroed again first) is a
+    RuntimeError; a bad draft is the reference's ValueError."""
+    if bool((flags & ACCEPT_TIMEOUT).any()):
+        (workspace or accept_workspace_for(device)).reset()
+        raise KernelError("accept_reject: a barrier of the many-CU kernel timed out (the workgroups of a row were "
+                          "not resident together); the workspace was reset")
 
 
 def accept_count(p, q, draft, u_accept) -> torch.Tensor:
