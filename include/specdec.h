@@ -53,7 +53,7 @@ extern "C" {
 #define SPECDEC_BF16 2
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 8). */
+ * below changes (currently 9). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -308,6 +308,43 @@ int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
                                  int32_t max_kv_len, int32_t split_tokens,
                                  float *workspace, int64_t workspace_floats, void *out,
                                  int64_t out_token_stride, void *stream);
+
+/* ------------------------------------------------------------------ head --- */
+
+/* Output head: logits [rows, vocab] fp32 (logits_stride apart) = x [rows,
+ * hidden] bf16 (x_stride apart) times w [vocab, hidden] bf16 (w_stride
+ * apart) transposed, bf16 products accumulated in fp32 on MFMA in a fixed
+ * k order, so a row's logits do not depend on the other rows of the call or
+ * their number.  hidden % 32 == 0, hidden <= 2048 and w within 2 GiB, else
+ * SPECDEC_EUNSUPPORTED; x and w 16-byte aligned with strides % 8 == 0.
+ * Replaces lm/forward.py:71-84 (the fp32 output projection). */
+int specdec_head_logits(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                        int64_t rows, int64_t hidden, int64_t vocab, float *logits,
+                        int64_t logits_stride, void *stream);
+
+/* Bytes of the workspace of specdec_head_probabilities: zeroed once by the
+ * caller, then never cleared (its words carry a per-call tag). */
+int specdec_head_workspace(int64_t *bytes);
+
+/* The output head and probabilities in one launch, for at most 16 rows:
+ * out [rows, vocab] fp32 (out_stride apart) = one-hot of each row's argmax
+ * (lowest id among ties) at temperature 0, else softmax(logits /
+ * temperature), with the logits of specdec_head_logits (same bits, also
+ * written to `logits` when non-NULL).  At temperature 0 a non-NULL
+ * index_out receives each row's argmax.  The workgroups exchange per-slice
+ * statistics through `workspace` (specdec_head_workspace bytes, zeroed
+ * before its first call; calls sharing it must be ordered on one stream);
+ * a workgroup that has polled `spin` times without seeing every slice
+ * computes the missing statistics itself, with the same bits.  Shapes the
+ * launch does not take (more than 16 rows, a vocab needing more than one
+ * workgroup of 16 tiles per compute unit) return SPECDEC_EUNSUPPORTED.
+ * Replaces lm/forward.py:71-84 followed by lm/sampling.py:13-18. */
+int specdec_head_probabilities(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                               int64_t rows, int64_t hidden, int64_t vocab, float temperature,
+                               float *out, int64_t out_stride, int64_t *index_out,
+                               int64_t index_stride, float *logits, int64_t logits_stride,
+                               void *workspace, int64_t workspace_bytes, int32_t spin,
+                               void *stream);
 
 /* fp32 split partials the library holds per GPU for
  * specdec_paged_attention_static (8 MiB). */

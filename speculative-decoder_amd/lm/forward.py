@@ -63,7 +63,8 @@ def _project_add(hidden: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemv: b
 
 def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Tensor, max_kv_len: int,
                  last: torch.Tensor | None = None, workspace: ops.AttentionWorkspace | None = None,
-                 split_tokens: int = 0) -> torch.Tensor:
+                 split_tokens: int = 0, temperature: float | None = None, out: torch.Tensor | None = None,
+                 index_out: torch.Tensor | None = None) -> torch.Tensor:
     """Device-only forward of ids [B, T] whose rows were appended with `meta`
     (int32 [3, B] on the device).  `max_kv_len` bounds every row's cached
     length after the append; `last` (int64 [B]) selects one row per batch
@@ -71,7 +72,9 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     split (0: the fixed default whose results do not depend on the other
     queries of the call; nonzero marks a latency call -- the draft -- whose
     bits need not match other calls, which also lets single-row projections
-    run as matrix-vector products)."""
+    run as matrix-vector products).  With a `temperature` the result is the
+    probabilities of the logits instead (`out`, `index_out` as in
+    `probabilities`)."""
     cfg = llama.config
     gemv = split_tokens != 0
     b, t = ids.shape
@@ -103,12 +106,14 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
             ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.unit_norm, x, eps)
     if last is not None:
         x = x[torch.arange(b, device=x.device), last]
-    return logits(llama, x)
+    if temperature is None:
+        return logits(llama, x)
+    return probabilities(llama, x, temperature, out, index_out)
 
 
 @torch.no_grad()
 def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, n_new: list[int],
-            last_only: bool = False, latency_split: bool = False) -> torch.Tensor:
+            last_only: bool = False, latency_split: bool = False, temperature: float | None = None) -> torch.Tensor:
     """Run `input_ids` [B, T] (right-padded; row b has n_new[b] real tokens)
     through the model, appending to each sequence's cache.  Returns logits
     [B, T, V]; rows past n_new[b] are padding.  With `last_only`, only each
@@ -116,7 +121,9 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
 
     The same call serves prefill (T = prompt length), decode (T = 1) and
     speculative verification (T = k + 1).  `latency_split` lets attention
-    pick a split for latency (the draft) instead of the fixed default."""
+    pick a split for latency (the draft) instead of the fixed default.  With
+    a `temperature` the probabilities of those logits are returned instead
+    (the head and the softmax in one launch where it applies)."""
     llama = as_llama(model, cache.device)
     step = cache.append(seq_ids, n_new)
     ids = input_ids.to(cache.device, non_blocking=True)
@@ -128,7 +135,8 @@ def forward(model, cache: KVCache, seq_ids: list[int], input_ids: torch.Tensor, 
     cfg = llama.config
     split = (ops.latency_split(ids.shape[0], ids.shape[1], cfg.num_attention_heads, cfg.num_key_value_heads,
                                step.max_total) if latency_split else 0)
-    return forward_core(llama, cache, step.meta, ids, step.max_total, last, split_tokens=split)
+    return forward_core(llama, cache, step.meta, ids, step.max_total, last, split_tokens=split,
+                        temperature=temperature)
 
 
 def logits(model, hidden: torch.Tensor) -> torch.Tensor:
@@ -136,12 +144,29 @@ def logits(model, hidden: torch.Tensor) -> torch.Tensor:
     near-tied candidates round to the same logit and argmax would break the
     tie by whichever rounding a (k+1)-token verify and a 1-token decode
     produced.  The reference multiplies by an fp32 copy of the head
-    (lm/forward.py:71-84); bf16 weights are read here as stored, half the
-    bytes, and since the product of two bf16 values is exact in fp32 the
-    arithmetic is the fp32 head's up to the GEMM's summation order."""
+    (lm/forward.py:71-84); a bf16 head is read here as stored, half the
+    bytes, by the head kernel: bf16 products are exact in fp32, and the
+    kernel accumulates them in one fixed order for every row, so a row's
+    logits have the same bits whatever other rows share the call."""
     llama = as_llama(model)
     w = llama.head_wide
+    if w.dtype == torch.bfloat16 and w.shape[1] % 32 == 0 and w.shape[1] <= 2048:
+        return ops.head_logits(hidden.to(w.dtype), w)
     if w.dtype not in (torch.bfloat16, torch.float16):
         return F.linear(hidden.to(w.dtype), w)
     flat = hidden.reshape(-1, hidden.shape[-1]).to(w.dtype)
     return torch.mm(flat, w.t(), out_dtype=torch.float32).view(*hidden.shape[:-1], w.shape[0])
+
+
+def probabilities(model, hidden: torch.Tensor, temperature: float, out: torch.Tensor | None = None,
+                  index_out: torch.Tensor | None = None) -> torch.Tensor:
+    """lm/sampling.py:13-18 applied to `logits(model, hidden)`: the head and
+    the softmax / argmax in one launch for a bf16 head where that is the
+    faster way (a few rows; the same logits bits, so the same argmax), else
+    the logits and then the softmax kernel."""
+    llama = as_llama(model)
+    w = llama.head_wide
+    rows = hidden.numel() // hidden.shape[-1]
+    if hidden.dtype == torch.bfloat16 and ops.head_fused(w, rows, fastest=True):
+        return ops.head_probabilities(hidden, w, temperature, out=out, index_out=index_out)
+    return ops.probabilities(logits(llama, hidden), temperature, out=out, index_out=index_out)

@@ -1,9 +1,10 @@
 """HIP-graph replay of the fixed-shape forwards of the round loop.
 
 A speculative round runs the same few shapes again and again: the verify
-pass (B rows of k+1 tokens, then the softmax / one-hot kernel) and the k
-draft steps (B rows of 1 token, then softmax and the inverse-CDF sampler,
-each step's token feeding the next step).  Each is captured once per
+pass (B rows of k+1 tokens, ending in the output head fused with the
+softmax / one-hot) and the k draft steps (B rows of 1 token, ending in the
+same fused head, then the inverse-CDF sampler at T > 0, each step's token
+feeding the next step).  Each is captured once per
 (cache, batch, width, temperature, context bucket) and replayed; block
 allocation and the per-step metadata stay on the host side of the replay
 (one block-plan launch and one small copy per round), because they decide
@@ -76,6 +77,7 @@ class _Captured:
         self.llama, self.batch, self.bucket = llama, batch, bucket
         dev = cache.device
         self.ws = ops.AttentionWorkspace(dev)
+        ops.head_workspace(dev)  # allocated (and zeroed) once, outside any capture
         cfg = llama.config
         self.split = (ops.latency_split(batch, width, cfg.num_attention_heads, cfg.num_key_value_heads, bucket)
                       if latency else 0)
@@ -123,8 +125,8 @@ class VerifyGraph(_Captured):
             self.meta.copy_(meta, non_blocking=True)
 
         def work():
-            lg = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, None, self.ws)
-            return ops.probabilities(lg, self.temperature)
+            return forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, None, self.ws,
+                                temperature=self.temperature)
 
         return self.replay(prepare, work)
 
@@ -150,10 +152,12 @@ class DraftStepGraph(_Captured):
 
         def work():
             last = self.meta[2].long() - 1
-            lg = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split)
             if self.temperature == 0.0:  # the one-hot row's inverse-CDF draw is its argmax
-                return ops.probabilities(lg, 0.0, index_out=self.token), self.token
-            q = ops.probabilities(lg, self.temperature)
+                q = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split,
+                                 temperature=0.0, index_out=self.token)
+                return q, self.token
+            q = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split,
+                             temperature=self.temperature)
             return q, ops.sample_inverse_cdf(q, self.u)
 
         return self.replay(prepare, work)
@@ -183,14 +187,14 @@ class DraftChainGraph(_Captured):
         def work():
             ids = self.first
             for i in range(self.steps):
-                lg = forward_core(self.llama, self.cache, self.metas[i], ids, self.bucket, None, self.ws,
-                                  self.split)
                 if self.temperature == 0.0:
                     # the inverse-CDF draw from a one-hot row is its argmax for
-                    # every u, so the softmax kernel writes the token itself
-                    ops.probabilities(lg.view(self.batch, -1), 0.0, out=self.q[:, i], index_out=self.tokens[:, i])
+                    # every u, so the head writes the token itself
+                    forward_core(self.llama, self.cache, self.metas[i], ids, self.bucket, None, self.ws, self.split,
+                                 temperature=0.0, out=self.q[:, i], index_out=self.tokens[:, i])
                 else:
-                    ops.probabilities(lg.view(self.batch, -1), self.temperature, out=self.q[:, i])
+                    forward_core(self.llama, self.cache, self.metas[i], ids, self.bucket, None, self.ws, self.split,
+                                 temperature=self.temperature, out=self.q[:, i])
                     self.tokens[:, i].copy_(ops.sample_inverse_cdf(self.q[:, i], self.u[i]))
                 ids = self.tokens[:, i:i + 1]
             return self.q, self.tokens

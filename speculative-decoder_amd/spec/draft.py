@@ -1,7 +1,8 @@
 """Drafters (reference: spec/draft.py).
 
 ModelDraft keeps the whole k-step draft loop on the GPU: each step's
-probabilities come from the softmax kernel, its token from the inverse-CDF
+probabilities come from the output head fused with the softmax (the token
+itself from the same launch at temperature 0), its token from the inverse-CDF
 kernel with a uniform drawn from the caller's generator (the reference's
 stream and order, spec/draft.py:27-29), and the sampled ids feed the next
 step's forward directly, with no host round trip between steps.
@@ -16,7 +17,6 @@ from cache.kv import KVCache
 from lm import graphs
 from lm.forward import forward
 from lm.model import as_llama
-from lm.sampling import probabilities
 from spec.accept import sample_inverse_cdf
 
 
@@ -72,7 +72,7 @@ class ModelDraft:
             return self._propose_graphs(seq_ids, pending, k, temperature, generator)
         tokens, qs = [], []
         for _ in range(k):
-            q = probabilities(run(self.model, self.cache, seq_ids, pending, latency_split=not self.exact), temperature)
+            q = run(self.model, self.cache, seq_ids, pending, latency_split=not self.exact, temperature=temperature)
             token = sample(q, generator)
             tokens.append(token)
             qs.append(q)
@@ -138,14 +138,16 @@ class UniformDraft:
 
 
 def run(model, cache: KVCache, seq_ids: list[int], chunks: list[list[int]] | torch.Tensor,
-        latency_split: bool = False) -> torch.Tensor:
+        latency_split: bool = False, temperature: float | None = None) -> torch.Tensor:
     """Forward right-padded chunks; returns the logits after each row's last
-    real token, [B, V].  `chunks` may also be a [B, w] id tensor already on
-    the device (every row w tokens long)."""
+    real token, [B, V] (their probabilities at `temperature`, when given).
+    `chunks` may also be a [B, w] id tensor already on the device (every row
+    w tokens long)."""
     if isinstance(chunks, torch.Tensor):
         return forward(model, cache, seq_ids, chunks, [chunks.shape[1]] * chunks.shape[0], last_only=True,
-                       latency_split=latency_split)
+                       latency_split=latency_split, temperature=temperature)
     n_new = [len(c) for c in chunks]
     width = max(n_new)
     input_ids = torch.tensor([c + [0] * (width - len(c)) for c in chunks], dtype=torch.int64)
-    return forward(model, cache, seq_ids, input_ids, n_new, last_only=True, latency_split=latency_split)
+    return forward(model, cache, seq_ids, input_ids, n_new, last_only=True, latency_split=latency_split,
+                   temperature=temperature)

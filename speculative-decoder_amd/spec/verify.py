@@ -7,7 +7,6 @@ from cache.kv import KVCache
 from lm import graphs
 from lm.forward import forward
 from lm.model import as_llama
-from lm.sampling import probabilities
 
 
 def verify(target, cache: KVCache, seq_ids: list[int], contexts: list[list[int]], draft: torch.Tensor,
@@ -26,7 +25,7 @@ def verify(target, cache: KVCache, seq_ids: list[int], contexts: list[list[int]]
     input_ids = torch.cat([last, draft.to(cache.device, torch.int64)], dim=1)
     b, k1 = input_ids.shape
     if not graphs.enabled():
-        return probabilities(forward(target, cache, seq_ids, input_ids, [k1] * b), temperature)
+        return forward(target, cache, seq_ids, input_ids, [k1] * b, temperature=temperature)
     llama = as_llama(target, cache.device)
     step = cache.append(seq_ids, [k1] * b)
     llama.ensure_positions(step.max_total)

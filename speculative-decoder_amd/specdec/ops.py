@@ -222,6 +222,122 @@ def one_hot(ids: torch.Tensor, vocab: int) -> torch.Tensor:
     return out.view(*ids.shape, vocab)
 
 
+# -------------------------------------------------------------------- head --
+# rows of one fused head call (hidden rows whose probabilities one launch
+# writes), at most
+HEAD_FUSED_ROWS = 16
+# polls of the fused head's meeting before a workgroup computes the missing
+# statistics itself (about 0.2 us each)
+HEAD_SPIN = 1 << 17
+_head_workspaces: dict[torch.device, torch.Tensor] = {}
+
+
+def head_workspace(device: torch.device) -> torch.Tensor:
+    """The fused head's meeting slots on `device`: allocated zeroed once, never
+    cleared or reallocated (graph captures keep its address).  Calls sharing
+    it must be ordered on one stream."""
+    ws = _head_workspaces.get(device)
+    if ws is None:
+        import ctypes
+
+        nbytes = ctypes.c_int64()
+        _check(lib().specdec_head_workspace(ctypes.byref(nbytes)), "head_workspace")
+        ws = _head_workspaces[device] = torch.zeros(nbytes.value, dtype=torch.uint8, device=device)
+    return ws
+
+
+def _head_operands(x: torch.Tensor, w: torch.Tensor) -> tuple[torch.Tensor, int]:
+    gpu(w, "w")
+    _on(w.device, x, "hidden", torch.bfloat16)
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("the head must be a contiguous bf16 [V, H] tensor")
+    h = w.shape[1]
+    if x.shape[-1] != h:
+        raise ValueError(f"hidden rows have {x.shape[-1]} features, the head {h}")
+    x2 = x.reshape(-1, h)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2, x2.shape[0]
+
+
+def _rows_out(out: torch.Tensor | None, rows: int, v: int, dev: torch.device, name: str) -> torch.Tensor:
+    """`out` as an fp32 [rows, V] view with unit inner stride (any row stride)."""
+    if out is None:
+        return torch.empty(rows, v, dtype=torch.float32, device=dev)
+    _on(dev, out, name, torch.float32)
+    o2 = out if out.dim() == 2 else out.view(rows, v)
+    if tuple(o2.shape) != (rows, v) or o2.stride(-1) != 1:
+        raise ValueError(f"{name} must be fp32 [rows, V] with unit inner stride")
+    return o2
+
+
+def head_logits(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., H] bf16 times the head w [V, H] bf16, accumulated in fp32:
+    fp32 logits [..., V].  A row's logits do not depend on the other rows
+    of the call."""
+    x2, rows = _head_operands(x, w)
+    v = w.shape[0]
+    o2 = _rows_out(out, rows, v, w.device, "out")
+    st = lib().specdec_head_logits(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.shape[1], rows, w.shape[1], v,
+                                   o2.data_ptr(), o2.stride(0), stream())
+    _check(st, "head_logits")
+    return o2.view(*x.shape[:-1], v) if out is None else out
+
+
+def head_probabilities(x: torch.Tensor, w: torch.Tensor, temperature: float, out: torch.Tensor | None = None,
+                       index_out: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
+                       spin: int = HEAD_SPIN) -> torch.Tensor:
+    """probabilities(head_logits(x, w), temperature) in one launch, at most
+    HEAD_FUSED_ROWS hidden rows: fp32 [..., V], the one-hot of each row's
+    argmax (lowest id among ties) at temperature 0, else softmax(logits / T).
+    `index_out` (int64, one per row) receives the argmax at temperature 0;
+    `logits_out` the logits, the bits head_logits gives."""
+    x2, rows = _head_operands(x, w)
+    if rows > HEAD_FUSED_ROWS:
+        raise ValueError(f"a fused head call takes at most {HEAD_FUSED_ROWS} rows (got {rows})")
+    v = w.shape[0]
+    fresh = out is None
+    o2 = _rows_out(out, rows, v, w.device, "out")
+    l2 = None if logits_out is None else _rows_out(logits_out, rows, v, w.device, "logits_out")
+    idx_ptr, idx_stride = None, 0
+    if index_out is not None:
+        if temperature != 0.0:
+            raise ValueError("index_out is defined at temperature 0 only")
+        _on(w.device, index_out, "index_out", torch.int64, numel=rows)
+        if index_out.dim() > 1 and not index_out.is_contiguous():
+            raise ValueError("index_out must be a vector or contiguous")
+        idx_ptr, idx_stride = index_out.data_ptr(), (index_out.stride(0) if index_out.dim() else 1)
+    ws = head_workspace(w.device)
+    st = lib().specdec_head_probabilities(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.shape[1], rows, w.shape[1], v,
+                                          float(temperature), o2.data_ptr(), o2.stride(0), idx_ptr, idx_stride,
+                                          ptr(l2), 0 if l2 is None else l2.stride(0), ws.data_ptr(), ws.numel(),
+                                          int(spin), stream())
+    _check(st, "head_probabilities")
+    return o2.view(*x.shape[:-1], v) if fresh else out
+
+
+def head_fused(w: torch.Tensor, rows: int, fastest: bool = False) -> bool:
+    """Whether head_probabilities takes `rows` hidden rows against head w on
+    this GPU (bf16, H a multiple of 32 up to 2048, the vocab spread over at
+    most one workgroup per compute unit with at most 16 tiles of 16 each).
+    With `fastest`, also whether one fused launch beats head_logits and the
+    softmax kernel on MI355X: its exchange of per-slice statistics grows
+    with the rows, so it pays up to 8 rows of a 2048-wide head (5 rows:
+    52.9 against 54.8 us) and for a single row of a narrower one (576 wide:
+    21.8 against 22.2 us; 5 rows: 23.5 against 21.9 us)."""
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not (1 <= rows <= HEAD_FUSED_ROWS):
+        return False
+    if fastest and rows > (8 if w.shape[1] >= 1024 else 1):
+        return False
+    v, h = w.shape
+    if h % 32 or h > 2048 or v * h * 2 > 2**31 - 1:
+        return False
+    cus = torch.cuda.get_device_properties(w.device).multi_processor_count
+    tiles = -(-v // 16)
+    tpw = max(1, -(-tiles // cus))
+    return tpw <= 16 and -(-tiles // tpw) <= min(cus, 256)
+
+
 # ------------------------------------------------------------------ n-gram --
 def ngram_lookup(history: torch.Tensor, lengths: torch.Tensor, k: int, max_n: int):
     """history int32 [B, cap], lengths int32 [B] -> (draft int64 [B, k], match int32 [B, 2])."""

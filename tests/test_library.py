@@ -42,3 +42,17 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.specdec_probabilities(None, 0, -1, 10, 10, 1.0, None, 10, None, 0, None) == 1
     assert lib.specdec_ngram_lookup(None, 0, None, 1, 4, 9, None, None, None) == 3  # max_n > 8
     assert lib.specdec_block_plan(None, 1, None, None, 4, 5, None, 1, 0, None, None) == 1  # top > num_blocks
+
+
+def test_head_entry_points_check_shapes_before_launch():
+    import ctypes
+
+    lib = _lib.load()
+    nbytes = ctypes.c_int64()
+    assert lib.specdec_head_workspace(ctypes.byref(nbytes)) == 0 and nbytes.value > 0
+    # hidden not a multiple of 32: unsupported; a negative row count: invalid
+    assert lib.specdec_head_logits(16, 48, 16, 48, 1, 48, 100, 16, 100, None) == 3
+    assert lib.specdec_head_logits(16, 64, 16, 64, -1, 64, 100, 16, 100, None) == 1
+    # more than 16 rows in one fused call
+    assert lib.specdec_head_probabilities(16, 64, 16, 64, 17, 64, 100, 1.0, 16, 100, None, 0, None, 0, 16,
+                                          nbytes.value, 0, None) == 3
