@@ -356,6 +356,47 @@ def time_fn(fn, iters=100, graph=False):
     return start.elapsed_time(end) * 1000 / iters
 
 
+def bench_head():
+    """The output head (49152 x 2048 target, 49152 x 576 draft, bf16) at 1 and
+    5 hidden rows: torch's mm with fp32 output, that plus the softmax kernel,
+    the head kernel alone, and the head fused with the softmax.  Launches
+    cycle over copies of the head so W is read from HBM."""
+    from specdec import ops
+
+    res = {}
+    for name, hidden, copies in (("target", 2048, 4), ("draft", 576, 12)):
+        g = torch.Generator(device="cuda").manual_seed(3)
+        heads = [(torch.randn(V, hidden, generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(copies)]
+        for rows in (1, 5):
+            x = torch.randn(rows, hidden, generator=g, device="cuda").to(torch.bfloat16)
+            out = torch.empty(rows, V, device="cuda")
+            lg = torch.empty(rows, V, device="cuda")
+            turn = [0]
+
+            def w():
+                turn[0] += 1
+                return heads[turn[0] % copies]
+
+            r = {"torch_mm_us": time_fn(lambda: torch.mm(x, w().t(), out_dtype=torch.float32, out=lg), graph=True),
+                 "torch_mm_softmax_us": time_fn(
+                     lambda: ops.probabilities(torch.mm(x, w().t(), out_dtype=torch.float32, out=lg), 1.0, out=out),
+                     graph=True),
+                 "head_logits_us": time_fn(lambda: ops.head_logits(x, w(), out=lg), graph=True),
+                 "head_logits_softmax_us": time_fn(
+                     lambda: ops.probabilities(ops.head_logits(x, w(), out=lg), 1.0, out=out), graph=True),
+                 "head_fused_us": time_fn(lambda: ops.head_probabilities(x, w(), 1.0, out=out), graph=True)}
+            nbytes = V * hidden * 2 + rows * hidden * 2 + rows * V * 4
+            r["bytes"] = nbytes
+            r["head_logits_gbs"] = nbytes / r["head_logits_us"] / 1e3
+            r["head_logits_frac_of_peak"] = r["head_logits_gbs"] / HBM_PEAK_GBS
+            r["head_fused_gbs"] = nbytes / r["head_fused_us"] / 1e3
+            r["head_fused_frac_of_peak"] = r["head_fused_gbs"] / HBM_PEAK_GBS
+            res[f"head_{name}_rows{rows}"] = r
+        del heads
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_kernels(attention_grid=True):
     from specdec import ops
     from specdec.workloads import planted_rows
@@ -409,6 +450,7 @@ def bench_kernels(attention_grid=True):
                            "frac_of_peak": app_bytes / us_app / 1e3 / HBM_PEAK_GBS}
     del cache
     res["rollback_grow_b8"] = bench_rollback()
+    res.update(bench_head())
     if not attention_grid:
         return res
     # attention over the config-2 grid
@@ -879,7 +921,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--only", choices=["all", "e2e", "batched", "attention", "kernels", "small", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "e2e", "batched", "attention", "kernels", "small", "copy", "head"],
+                    default="all",
                     help="small: the kernels of configs 1-3 without the attention grid (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
@@ -899,6 +942,9 @@ def main():
     if args.only == "attention":
         r = time_attention(args.batch, 4096, iters=max(args.steps, 1) * 100, rotate=not args.one_pool)
         print(json.dumps({f"attention_b{args.batch}_L4096": r}))
+        return
+    if args.only == "head":
+        print(json.dumps(bench_head()))
         return
     if args.only in ("kernels", "small"):
         print(json.dumps(bench_kernels(attention_grid=args.only == "kernels")))

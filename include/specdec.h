@@ -270,7 +270,10 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * inside one workgroup with the same arithmetic, and so are 5 to 12 splits
  * when the call has a (row, kv head) tile for every compute unit and at
  * most 8 query rows per kv head: the workspace is then not used); calls
- * sharing a workspace must be ordered.
+ * sharing a workspace must be ordered.  max_kv_len must bound every row's
+ * cached length after the call (past + n_new): the grid is sized from it,
+ * and a row beyond it gets NaN in its output rows (and, in the fused-append
+ * entry point, nothing appended) instead of a silent skip.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
  * cache/kv.py:108-112. */
 int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,

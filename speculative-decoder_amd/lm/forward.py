@@ -161,9 +161,9 @@ def logits(model, hidden: torch.Tensor) -> torch.Tensor:
 def probabilities(model, hidden: torch.Tensor, temperature: float, out: torch.Tensor | None = None,
                   index_out: torch.Tensor | None = None) -> torch.Tensor:
     """lm/sampling.py:13-18 applied to `logits(model, hidden)`: the head and
-    the softmax / argmax in one launch for a bf16 head where that is the
-    faster way (a few rows; the same logits bits, so the same argmax), else
-    the logits and then the softmax kernel."""
+    the softmax / argmax in one launch for a bf16 head and a few rows (where
+    it is no slower than the pair; the same logits bits, so the same
+    argmax), else the logits and then the softmax kernel."""
     llama = as_llama(model)
     w = llama.head_wide
     rows = hidden.numel() // hidden.shape[-1]

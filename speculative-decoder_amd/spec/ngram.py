@@ -25,7 +25,9 @@ class _History:
         self.buf = torch.zeros(rows, cap, dtype=torch.int32, device=device)
         self.row_of: dict[int, int] = {}
         self.length: dict[int, int] = {}
-        self.last: dict[int, int] = {}
+        # the tokens a row holds, and the context list they came from
+        self.tokens: dict[int, list[int]] = {}
+        self.source: dict[int, list[int]] = {}
         self._free = list(range(rows - 1, -1, -1))
 
     def _grow(self, rows: int, cap: int) -> None:
@@ -49,13 +51,16 @@ class _History:
         if r is not None:
             self._free.append(r)
             self.length.pop(seq_id, None)
-            self.last.pop(seq_id, None)
+            self.tokens.pop(seq_id, None)
+            self.source.pop(seq_id, None)
 
     def sync(self, seq_ids: list[int], contexts: list[list[int]]) -> torch.Tensor:
         """Bring each sequence's device row up to its context; returns the
-        int32 lengths [B] on the device.  A context that is not an extension
-        of what was uploaded (shorter, or a different last known token) is
-        uploaded whole."""
+        int32 lengths [B] on the device.  Only the tokens past the row's are
+        uploaded when the context extends them: the same list as last time
+        (the round loop appends to it in place) whose token at the row's end
+        is unchanged, or another list whose prefix equals the row's tokens
+        (compared once, on the host).  Anything else is uploaded whole."""
         need = max(len(c) for c in contexts)
         if need > self.buf.shape[1]:
             self._grow(self.buf.shape[0], max(need, 2 * self.buf.shape[1]))
@@ -65,14 +70,20 @@ class _History:
         for seq_id, ctx in zip(seq_ids, contexts):
             r = self.row(seq_id)
             have = self.length[seq_id]
-            if have > len(ctx) or (have > 0 and ctx[have - 1] != self.last.get(seq_id)):
-                have = 0
+            held = self.tokens.setdefault(seq_id, [])
+            if have > len(ctx):  # shorter: keep the rows' tokens if it is their prefix
+                have = len(ctx) if ctx == held[:len(ctx)] else 0
+            elif have > 0 and (ctx is not self.source.get(seq_id) or ctx[have - 1] != held[have - 1]):
+                if ctx[:have] != held[:have]:
+                    have = 0
+            del held[have:]
+            held.extend(ctx[have:])
             if have < len(ctx):
                 base = r * cap
                 flat_idx.extend(range(base + have, base + len(ctx)))
                 values.extend(ctx[have:])
             self.length[seq_id] = len(ctx)
-            self.last[seq_id] = ctx[-1]
+            self.source[seq_id] = ctx
         if values:
             host = torch.tensor([flat_idx, values], dtype=torch.int64).pin_memory()
             dev = host.to(self.device, non_blocking=True)

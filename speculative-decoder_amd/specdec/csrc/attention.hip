@@ -95,6 +95,7 @@ struct AttnArgs {
 
 struct TileInfo {
   int b, h, qt, group, row, past, nnew, nrows, kv_len, nsplit, unit;
+  bool overflow;  // the row's keys need more splits than max_kv_len allows
 };
 
 __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
@@ -113,12 +114,14 @@ __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool 
   ti.nnew = a.meta[2 * a.batch + ti.b];
   __asm__ volatile("" ::"s"(ti.row), "s"(ti.past), "s"(ti.nnew));
   ti.nrows = ti.nnew * ti.group;
+  ti.overflow = false;
   const int r0 = ti.qt * kRows;
   if (r0 >= ti.nrows) return false;
   const int t_hi = min(r0 + kRows - 1, ti.nrows - 1) / ti.group;
   ti.kv_len = ti.past + t_hi + 1;
   ti.nsplit = (ti.kv_len + a.split - 1) / a.split;
-  if (ti.nsplit > a.max_splits) return false;
+  ti.overflow = ti.nsplit > a.max_splits;
+  if (ti.overflow) return false;
   if (!any_split && (int)blockIdx.y >= ti.nsplit) return false;
   return true;
 }
@@ -193,6 +196,18 @@ __device__ __forceinline__ void store_row4(const AttnArgs &a, const TileInfo &ti
   T *dst = reinterpret_cast<T *>(a.out) + ((int64_t)ti.b * a.width + t) * a.out_stride + (int64_t)hq * kD + d0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(v[i]);
+}
+
+// A row whose cached length exceeds the call's max_kv_len (a caller broke
+// the contract): its tile's output rows are set to NaN by the tile's first
+// workgroup, so the error shows instead of stale output.
+template <typename T>
+__device__ void poison_tile(const AttnArgs &a, const TileInfo &ti) {
+  if (!ti.overflow || blockIdx.y != 0 || threadIdx.x >= 256) return;
+  const int qq = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 4;
+  if (ti.qt * kRows + qq >= ti.nrows) return;
+  const float nan4[4] = {NAN, NAN, NAN, NAN};
+  store_row4<T>(a, ti, qq, d0, nan4);
 }
 
 // Fold of the 4 waves of a 256-thread workgroup through LDS: thread
@@ -565,7 +580,10 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(PF ?
 attention_bf16_kernel(
     AttnArgs a) {
   TileInfo ti;
-  if (!tile_info(a, ti, /*any_split=*/NW == 16)) return;
+  if (!tile_info(a, ti, /*any_split=*/NW == 16)) {
+    poison_tile<__hip_bfloat16>(a, ti);
+    return;
+  }
   const bool flat = NW == 16 && a.flat;
   const int tid = threadIdx.x, lane = tid & 63, wave = flat ? (tid >> 6) : ((tid >> 6) & 3);
   int split_idx = (NW == 16) ? (flat ? 0 : (tid >> 8)) : (int)blockIdx.y;
@@ -957,7 +975,10 @@ attention_bf16_kernel(
 template <bool BS16>
 __global__ __launch_bounds__(kAttnThreads) void attention_f32_kernel(AttnArgs a) {
   TileInfo ti;
-  if (!tile_info(a, ti)) return;
+  if (!tile_info(a, ti)) {
+    poison_tile<float>(a, ti);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int r = ti.qt * kRows + c;

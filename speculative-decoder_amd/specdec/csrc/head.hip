@@ -23,10 +23,10 @@
 //   1. each finds its slice's statistics per hidden row from the logits it
 //      keeps in LDS -- the slice maximum of l/T and the sum of
 //      2^((l/T - max) log2 e) (T > 0), or the slice's maximum and its lowest
-//      index (T = 0) -- and publishes them as tagged 64-bit words into a
-//      region of every workgroup, so that each workgroup reads only its own
-//      region and no two poll the same memory lines;
-//   2. it reads its region until every slice's words are there, folds them
+//      index (T = 0) -- and publishes them as tagged 64-bit words into
+//      each of 16 copies of the slot region (a workgroup polls one copy, so
+//      few poll the same memory lines);
+//   2. it reads its copy until every slice's words are there, folds them
 //      in slice order with a fixed lane pattern (so every workgroup gets the
 //      same bits), and writes its slice of p from the logits still in LDS:
 //      2^((l/T - M) log2 e) * (1 / S), or the one-hot row;
@@ -60,13 +60,16 @@ constexpr int kHXPad = 8;                   // bf16 padding per staged hidden ro
 constexpr int kHXElems = kHT * (2048 + kHXPad);  // staged hidden elements (bf16)
 constexpr int kHMaxGrid = 256;              // workgroups of a fused call, at most
 constexpr int kHFusedRows = 16;             // hidden rows of a fused call, at most
-// workspace words: two arrival counters, the call epoch, then one region
-// per reading workgroup holding every slice's words, [slice][row][2]
-// packed by the call's row count (so a reader's words are contiguous and
-// no two workgroups poll the same lines)
+// workspace words: two arrival counters, the call epoch, then kHCopies
+// regions, each holding every slice's words, [slice][row][2] packed by the
+// call's row count.  Workgroup j reads region j % kHCopies: a writer stores
+// its words kHCopies times, and a line is polled by grid / kHCopies readers
+// (256 readers of one copy queued for the same lines; a copy per reader
+// multiplied the stores by 256)
+constexpr int kHCopies = 16;
 constexpr int64_t kHWsHead = 3;
 constexpr int64_t kHWsRegion = (int64_t)kHMaxGrid * kHFusedRows * 2;
-constexpr int64_t kHWsWords = kHWsHead + kHMaxGrid * kHWsRegion;
+constexpr int64_t kHWsWords = kHWsHead + kHCopies * kHWsRegion;
 constexpr int kHLoadsInFlight = 8;  // region words a thread reads per round
 
 enum HeadMode { kLogits = 0, kSoftmax = 1, kArgmax = 2 };
@@ -372,7 +375,7 @@ __global__ __launch_bounds__(1024) void head_softmax_kernel(HeadArgs a) {
   // per thread per pass; a word seen with the call's tag is kept (s_ex) and
   // not read again.  The first pass is issued before this workgroup
   // publishes, so waiting for it does not wait for the publishing stores.
-  const uint64_t *mine = regions + (int64_t)j0 * kHWsRegion;
+  const uint64_t *mine = regions + (int64_t)(j0 % kHCopies) * kHWsRegion;
   const int nwords = grid * nw2;
   const int per_pass = kHLoadsInFlight * (int)blockDim.x;
   uint64_t w[kHLoadsInFlight];
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(1024) void head_softmax_kernel(HeadArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   // 3. publish: this slice's words into every reader's region (8-byte
   // stores, contiguous per region)
-  for (int u = tid; u < grid * nw2; u += blockDim.x) {
+  for (int u = tid; u < kHCopies * nw2; u += blockDim.x) {
     const int reader = u / nw2, re = u - reader * nw2;
     const uint64_t word = ((uint64_t)tag << 32) | s_own[re >> 1][re & 1];
     __hip_atomic_store(regions + reader * kHWsRegion + (int64_t)j0 * nw2 + re, word, __ATOMIC_RELAXED,

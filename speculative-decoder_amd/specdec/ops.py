@@ -320,14 +320,16 @@ def head_fused(w: torch.Tensor, rows: int, fastest: bool = False) -> bool:
     """Whether head_probabilities takes `rows` hidden rows against head w on
     this GPU (bf16, H a multiple of 32 up to 2048, the vocab spread over at
     most one workgroup per compute unit with at most 16 tiles of 16 each).
-    With `fastest`, also whether one fused launch beats head_logits and the
-    softmax kernel on MI355X: its exchange of per-slice statistics grows
-    with the rows, so it pays up to 8 rows of a 2048-wide head (5 rows:
-    52.9 against 54.8 us) and for a single row of a narrower one (576 wide:
-    21.8 against 22.2 us; 5 rows: 23.5 against 21.9 us)."""
+    With `fastest`, also whether the one fused launch is at least as fast as
+    head_logits followed by the softmax kernel on MI355X (kernel traces of
+    graph replays, W from HBM): up to 5 rows of a 2048-wide head (52.9 against
+    53.1 us at 5 rows, 51.9 against 51.9 at 1) and a single row of a narrower
+    one (576 wide: 22.3 against 22.2 us at 1 row, 22.8 against 22.0 at 5).
+    Its exchange of per-slice statistics grows with the rows; the pair does
+    not."""
     if w.dtype != torch.bfloat16 or w.dim() != 2 or not (1 <= rows <= HEAD_FUSED_ROWS):
         return False
-    if fastest and rows > (8 if w.shape[1] >= 1024 else 1):
+    if fastest and rows > (5 if w.shape[1] >= 1024 else 1):
         return False
     v, h = w.shape
     if h % 32 or h > 2048 or v * h * 2 > 2**31 - 1:

@@ -564,3 +564,38 @@ def test_bf16_prefill_matches_oracle(width, heads, past):
     for b in range(batch):
         err = (got[b, :, : n_new[b]] - want[b, :, : n_new[b]]).abs()
         assert err.max().item() < 2e-2 and err.mean().item() < 2e-3, (b, err.max().item(), err.mean().item())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("max_kv_len", [1030, 2600])
+def test_rows_beyond_max_kv_len_get_nan(dtype, max_kv_len):
+    """A caller passing a max_kv_len below a row's cached length breaks the
+    contract: that row's output is NaN (not left stale), the other rows are
+    exact.  1030 keys: the one-workgroup grid; 2600: split partials and the
+    combine launch."""
+    d, h, hkv, bs, t_new = 64, 8, 8, 16, 5
+    lengths = [100, 4000]
+    g = torch.Generator().manual_seed(9)
+    cache = make_cache(1, hkv, d, sum(L // bs + 2 for L in lengths) + 8, bs, dtype, 9)
+    for s in (0, 1):
+        cache.add(s)
+    step = cache.append([0, 1], lengths)
+    kh = torch.randn(2, hkv, max(lengths), d, generator=g).to(dtype)
+    vh = torch.randn(2, hkv, max(lengths), d, generator=g).to(dtype)
+    cache.write(0, step, kh.cuda(), vh.cuda())
+    step = cache.append([0, 1], [t_new, t_new])
+    kn = torch.randn(2, hkv, t_new, d, generator=g).to(dtype)
+    vn = torch.randn(2, hkv, t_new, d, generator=g).to(dtype)
+    cache.write(0, step, kn.cuda(), vn.cuda())
+    q = torch.randn(2, t_new, h * d, generator=g).to(dtype).cuda()
+    out = torch.zeros(2, t_new, h * d, dtype=dtype, device="cuda")
+    ops.paged_attention(q, q.stride(1), cache.k[0], cache.v[0], cache.table_tensor, step.meta, 2, t_new, h, hkv, d,
+                        bs, d ** -0.5, max_kv_len, out, out.stride(1))
+    got = out.float().cpu()
+    assert bool(torch.isnan(got[1]).all())
+    k0 = torch.cat([kh[0, :, :100], kn[0]], dim=1).float()[None]
+    v0 = torch.cat([vh[0, :, :100], vn[0]], dim=1).float()[None]
+    want = of.attention(q[:1].view(1, t_new, h, d).transpose(1, 2).float().cpu(), k0, v0, torch.tensor([100]),
+                        torch.tensor([105]), d ** -0.5)
+    tol = 2e-2 if dtype == torch.bfloat16 else 2e-5
+    assert (got[0].view(t_new, h, d).transpose(0, 1) - want[0]).abs().max().item() < tol

@@ -73,6 +73,34 @@ def test_drafter_incremental_history_matches_full_lookup():
     assert draft.cpu().tolist() == [on.lookup(rows[1][:50], 4, 3)]
 
 
+def test_reused_sequence_id_with_another_context_is_uploaded_again():
+    """A sequence id reused for a different context of the same length and
+    last token (the reference's NGramDraft keeps no state, so its proposal
+    depends on the context alone): the history is re-uploaded, not reused."""
+    a = [5, 6, 7, 1, 2, 3, 9, 1, 2, 3]
+    b = [8, 8, 8, 1, 2, 4, 6, 1, 2, 3]  # same length and last tokens, other content
+    drafter = NGramDraft(16)
+    for ctx in (a, b, list(a), a[:7], b + [6]):
+        draft, _ = drafter.propose([0], [ctx], 4, 0.0, None)
+        assert draft.cpu().tolist() == [on.lookup(ctx, 4, 3)], ctx
+
+
+@pytest.mark.parametrize("max_n", [9, 17, 64, 65, 100, 1000])
+def test_any_max_n_matches_oracle(max_n):
+    """max_n past the staged tail (64 tokens) and tile overlap: periodic rows
+    agree over long spans (agreements that run out of the staged tokens read
+    memory), random small-vocab rows over short ones; one row crosses the
+    8192-position tile boundary."""
+    g = torch.Generator().manual_seed(max_n)
+    rows = [[i % 5 for i in range(300)], [i % 7 for i in range(8300)], [(i * 3) % 11 for i in range(150)]]
+    rows += [torch.randint(0, 3, (int(n),), generator=g).tolist() for n in torch.randint(2, 120, (8,), generator=g)]
+    for k in (1, 4):
+        got, match = lookup_batch(rows, k, max_n)
+        for row, gt, m in zip(rows, got, match):
+            want, start, n = on.lookup_match(row, k, max_n)
+            assert gt == want and tuple(m) == (start, n), (len(row), k, max_n)
+
+
 def test_empty_context_raises():
     with pytest.raises(IndexError):
         lookup([], 3, 3)

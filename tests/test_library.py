@@ -40,7 +40,7 @@ def test_invalid_arguments_are_rejected_before_launch():
     lib = _lib.load()
     # negative sizes and null pointers return SPECDEC_EINVAL without touching a device
     assert lib.specdec_probabilities(None, 0, -1, 10, 10, 1.0, None, 10, None, 0, None) == 1
-    assert lib.specdec_ngram_lookup(None, 0, None, 1, 4, 9, None, None, None) == 3  # max_n > 8
+    assert lib.specdec_ngram_lookup(None, 0, None, 1, 4, 9, None, None, None) == 1  # null pointers
     assert lib.specdec_block_plan(None, 1, None, None, 4, 5, None, 1, 0, None, None) == 1  # top > num_blocks
 
 
