@@ -397,6 +397,41 @@ def bench_head():
     return res
 
 
+def bench_prefill_attention():
+    """Prompt-sized attention (B=1, 32/32 heads x 64, bf16, block 16, an empty
+    cache): RoPE + append + causal attention of T = 256 and 1024 new tokens
+    through the paged cache, against torch's scaled_dot_product_attention
+    on contiguous q/k/v of the same shape (no RoPE, no paging) for scale.
+    Flops are the causal triangle's QK^T and PV: 2 * 2 * H * d * T(T+1)/2."""
+    from cache.kv import KVCache
+    from lm.model import SMOLLM2_1_7B, rope_tables
+    from specdec import ops
+
+    cos, sin = (t.cuda() for t in rope_tables(SMOLLM2_1_7B, 4096))
+    res = {}
+    for width in (256, 1024):
+        cache = KVCache(1, 32, 64, 4096, BLOCK, torch.bfloat16, "cuda", max_seqs=2)
+        cache.add(0)
+        step = cache.append([0], [width])
+        g = torch.Generator(device="cuda").manual_seed(width)
+        qkv = torch.randn(1, width, 96 * 64, generator=g, device="cuda").to(torch.bfloat16)
+        out = torch.empty(1, width, 32 * 64, device="cuda", dtype=torch.bfloat16)
+        ws = ops.AttentionWorkspace(qkv.device)
+        us = time_fn(lambda: ops.rope_paged_attention(qkv, cos, sin, cache.k[0], cache.v[0], cache.table_tensor,
+                                                      step.meta, 1, width, 32, 32, 64, BLOCK, 0.125, step.max_total,
+                                                      out, out.stride(1), ws), graph=True)
+        q, k, v = (torch.randn(1, 32, width, 64, generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+        us_sdpa = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True),
+                          graph=True)
+        flops = 2 * 32 * 64 * width * (width + 1)
+        res[f"prefill_attention_T{width}"] = {"us": us, "tflops": flops / us / 1e6,
+                                              "frac_of_mfma_peak": flops / us / 1e6 / 2500.0,
+                                              "torch_sdpa_contiguous_us": us_sdpa}
+        del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_kernels(attention_grid=True):
     from specdec import ops
     from specdec.workloads import planted_rows
@@ -451,6 +486,7 @@ def bench_kernels(attention_grid=True):
     del cache
     res["rollback_grow_b8"] = bench_rollback()
     res.update(bench_head())
+    res.update(bench_prefill_attention())
     if not attention_grid:
         return res
     # attention over the config-2 grid

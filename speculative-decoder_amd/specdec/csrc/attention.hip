@@ -98,8 +98,7 @@ struct TileInfo {
   bool overflow;  // the row's keys need more splits than max_kv_len allows
 };
 
-__device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
-  const int unit = blockIdx.x;
+__device__ __forceinline__ bool tile_info_at(const AttnArgs &a, int unit, TileInfo &ti, bool any_split) {
   ti.unit = unit;
   ti.qt = unit % a.n_qtiles;
   const int bh = unit / a.n_qtiles;
@@ -124,6 +123,10 @@ __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool 
   if (ti.overflow) return false;
   if (!any_split && (int)blockIdx.y >= ti.nsplit) return false;
   return true;
+}
+
+__device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
+  return tile_info_at(a, blockIdx.x, ti, any_split);
 }
 
 __device__ __forceinline__ int64_t block_of(const AttnArgs &a, const TileInfo &ti, int pos) {
@@ -969,6 +972,192 @@ attention_bf16_kernel(
   else finish_grouped<__hip_bfloat16>(a, ti, m, l, o, s_pool);
 }
 
+// ------------------------------------------------------------- prefill ----
+// Wide bf16 calls (more than kStage new tokens per row: a prompt), with the
+// new K/V already in the pools (rope_append ran first, or the caller wrote
+// them).  One 4-wave workgroup per (row, kv head, four consecutive 16-row
+// query tiles); each wave owns one tile and walks every key up to its last
+// query's position in 64-token steps, online softmax in registers, then
+// writes O / l.  No split partials, no cross-wave fold; the four waves read
+// the same key steps about together, so three of the four reads of a K/V
+// tile are cache hits.  A step's loads are issued while the previous step
+// is computed.  Per step and wave the arithmetic is the decode kernel's
+// (K rows permuted so P^T comes out of the S^T accumulators); the fold
+// order differs from the split kernels', so prefill rows need not equal the
+// bits a decode step of the same token would get (nothing compares them:
+// every path prefills with this kernel).
+constexpr int kPrefillTiles = 4;  // query tiles (waves) per workgroup
+
+template <int MODE>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attention_prefill_kernel(AttnArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qb = blockIdx.x % ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
+  const int bh = blockIdx.x / ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
+  const int qt = qb * kPrefillTiles + wave;
+  if (qt >= a.n_qtiles) return;
+  TileInfo ti;
+  const int g = lane >> 4, c = lane & 15;
+  if (!tile_info_at(a, bh * a.n_qtiles + qt, ti, /*any_split=*/true)) {
+    if (ti.overflow && ti.qt * kRows + c < ti.nrows) {  // beyond max_kv_len: NaN rows, as the other kernels
+      const int rr = ti.qt * kRows + c, tr = rr / ti.group, hr = ti.h * ti.group + rr % ti.group;
+      __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) +
+                            ((int64_t)ti.b * a.width + tr) * a.out_stride + (int64_t)hr * kD;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[16 * g + i] = from_f32<__hip_bfloat16>(NAN);
+    }
+    return;
+  }
+  const int r = ti.qt * kRows + c;
+  const bool row_ok = r < ti.nrows;
+  const int t = row_ok ? r / ti.group : 0;
+  const int hq = ti.h * ti.group + (row_ok ? r % ti.group : 0);
+  const int qpos = ti.past + t;
+  typedef unsigned short u16;
+  const u16 *kp = reinterpret_cast<const u16 *>(a.k);
+  const u16 *vp = reinterpret_cast<const u16 *>(a.v);
+  const u16 *qrow =
+      reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
+  const int Hkv = a.Hkv;
+  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+  const int bs = (MODE == 1) ? 16 : a.bs;
+  const int64_t tile_elems = (int64_t)bs * kD;
+  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
+  const int kv_len = ti.kv_len;
+  const int last_blk = (kv_len - 1) / bs;
+  auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
+  int bj = step_blocks(0);
+
+  // Q operand, rotated in registers for rope calls
+  bf16x8 qop[2];
+  {
+    u32x4 raw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (row_ok) {
+      raw[0] = *reinterpret_cast<const u32x4 *>(qrow + 8 * g);
+      raw[1] = *reinterpret_cast<const u32x4 *>(qrow + 32 + 8 * g);
+    }
+    qop[0] = __builtin_bit_cast(bf16x8, raw[0]);
+    qop[1] = __builtin_bit_cast(bf16x8, raw[1]);
+  }
+  if (a.rope && row_ok) {
+    const float *cs = a.cos_t + (int64_t)qpos * (kD / 2) + 8 * g;
+    const float *sn = a.sin_t + (int64_t)qpos * (kD / 2) + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y1, y2;
+      rope_pair((float)qop[0][j], (float)qop[1][j], cs[j], sn[j], y1, y2);
+      qop[0][j] = (__bf16)y1;
+      qop[1][j] = (__bf16)y2;
+    }
+  }
+
+  struct StepRegs {
+    u32x4 k[2][2][2];  // [chunk][half][kk]
+    u32x4 v[2][4];     // [chunk][dim tile]
+  };
+  auto issue = [&](int c0, int bjv, StepRegs &rg) {
+    const int64_t tofs0 = ((int64_t)__builtin_amdgcn_readlane(bjv, 0) * Hkv + ti.h) * tile_elems;
+    const int64_t tofs1 = ((int64_t)__builtin_amdgcn_readlane(bjv, 1) * Hkv + ti.h) * tile_elems;
+    const int64_t tofs2 = ((int64_t)__builtin_amdgcn_readlane(bjv, 2) * Hkv + ti.h) * tile_elems;
+    const int64_t tofs3 = ((int64_t)__builtin_amdgcn_readlane(bjv, 3) * Hkv + ti.h) * tile_elems;
+    auto group_tile = [&](int ch, bool upper) -> int64_t {
+      return ch == 0 ? (upper ? tofs1 : tofs0) : (upper ? tofs3 : tofs2);
+    };
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cs = c0 + 32 * ch;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
+        rg.k[ch][hf][0] = rg.k[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
+        if ((tok / bs) * bs < kv_len) {
+          const u16 *kb = kp + group_tile(ch, (c >> 3) != 0) + (int64_t)(tok % bs) * kD + 8 * g;
+          rg.k[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
+          rg.k[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
+        }
+      }
+      const int vt = cs + 8 * g;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) rg.v[ch][tt] = u32x4{0u, 0u, 0u, 0u};
+      if ((vt / bs) * bs < kv_len) {
+        const u16 *vb = vp + group_tile(ch, (g >> 1) != 0) + vt % bs;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          rg.v[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
+      }
+    }
+  };
+  f32x4 o[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+  auto compute = [&](int c0, const StepRegs &rg) {
+    float sv[16];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.k[ch][hf][0]), qop[0], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.k[ch][hf][1]), qop[1], sc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = sc[i] * c2;
+      }
+    }
+    if (c0 + 64 > ti.past) {
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int pos = c0 + 32 * ch + 8 * g + j;
+          if (!(row_ok && pos <= qpos && pos < kv_len)) sv[8 * ch + j] = -INFINITY;
+        }
+    }
+    online_update<16>(sv, m, l, o);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      bf16x8 pop;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[8 * ch + j];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.v[ch][tt]), pop, o[tt], 0, 0, 0);
+    }
+  };
+  // two steps in flight: step s + 1's loads go out before step s is computed
+  StepRegs r0, r1;
+  issue(0, bj, r0);
+  int c0 = 0;
+  if (64 < kv_len) bj = step_blocks(64);
+  for (;;) {
+    const bool more = c0 + 64 < kv_len;
+    if (more) {
+      issue(c0 + 64, bj, r1);
+      if (c0 + 128 < kv_len) bj = step_blocks(c0 + 128);
+    }
+    compute(c0, r0);
+    if (!more) break;
+    c0 += 64;
+    const bool more2 = c0 + 64 < kv_len;
+    if (more2) {
+      issue(c0 + 64, bj, r0);
+      if (c0 + 128 < kv_len) bj = step_blocks(c0 + 128);
+    }
+    compute(c0, r1);
+    if (!more2) break;
+    c0 += 64;
+  }
+  // O^T accumulators: lane (c, g) holds dims 16 tt + 4 g + i of query row c
+  if (row_ok) {
+    __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) + ((int64_t)ti.b * a.width + t) * a.out_stride +
+                          (int64_t)hq * kD;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[16 * tt + 4 * g + i] = from_f32<__hip_bfloat16>(o[tt][i] / l);
+  }
+}
+
 // ---------------------------------------------------------------- fp32 ----
 // Same structure on v_mfma_f32_16x16x4_f32: per 16-token group the k index
 // of lane group g is dim 16g+s at step s (QK^T) and token 4g+i at step i (PV).
@@ -1144,6 +1333,7 @@ struct AttnPlan {
   int64_t units = 0;       // (row, kv head, query tile) workgroups
   int64_t need_floats = 0; // workspace floats this call reads and writes
   bool single = false;     // one 16-wave workgroup per unit, no combine
+  bool prefill = false;    // wide bf16 call: attention_prefill_kernel (after rope_append)
   bool nothing = false;    // no work: the call returns at once
 };
 
@@ -1189,6 +1379,12 @@ static int plan_attention(AttnArgs &a, AttnPlan &plan, int dtype, int32_t batch,
   // in one 16-wave workgroup; otherwise one 4-wave workgroup per split +
   // combine
   plan.single = dtype == SPECDEC_BF16 && (a.flat || a.tiled || a.max_splits <= 4);
+  // more than kStage new tokens per row (a prompt): one pass per query tile
+  plan.prefill = dtype == SPECDEC_BF16 && !a.flat && width > kStage && block_size % 16 == 0;
+  if (plan.prefill) {
+    a.tiled = 0;
+    plan.single = true;
+  }
   a.parts = plan.single ? 1 : a.max_splits;
   if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
   plan.units = units;
@@ -1201,6 +1397,20 @@ static int run_attention(AttnArgs &a, const AttnPlan &plan, int dtype, int32_t b
   const bool bs16 = (block_size % 16) == 0;
   const int64_t units = plan.units;
   dim3 grid((unsigned)units, (unsigned)a.parts);
+  if (plan.prefill) {
+    if (a.rope) {  // the new tokens' rotated K and V into the pools, once; q is rotated in registers
+      const int st = launch_rope_append(const_cast<void *>(a.q), SPECDEC_BF16, a.q_stride, a.H, a.Hkv, kD, a.cos_t,
+                                        a.sin_t, a.meta, a.batch, a.width, a.tables, a.table_stride, block_size,
+                                        const_cast<void *>(a.k), const_cast<void *>(a.v), /*kv_only=*/true, s);
+      if (st != SPECDEC_OK) return st;
+    }
+    const int64_t blocks = (int64_t)a.batch * a.Hkv * ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
+    if (blocks > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+    dim3 pgrid((unsigned)blocks), pblock(kAttnThreads);
+    if (block_size == 16) attention_prefill_kernel<1><<<pgrid, pblock, 0, s>>>(a);
+    else attention_prefill_kernel<2><<<pgrid, pblock, 0, s>>>(a);
+    return launch_status();
+  }
   if (a.tiled) {
     dim3 block(16 * kWave);
     if (block_size == 16) attention_bf16_kernel<1, 16, true><<<grid, block, 0, s>>>(a);

@@ -96,21 +96,22 @@ __global__ void slot_map_kernel(const int32_t *__restrict__ tables, int64_t tabl
 }
 
 // One thread per (token, head, rotation pair).  Heads [0, H) are queries,
-// [H, H+Hkv) keys, [H+Hkv, H+2Hkv) values (copied, not rotated).
+// [H, H+Hkv) keys, [H+Hkv, H+2Hkv) values (copied, not rotated).  Heads
+// below head0 are skipped (head0 = H: k and v only, q left as it is).
 template <typename T>
 __global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, int32_t H,
                                    int32_t Hkv, int32_t d, const float *__restrict__ cos_t,
                                    const float *__restrict__ sin_t, const int32_t *__restrict__ meta,
                                    int32_t batch, int32_t width, const int32_t *__restrict__ tables,
                                    int64_t table_stride, int32_t bs, T *__restrict__ kpool,
-                                   T *__restrict__ vpool) {
+                                   T *__restrict__ vpool, int32_t head0) {
   const int half = d / 2;
-  const int heads = H + 2 * Hkv;
+  const int heads = H + 2 * Hkv - head0;
   const int64_t total = (int64_t)batch * width * heads * half;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int i = (int)(idx % half);
-    const int head = (int)((idx / half) % heads);
+    const int head = head0 + (int)((idx / half) % heads);
     const int64_t tok = idx / ((int64_t)half * heads);
     const int b = (int)(tok / width), t = (int)(tok % width);
     const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
@@ -206,6 +207,28 @@ inline unsigned grid_for(int64_t n, int threads) {
   return (unsigned)g;
 }
 
+int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, int32_t Hkv, int32_t d,
+                       const float *cos_t, const float *sin_t, const int32_t *meta, int32_t batch, int32_t width,
+                       const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
+                       bool kv_only, hipStream_t s) {
+  const int32_t head0 = kv_only ? H : 0;
+  const int64_t n = (int64_t)batch * width * (H + 2 * Hkv - head0) * (d / 2);
+  dim3 grid(grid_for(n, 256)), block(256);
+  if (dtype == SPECDEC_BF16) {
+    rope_append_kernel<__hip_bfloat16><<<grid, block, 0, s>>>((__hip_bfloat16 *)qkv, token_stride, H, Hkv, d, cos_t,
+                                                              sin_t, meta, batch, width, tables, table_stride, bs,
+                                                              (__hip_bfloat16 *)k_pool, (__hip_bfloat16 *)v_pool,
+                                                              head0);
+  } else if (dtype == SPECDEC_F32) {
+    rope_append_kernel<float><<<grid, block, 0, s>>>((float *)qkv, token_stride, H, Hkv, d, cos_t, sin_t, meta, batch,
+                                                     width, tables, table_stride, bs, (float *)k_pool,
+                                                     (float *)v_pool, head0);
+  } else {
+    return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
 }  // namespace specdec
 
 using namespace specdec;
@@ -272,22 +295,9 @@ SPECDEC_API int specdec_rope_append(void *qkv, int dtype, int64_t token_stride, 
   if (batch == 0 || width == 0) return SPECDEC_OK;
   if (!qkv || !cos_table || !sin_table || !meta || !tables || !k_pool || !v_pool)
     return SPECDEC_EINVAL;
-  const int64_t n = (int64_t)batch * width * (n_heads + 2 * n_kv_heads) * (head_dim / 2);
-  dim3 grid(grid_for(n, 256)), block(256);
-  hipStream_t s = as_stream(stream);
-  if (dtype == SPECDEC_BF16) {
-    rope_append_kernel<__hip_bfloat16><<<grid, block, 0, s>>>(
-        (__hip_bfloat16 *)qkv, token_stride, n_heads, n_kv_heads, head_dim, cos_table, sin_table,
-        meta, batch, width, tables, table_stride, block_size, (__hip_bfloat16 *)k_pool,
-        (__hip_bfloat16 *)v_pool);
-  } else if (dtype == SPECDEC_F32) {
-    rope_append_kernel<float><<<grid, block, 0, s>>>(
-        (float *)qkv, token_stride, n_heads, n_kv_heads, head_dim, cos_table, sin_table, meta,
-        batch, width, tables, table_stride, block_size, (float *)k_pool, (float *)v_pool);
-  } else {
-    return SPECDEC_EINVAL;
-  }
-  return launch_status();
+  return launch_rope_append(qkv, dtype, token_stride, n_heads, n_kv_heads, head_dim, cos_table, sin_table, meta,
+                            batch, width, tables, table_stride, block_size, k_pool, v_pool, false,
+                            as_stream(stream));
 }
 
 SPECDEC_API int specdec_kv_write(const void *k, const void *v, int dtype, int32_t n_kv_heads,

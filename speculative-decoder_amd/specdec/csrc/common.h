@@ -35,6 +35,14 @@ inline int cu_count() {
   return counts[dev];
 }
 
+// RoPE + paged append of a call's new tokens (cache.hip): q rotated in place
+// and k rotated, both written back / into the pools, v copied; with kv_only
+// the q heads are left untouched.
+int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, int32_t Hkv, int32_t d,
+                       const float *cos_t, const float *sin_t, const int32_t *meta, int32_t batch, int32_t width,
+                       const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
+                       bool kv_only, hipStream_t s);
+
 // ---- element conversion -------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(double x) { return static_cast<float>(x); }
