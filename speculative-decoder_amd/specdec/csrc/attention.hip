@@ -975,64 +975,140 @@ attention_bf16_kernel(
 // ------------------------------------------------------------- prefill ----
 // Wide bf16 calls (more than kStage new tokens per row: a prompt), with the
 // new K/V already in the pools (rope_append ran first, or the caller wrote
-// them).  One 4-wave workgroup per (row, kv head, four consecutive 16-row
-// query tiles); each wave owns one tile and walks every key up to its last
-// query's position in 64-token steps, online softmax in registers, then
-// writes O / l.  No split partials, no cross-wave fold; the four waves read
-// the same key steps about together, so three of the four reads of a K/V
-// tile are cache hits.  A step's loads are issued while the previous step
-// is computed.  Per step and wave the arithmetic is the decode kernel's
-// (K rows permuted so P^T comes out of the S^T accumulators); the fold
-// order differs from the split kernels', so prefill rows need not equal the
-// bits a decode step of the same token would get (nothing compares them:
-// every path prefills with this kernel).
-constexpr int kPrefillTiles = 4;  // query tiles (waves) per workgroup
+// them).  One 8-wave workgroup per (row, kv head, eight consecutive 16-row
+// query tiles); each wave owns one tile.  The workgroup walks its keys in
+// 128-token stages: each stage's K and V tiles (8 pool tiles of 16 tokens,
+// 32 KB) are staged into LDS once, with coalesced 16-byte loads issued two
+// stages ahead (three LDS buffers: a stage's loads have two stages' compute
+// to arrive in), two 64-token steps per stage; every wave reads its MFMA
+// operands from LDS, and a wave whose queries end before a step skips it.  Online softmax in registers, then O / l.  No split partials,
+// no cross-wave fold.  Per step and wave the arithmetic is the decode
+// kernel's (K rows permuted so P^T comes out of the S^T accumulators); the
+// fold order differs from the split kernels', so prefill rows need not equal
+// the bits a decode step of the same token would get (nothing compares
+// them: every path prefills with this kernel).
+constexpr int kPrefillTiles = 8;                     // query tiles (waves) per workgroup
+constexpr int kPrefillThreads = kPrefillTiles * kWave;
+constexpr int kPKStride = kD + 8;                    // bf16 per staged K row (token): 144 bytes
+constexpr int kPVStride = 16 + 8;                    // bf16 per staged V row (dim of a 16-token group): 48 bytes
+constexpr int kPStage = 128;                         // tokens per staged stage
+constexpr int kPGroups = kPStage / 16;               // 16-token groups per stage
+constexpr int kPKElems = kPStage * kPKStride;        // one stage's K
+constexpr int kPVElems = kPGroups * kD * kPVStride;  // one stage's V: [group][dim][token]
+constexpr int kPUnits = 2 * kPGroups * 128 / kPrefillThreads;  // 16-byte staging units per thread
 
 template <int MODE>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-attention_prefill_kernel(AttnArgs a) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int qb = blockIdx.x % ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
-  const int bh = blockIdx.x / ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
-  const int qt = qb * kPrefillTiles + wave;
-  if (qt >= a.n_qtiles) return;
-  TileInfo ti;
-  const int g = lane >> 4, c = lane & 15;
-  if (!tile_info_at(a, bh * a.n_qtiles + qt, ti, /*any_split=*/true)) {
-    if (ti.overflow && ti.qt * kRows + c < ti.nrows) {  // beyond max_kv_len: NaN rows, as the other kernels
-      const int rr = ti.qt * kRows + c, tr = rr / ti.group, hr = ti.h * ti.group + rr % ti.group;
-      __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) +
-                            ((int64_t)ti.b * a.width + tr) * a.out_stride + (int64_t)hr * kD;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dst[16 * g + i] = from_f32<__hip_bfloat16>(NAN);
-    }
-    return;
-  }
-  const int r = ti.qt * kRows + c;
-  const bool row_ok = r < ti.nrows;
-  const int t = row_ok ? r / ti.group : 0;
-  const int hq = ti.h * ti.group + (row_ok ? r % ti.group : 0);
-  const int qpos = ti.past + t;
+__global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(AttnArgs a) {
+  __shared__ __align__(16) unsigned short s_k[3][kPKElems];
+  __shared__ __align__(16) unsigned short s_v[3][kPVElems];
   typedef unsigned short u16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int nqb = (a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles;
+  const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
+  const int qt = qb * kPrefillTiles + wave;
+  // this wave's tile; a wave without one (past the tiles, or rows past the
+  // row's new tokens) still stages and meets the barriers
+  TileInfo ti;
+  const bool live = qt < a.n_qtiles && tile_info_at(a, bh * a.n_qtiles + qt, ti, /*any_split=*/true);
+  if (!live && qt < a.n_qtiles && ti.overflow && ti.qt * kRows + c < ti.nrows) {
+    // beyond max_kv_len: NaN rows, as the other kernels
+    const int rr = ti.qt * kRows + c, tr = rr / ti.group, hr = ti.h * ti.group + rr % ti.group;
+    __hip_bfloat16 *dst =
+        reinterpret_cast<__hip_bfloat16 *>(a.out) + ((int64_t)ti.b * a.width + tr) * a.out_stride + (int64_t)hr * kD;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dst[16 * g + i] = from_f32<__hip_bfloat16>(NAN);
+  }
+  // the workgroup's key range: up to its first wave's tile's row metadata
+  // and the last live tile's last query
+  TileInfo t0;
+  if (!tile_info_at(a, bh * a.n_qtiles + qb * kPrefillTiles, t0, /*any_split=*/true)) return;  // no live tile
+  // (tiles whose keys would pass max_kv_len took the NaN branch above)
+  const int last_qt = min(qb * kPrefillTiles + kPrefillTiles - 1, (t0.nrows - 1) / kRows);
+  const int t_last = min(min(last_qt * kRows + kRows - 1, t0.nrows - 1) / t0.group,
+                         a.max_splits * a.split - 1 - t0.past);
+  const int wg_kv = t0.past + t_last + 1;
+  const int bs = (MODE == 1) ? 16 : a.bs;
+  const int Hkv = a.Hkv;
+  const int32_t *trow = a.tables + (int64_t)t0.row * a.table_stride;
+  const int last_blk = (wg_kv - 1) / bs;
   const u16 *kp = reinterpret_cast<const u16 *>(a.k);
   const u16 *vp = reinterpret_cast<const u16 *>(a.v);
-  const u16 *qrow =
-      reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
-  const int Hkv = a.Hkv;
-  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
-  const int bs = (MODE == 1) ? 16 : a.bs;
   const int64_t tile_elems = (int64_t)bs * kD;
-  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
-  const int kv_len = ti.kv_len;
-  const int last_blk = (kv_len - 1) / bs;
-  auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
-  int bj = step_blocks(0);
 
-  // Q operand, rotated in registers for rope calls
+  // staging: thread tid takes 16-byte units tid + 512 i of the stage's
+  // 2048 (units 0..1023: K, 8 groups x 16 tokens x 8; 1024..2047: V, 8
+  // groups x 64 dims x 2): groups tid / 128 and tid / 128 + 4, the same for
+  // a whole wave, so their block ids are scalar loads (counted apart from
+  // the vector loads: waiting for an id never waits for staged data)
+  u32x4 stg_a[kPUnits], stg_b[kPUnits];
+  const int grp_lo = __builtin_amdgcn_readfirstlane(tid >> 7);
+  // the table is not written while the kernel runs: read through the
+  // constant address space, so a uniform index becomes a scalar load
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const_i32 *trow_c = (const_i32 *)trow;
+  auto blocks_of_stage = [&](int c0, int (&bid)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      bid[h] = trow_c[__builtin_amdgcn_readfirstlane(min((c0 + 16 * (grp_lo + 4 * h)) / bs, last_blk))];
+  };
+  auto unit_of = [&](int i, int &isv, int &grp, int &x) {
+    const int u = tid + i * kPrefillThreads;
+    isv = u >> 10;
+    const int w = u & 1023;
+    grp = w >> 7;
+    x = w & 127;
+  };
+  // Loads are unconditional (a group past the workgroup's keys reads its
+  // clamped block, which is the row's own), so the compiler counts them in
+  // straight-line code and a store waits only for its own stage's loads;
+  // such groups are zeroed when stored.
+  auto stage_load = [&](u32x4 (&stg)[kPUnits], int c0, const int (&bid)[2]) {
+#pragma unroll
+    for (int i = 0; i < kPUnits; ++i) {
+      int isv, grp, x;
+      unit_of(i, isv, grp, x);
+      const int tok0 = c0 + 16 * grp;
+      const int64_t tile = ((int64_t)bid[grp >> 2] * Hkv + t0.h) * tile_elems;
+      if (!isv) {  // K: token x / 8, dims 8 (x % 8) ..
+        const int tk = x >> 3, dd = (x & 7) * 8;
+        stg[i] = *reinterpret_cast<const u32x4 *>(kp + tile + (int64_t)(tok0 % bs + tk) * kD + dd);
+      } else {  // V: dim x / 2, tokens 8 (x % 2) .. of the group
+        const int dim = x >> 1, t8 = (x & 1) * 8;
+        stg[i] = *reinterpret_cast<const u32x4 *>(vp + tile + (int64_t)dim * bs + tok0 % bs + t8);
+      }
+    }
+  };
+  auto stage_store = [&](const u32x4 (&stg)[kPUnits], int buf, int c0) {
+#pragma unroll
+    for (int i = 0; i < kPUnits; ++i) {
+      int isv, grp, x;
+      unit_of(i, isv, grp, x);
+      const u32x4 v = c0 + 16 * grp < wg_kv ? stg[i] : u32x4{0u, 0u, 0u, 0u};
+      if (!isv) {
+        const int tk = x >> 3, dd = (x & 7) * 8;
+        *reinterpret_cast<u32x4 *>(&s_k[buf][(16 * grp + tk) * kPKStride + dd]) = v;
+      } else {
+        const int dim = x >> 1, t8 = (x & 1) * 8;
+        *reinterpret_cast<u32x4 *>(&s_v[buf][(grp * kD + dim) * kPVStride + t8]) = v;
+      }
+    }
+  };
+
+  // this wave's queries
+  const int r = live ? ti.qt * kRows + c : 0;
+  const bool row_ok = live && r < ti.nrows;
+  const int t = row_ok ? r / ti.group : 0;
+  const int hq = live ? ti.h * ti.group + (row_ok ? r % ti.group : 0) : 0;
+  const int qpos = t0.past + t;
+  const int my_kv = live ? ti.kv_len : 0;
+  const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
   bf16x8 qop[2];
   {
     u32x4 raw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
     if (row_ok) {
+      const u16 *qrow =
+          reinterpret_cast<const u16 *>(a.q) + ((int64_t)t0.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
       raw[0] = *reinterpret_cast<const u32x4 *>(qrow + 8 * g);
       raw[1] = *reinterpret_cast<const u32x4 *>(qrow + 32 + 8 * g);
     }
@@ -1050,67 +1126,35 @@ attention_prefill_kernel(AttnArgs a) {
       qop[1][j] = (__bf16)y2;
     }
   }
-
-  struct StepRegs {
-    u32x4 k[2][2][2];  // [chunk][half][kk]
-    u32x4 v[2][4];     // [chunk][dim tile]
-  };
-  auto issue = [&](int c0, int bjv, StepRegs &rg) {
-    const int64_t tofs0 = ((int64_t)__builtin_amdgcn_readlane(bjv, 0) * Hkv + ti.h) * tile_elems;
-    const int64_t tofs1 = ((int64_t)__builtin_amdgcn_readlane(bjv, 1) * Hkv + ti.h) * tile_elems;
-    const int64_t tofs2 = ((int64_t)__builtin_amdgcn_readlane(bjv, 2) * Hkv + ti.h) * tile_elems;
-    const int64_t tofs3 = ((int64_t)__builtin_amdgcn_readlane(bjv, 3) * Hkv + ti.h) * tile_elems;
-    auto group_tile = [&](int ch, bool upper) -> int64_t {
-      return ch == 0 ? (upper ? tofs1 : tofs0) : (upper ? tofs3 : tofs2);
-    };
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      const int cs = c0 + 32 * ch;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
-        rg.k[ch][hf][0] = rg.k[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
-        if ((tok / bs) * bs < kv_len) {
-          const u16 *kb = kp + group_tile(ch, (c >> 3) != 0) + (int64_t)(tok % bs) * kD + 8 * g;
-          rg.k[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
-          rg.k[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
-        }
-      }
-      const int vt = cs + 8 * g;
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) rg.v[ch][tt] = u32x4{0u, 0u, 0u, 0u};
-      if ((vt / bs) * bs < kv_len) {
-        const u16 *vb = vp + group_tile(ch, (g >> 1) != 0) + vt % bs;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          rg.v[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
-      }
-    }
-  };
   f32x4 o[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.0f;
-  auto compute = [&](int c0, const StepRegs &rg) {
+  // one 64-token step (half hs of the stage) from LDS buffer buf
+  auto compute = [&](int c0, int buf, int hs) {
     float sv[16];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
+        const int tk = 64 * hs + 32 * ch + 8 * (c >> 2) + 4 * hf + (c & 3);  // token within the stage
+        const u16 *kr = &s_k[buf][tk * kPKStride + 8 * g];
+        const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kr);
+        const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kr + 32);
         f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.k[ch][hf][0]), qop[0], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.k[ch][hf][1]), qop[1], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k0), qop[0], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k1), qop[1], sc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = sc[i] * c2;
       }
     }
-    if (c0 + 64 > ti.past) {
+    if (c0 + 64 > t0.past) {
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int pos = c0 + 32 * ch + 8 * g + j;
-          if (!(row_ok && pos <= qpos && pos < kv_len)) sv[8 * ch + j] = -INFINITY;
+          if (!(row_ok && pos <= qpos && pos < my_kv)) sv[8 * ch + j] = -INFINITY;
         }
     }
     online_update<16>(sv, m, l, o);
@@ -1119,37 +1163,46 @@ attention_prefill_kernel(AttnArgs a) {
       bf16x8 pop;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[8 * ch + j];
+      // lane group g's 8 tokens: 16-token group 2 ch + g / 2, tokens 8 (g % 2) ..
+      const u16 *vr = &s_v[buf][((4 * hs + 2 * ch + (g >> 1)) * kD + c) * kPVStride + 8 * (g & 1)];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, rg.v[ch][tt]), pop, o[tt], 0, 0, 0);
+      for (int tt = 0; tt < 4; ++tt) {
+        const u32x4 vv = *reinterpret_cast<const u32x4 *>(vr + 16 * tt * kPVStride);
+        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pop, o[tt], 0, 0, 0);
+      }
     }
   };
-  // two steps in flight: step s + 1's loads go out before step s is computed
-  StepRegs r0, r1;
-  issue(0, bj, r0);
-  int c0 = 0;
-  if (64 < kv_len) bj = step_blocks(64);
-  for (;;) {
-    const bool more = c0 + 64 < kv_len;
-    if (more) {
-      issue(c0 + 64, bj, r1);
-      if (c0 + 128 < kv_len) bj = step_blocks(c0 + 128);
-    }
-    compute(c0, r0);
-    if (!more) break;
-    c0 += 64;
-    const bool more2 = c0 + 64 < kv_len;
-    if (more2) {
-      issue(c0 + 64, bj, r0);
-      if (c0 + 128 < kv_len) bj = step_blocks(c0 + 128);
-    }
-    compute(c0, r1);
-    if (!more2) break;
-    c0 += 64;
+  // stage s lives in LDS buffer s % 3; its loads go out during stage s - 2
+  int bid[2];
+  blocks_of_stage(0, bid);
+  stage_load(stg_a, 0, bid);
+  blocks_of_stage(kPStage, bid);
+  stage_store(stg_a, 0, 0);
+  stage_load(stg_a, kPStage, bid);  // stage 1, stored during stage 0
+  blocks_of_stage(2 * kPStage, bid);
+  __syncthreads();
+  auto stage_step = [&](int c0, int buf, u32x4 (&held)[kPUnits], u32x4 (&ahead)[kPUnits]) {
+    // held: stage c0 + kPStage's data, stored now; ahead: stage c0 + 2 kPStage's, loaded now
+    // (every step loads and stores, also past the keys: no branch around a
+    // load, so each wait is for exactly the loads it needs)
+    stage_load(ahead, c0 + 2 * kPStage, bid);
+    blocks_of_stage(c0 + 3 * kPStage, bid);
+    if (c0 < my_kv) compute(c0, buf, 0);
+    if (c0 + 64 < my_kv) compute(c0 + 64, buf, 1);
+    stage_store(held, buf == 2 ? 0 : buf + 1, c0 + kPStage);
+    __syncthreads();
+  };
+  int buf = 0;
+  for (int c0 = 0; c0 < wg_kv; c0 += 2 * kPStage) {
+    stage_step(c0, buf, stg_a, stg_b);
+    buf = buf == 2 ? 0 : buf + 1;
+    if (c0 + kPStage >= wg_kv) break;
+    stage_step(c0 + kPStage, buf, stg_b, stg_a);
+    buf = buf == 2 ? 0 : buf + 1;
   }
   // O^T accumulators: lane (c, g) holds dims 16 tt + 4 g + i of query row c
   if (row_ok) {
-    __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) + ((int64_t)ti.b * a.width + t) * a.out_stride +
+    __hip_bfloat16 *dst = reinterpret_cast<__hip_bfloat16 *>(a.out) + ((int64_t)t0.b * a.width + t) * a.out_stride +
                           (int64_t)hq * kD;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
@@ -1406,7 +1459,7 @@ static int run_attention(AttnArgs &a, const AttnPlan &plan, int dtype, int32_t b
     }
     const int64_t blocks = (int64_t)a.batch * a.Hkv * ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);
     if (blocks > INT32_MAX) return SPECDEC_EUNSUPPORTED;
-    dim3 pgrid((unsigned)blocks), pblock(kAttnThreads);
+    dim3 pgrid((unsigned)blocks), pblock(kPrefillThreads);
     if (block_size == 16) attention_prefill_kernel<1><<<pgrid, pblock, 0, s>>>(a);
     else attention_prefill_kernel<2><<<pgrid, pblock, 0, s>>>(a);
     return launch_status();
