@@ -392,6 +392,7 @@ def bench_head():
             r["head_fused_gbs"] = nbytes / r["head_fused_us"] / 1e3
             r["head_fused_frac_of_peak"] = r["head_fused_gbs"] / HBM_PEAK_GBS
             res[f"head_{name}_rows{rows}"] = r
+            log(f"head {name} rows {rows}: logits {r['head_logits_us']:.2f} us, fused {r['head_fused_us']:.2f} us")
         del heads
         torch.cuda.empty_cache()
     return res
@@ -455,6 +456,7 @@ def bench_kernels(attention_grid=True):
         # the accept kernel reads the rejected position's p and q rows (and
         # gathers 2k probabilities): 2 V fp32 per batch entry
         accept_bytes = 2 * V * 4 * b
+        log(f"accept b{b} k{k}: softmax {us_soft:.2f} us, accept {us_acc:.2f} us")
         res[f"accept_b{b}_k{k}"] = {"softmax_us": us_soft, "accept_us": us_acc, "logit_bytes": logit_bytes,
                                     "softmax_gbs": 2 * logit_bytes / us_soft / 1e3,
                                     "softmax_frac_of_peak": 2 * logit_bytes / us_soft / 1e3 / HBM_PEAK_GBS,
@@ -470,6 +472,7 @@ def bench_kernels(attention_grid=True):
         lens = torch.full((16,), length, dtype=torch.int32, device="cuda")
         us = time_fn(lambda: ops.ngram_lookup(hist, lens, 4, 3), graph=True)
         nbytes = 16 * length * 4
+        log(f"ngram b16 L{length}: {us:.2f} us")
         res[f"ngram_b16_L{length}"] = {"us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
                                        "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
     # config 2': cache append (rope + scatter of 5 tokens) and rollback plan
@@ -485,8 +488,11 @@ def bench_kernels(attention_grid=True):
                            "frac_of_peak": app_bytes / us_app / 1e3 / HBM_PEAK_GBS}
     del cache
     res["rollback_grow_b8"] = bench_rollback()
+    log("append and rollback done")
     res.update(bench_head())
+    log("head done")
     res.update(bench_prefill_attention())
+    log("prefill attention done")
     if not attention_grid:
         return res
     # attention over the config-2 grid

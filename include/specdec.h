@@ -312,6 +312,22 @@ int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
                                  float *workspace, int64_t workspace_floats, void *out,
                                  int64_t out_token_stride, void *stream);
 
+/* ---------------------------------------------------------------- linear --- */
+
+/* out [rows, out_features] bf16 (out_stride apart) = x [rows, in_features]
+ * bf16 (x_stride apart) times w [out_features, in_features] bf16 (w_stride
+ * apart) transposed, products accumulated in fp32 and rounded once to bf16
+ * (round to nearest even); with `accumulate`, the existing out is added
+ * before that rounding (a residual add).  At most 64 rows, in_features a
+ * multiple of 32 up to 8192, w within 2 GiB (else SPECDEC_EUNSUPPORTED); x
+ * and w 16-byte aligned with strides % 8 == 0.  A row's result does not
+ * depend on the other rows of the call or their number.
+ * Replaces the bias-free projections of lm/forward.py:56-58,63-64
+ * (transformers' q/k/v_proj, o_proj, gate/up/down_proj) at decode sizes. */
+int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                   int64_t rows, int64_t in_features, int64_t out_features, void *out,
+                   int64_t out_stride, int32_t accumulate, void *stream);
+
 /* ------------------------------------------------------------------ head --- */
 
 /* Output head: logits [rows, vocab] fp32 (logits_stride apart) = x [rows,

@@ -5,8 +5,8 @@ A forward is split in two:
     and uploads the per-row metadata (table row, past length, new tokens);
   * device part, `forward_core`: six launches per layer for decode,
     verification and draft steps (seven when the attention needs its split
-    combine): the fused QKV GEMM (torch/hipBLASLt) of the unnormalised
-    residual stream; the paged verify-attention kernel, which finishes the
+    combine): the fused QKV projection (specdec_linear at decode sizes,
+    else torch/hipBLASLt) of the unnormalised residual stream; the paged verify-attention kernel, which finishes the
     input RMSNorm (each token's q/k/v scaled by its row's rsqrt(mean(x^2) +
     eps)), applies RoPE, appends the new K/V to the paged pools and reads
     K/V blocks in place (no gather copy, no materialised mask); o_proj
@@ -39,23 +39,42 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return ops.add_rmsnorm(x.clone(), None, weight, out, eps)
 
 
+# bf16 projections of at most this many rows and this inner size run on
+# specdec_linear (one pass over the weight with every load in flight; a
+# row's bits do not depend on the other rows); wider inner sizes (the 8192
+# of the 1.7B's down projection) and more rows run on torch's GEMM, which
+# is faster there
+LINEAR_ROWS, LINEAR_K = 16, 2048
+
+
+def _small(x: torch.Tensor, w: torch.Tensor) -> bool:
+    k = w.shape[-1]
+    return k <= LINEAR_K and x.numel() <= LINEAR_ROWS * k and ops.linear_fits(x, w)
+
+
 def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool) -> torch.Tensor:
-    """x @ w.T on torch: a matrix-vector product when asked for and x is a
-    single row (about a microsecond less per call at decode sizes), else the
-    GEMM.  The two may round differently, so a model uses one of them for
-    every call whose bits must agree."""
+    """x @ w.T: specdec_linear for small bf16 calls; else on torch, a
+    matrix-vector product when asked for and x is a single row (about a
+    microsecond less per call at decode sizes), else the GEMM.  torch's two
+    may round differently, so a model uses one of them for every call whose
+    bits must agree."""
+    if _small(x, w):
+        return ops.linear(x, w)
     if gemv and x.numel() == x.shape[-1]:
         return torch.mv(w, x.reshape(-1)).view(*x.shape[:-1], w.shape[0])
     return F.linear(x, w)
 
 
 def _project_add(hidden: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemv: bool) -> None:
-    """hidden += x @ w.T inside the GEMM (beta = 1, in place), rounded once:
-    a residual add without a kernel of its own.
+    """hidden += x @ w.T inside the projection (specdec_linear's accumulate,
+    or torch's GEMM with beta = 1, in place), rounded once: a residual add
+    without a kernel of its own.
     A 5-row call's rows have the bits of the same rows projected alone, as
     with `_project`."""
     n, k = w.shape
-    if gemv and x.numel() == k:
+    if _small(x, w):
+        ops.linear(x, w, out=hidden.view(-1, n), accumulate=True)
+    elif gemv and x.numel() == k:
         hidden.view(n).addmv_(w, x.reshape(k))
     else:
         hidden.view(-1, n).addmm_(x.reshape(-1, k), w.t())

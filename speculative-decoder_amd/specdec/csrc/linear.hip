@@ -1,0 +1,202 @@
+// Linear layers of few rows (decode, draft and verify steps) on gfx950 MFMA.
+//
+// Reference semantics: the q/k/v, o, gate/up and down projections of
+// lm/forward.py:56-58,63-64 (transformers' nn.Linear without bias, bf16),
+// here with the projections fused as the model stores them (one q|k|v
+// weight, one gate|up weight) and, for the residual adds of :63-64, the
+// add folded into the same rounding: out = bf16(x W^T + out).
+//
+// At decode sizes a projection reads a few MB of weights for one to 64
+// rows, so its time is the latency of one pass over the weight with every
+// load in flight.  Layout: the weight W [N, K] bf16 is split into 16-row
+// feature tiles, one workgroup per tile; the K/32 k-steps of the tile are
+// split between the workgroup's waves (up to 8), each wave streaming its
+// steps' W rows and x rows in batches of 8 k-steps with the next batch's
+// loads in flight while one is multiplied on v_mfma_f32_16x16x32_bf16:
+//   D[feature 4g+i, row c] += W[feature c'][k 8g..] . x[row c][k 8g..]
+// (A = the tile's W rows, lane 16g + c loading the 16 bytes of row c at
+// k = 32s + 8g; B = x rows, the same layout, rows past M reading zeros
+// through the buffer bound).  The waves' partial sums meet in LDS and are
+// added in wave order; lane (c, g) then holds row c's features 4g .. 4g+3.
+// More than 16 rows: up to four 16-row column tiles per wave, each W load
+// feeding one MFMA per column tile.
+// Each output element goes through the same operations whatever M is, so
+// a row's result does not depend on the other rows of the call: a token
+// verified among k+1 and decoded alone get the same bits.
+#include "common.h"
+
+#include <algorithm>
+
+namespace specdec {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+constexpr int kLinRows = 64;        // rows of a call, at most (four 16-row column tiles)
+constexpr int kLinMaxWaves = 8;     // waves per workgroup (k-step split)
+constexpr int kLinMaxSteps = 256;   // K / 32, at most (K <= 8192)
+
+struct LinArgs {
+  const uint16_t *x;  // [M, K] bf16
+  int64_t x_stride;
+  const uint16_t *w;  // [N, K] bf16
+  int64_t w_stride;
+  uint16_t *out;  // [M, N] bf16
+  int64_t out_stride;
+  int M, K, N;
+  int steps;     // K / 32
+  int per_wave;  // k-steps per wave (the last waves may take fewer or none)
+  int accumulate;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// NCT 16-row column tiles of x per wave (each W load feeds NCT MFMAs),
+// KB k-steps per load batch (8 / NCT: the same registers for every NCT).
+template <int NCT, int KB>
+__global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
+  __shared__ f32x4 s_acc[kLinMaxWaves][NCT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int s_lo = wave * a.per_wave;
+  const int cnt = max(min(a.per_wave, a.steps - s_lo), 0);
+  // W rows past N read the last row (never stored); x rows past M read zeros
+  const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.w), 0, (int)((int64_t)a.N * a.w_stride * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.x), 0, (int)(((int64_t)(a.M - 1) * a.x_stride + a.K) * 2), 0x00020000);
+  const int row = min(n0 + c, a.N - 1);
+  const unsigned wbase = (unsigned)(((int64_t)row * a.w_stride + 8 * g) * 2);
+  const unsigned xbase = (unsigned)(((int64_t)c * a.x_stride + 8 * g) * 2);
+  const unsigned xtile = (unsigned)(16 * a.x_stride * 2);  // bytes between column tiles
+  f32x4 acc[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 A0[KB], A1[KB], B0[KB][NCT], B1[KB][NCT];
+  // batch b's loads: steps s_lo + KB b .. (past the wave's last step, its
+  // last step again; those are not multiplied)
+  auto issue = [&](u32x4 (&A)[KB], u32x4 (&B)[KB][NCT], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
+      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * 64u, 0, 0);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        B[j][ct] = __builtin_amdgcn_raw_buffer_load_b128(xb, xbase + ct * xtile + s * 64u, 0, 0);
+    }
+  };
+  auto consume = [&](const u32x4 (&A)[KB], const u32x4 (&B)[KB][NCT], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (b * KB + j < cnt) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[j]),
+                                                            __builtin_bit_cast(bf16x8, B[j][ct]), acc[ct], 0, 0, 0);
+      }
+  };
+  if (cnt > 0) {
+    const int nb = (cnt + KB - 1) / KB;
+    issue(A0, B0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+      issue(A1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A0, B0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(A0, B0, b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b + 1 < nb) {  // the last two batches
+      issue(A1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A0, B0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A1, B1, b + 1);
+    } else {  // the last batch
+      consume(A0, B0, b);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) s_acc[wave][ct][lane] = acc[ct];
+  __syncthreads();
+  // the sums of the waves, in wave order: wave w stores column tiles w,
+  // w + nw, ...
+  const int f0 = n0 + 4 * g;
+  for (int ct = wave; ct < NCT; ct += nw) {
+    const int r = ct * 16 + c;
+    if (r >= a.M) continue;
+    f32x4 t = s_acc[0][ct][lane];
+    for (int w = 1; w < nw; ++w) t += s_acc[w][ct][lane];
+    uint16_t *dst = a.out + (int64_t)r * a.out_stride + f0;
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = t[i];
+      if (a.accumulate && f0 + i < a.N) v += bf16_bits_to_f32(dst[i]);
+      o[i] = __builtin_bit_cast(uint16_t, __float2bfloat16(v));  // round to nearest even
+    }
+    if (f0 + 3 < a.N && ((uintptr_t)dst & 7) == 0) {
+      *reinterpret_cast<u32x2 *>(dst) =
+          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (f0 + i < a.N) dst[i] = o[i];
+    }
+  }
+}
+
+}  // namespace specdec
+
+using namespace specdec;
+
+SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_stride, int64_t rows,
+                               int64_t in_features, int64_t out_features, void *out, int64_t out_stride,
+                               int32_t accumulate, void *stream) {
+  if (rows < 0 || in_features <= 0 || out_features <= 0) return SPECDEC_EINVAL;
+  if (rows == 0) return SPECDEC_OK;
+  if (rows > kLinRows || in_features % 32 != 0 || in_features / 32 > kLinMaxSteps) return SPECDEC_EUNSUPPORTED;
+  // one buffer resource addresses W, another the rows of x (32-bit offsets)
+  if (out_features * w_stride * 2 > INT32_MAX || out_features > INT32_MAX / 2) return SPECDEC_EUNSUPPORTED;
+  if ((int64_t)kLinRows * x_stride * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  if (!x || !w || !out || x_stride < in_features || w_stride < in_features || out_stride < out_features)
+    return SPECDEC_EINVAL;
+  if (x_stride % 8 || w_stride % 8 || ((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 1))
+    return SPECDEC_EINVAL;
+  LinArgs a{};
+  a.x = (const uint16_t *)x;
+  a.x_stride = x_stride;
+  a.w = (const uint16_t *)w;
+  a.w_stride = w_stride;
+  a.out = (uint16_t *)out;
+  a.out_stride = out_stride;
+  a.M = (int)rows;
+  a.K = (int)in_features;
+  a.N = (int)out_features;
+  a.steps = (int)(in_features / 32);
+  a.accumulate = accumulate != 0;
+  const int64_t tiles = (out_features + 15) / 16;
+  if (tiles > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  // The k-split depends on the weight's shape only (never on the rows), so
+  // a row's sums are the same in every call.  Up to 8 k-steps per wave
+  // (one load batch) while that takes at most 8 waves; with a feature tile
+  // for every compute unit, 4 waves of up to 16 steps (more workgroups
+  // resident at once, the whole weight requested in one pass); the steps of
+  // wider weights spread evenly over 8 waves.
+  const int max_waves = tiles >= cu_count() ? 4 : kLinMaxWaves;
+  const int waves = std::min(max_waves, (a.steps + 7) / 8);
+  a.per_wave = (a.steps + waves - 1) / waves;
+  const dim3 grid((unsigned)tiles), block((unsigned)(64 * waves));
+  hipStream_t s = as_stream(stream);
+  if (rows <= 16) linear_kernel<1, 8><<<grid, block, 0, s>>>(a);
+  else if (rows <= 32) linear_kernel<2, 4><<<grid, block, 0, s>>>(a);
+  else linear_kernel<4, 2><<<grid, block, 0, s>>>(a);
+  return launch_status();
+}

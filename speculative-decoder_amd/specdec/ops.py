@@ -271,6 +271,48 @@ def _rows_out(out: torch.Tensor | None, rows: int, v: int, dev: torch.device, na
     return o2
 
 
+LINEAR_ROWS = 64  # rows of a specdec_linear call, at most
+
+
+def linear_fits(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether `linear` takes x @ w.T: bf16, at most LINEAR_ROWS rows, the
+    inner size a multiple of 32 up to 8192, a contiguous weight."""
+    k = w.shape[-1]
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_contiguous()
+            and k % 32 == 0 and k <= 8192 and x.numel() // k <= LINEAR_ROWS and x.is_cuda)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """x [..., K] bf16 times w [N, K] bf16 transposed, accumulated in fp32
+    and rounded once: bf16 [..., N].  With `accumulate`, out += x @ w.T
+    inside that rounding.  A row's result does not depend on the other rows
+    of the call."""
+    gpu(w, "w")
+    _on(w.device, x, "x", torch.bfloat16)
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous bf16 [N, K] tensor")
+    n, k = w.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"x rows have {x.shape[-1]} features, w {k}")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs an out to add to")
+        o2 = torch.empty(rows, n, dtype=torch.bfloat16, device=w.device)
+    else:
+        _on(w.device, out, "out", torch.bfloat16)
+        o2 = out.view(rows, n) if out.dim() != 2 else out
+        if tuple(o2.shape) != (rows, n) or o2.stride(-1) != 1:
+            raise ValueError("out must be bf16 [rows, N] with unit inner stride")
+    st = lib().specdec_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, rows, k, n, o2.data_ptr(), o2.stride(0),
+                              int(accumulate), stream())
+    _check(st, "linear")
+    return o2.view(*x.shape[:-1], n) if out is None else out
+
+
 def head_logits(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., H] bf16 times the head w [V, H] bf16, accumulated in fp32:
     fp32 logits [..., V].  A row's logits do not depend on the other rows

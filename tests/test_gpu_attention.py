@@ -300,9 +300,10 @@ def _attend(cache, step, q, ws, out=None, h=32, hkv=32):
 
 # (batch, cached lengths): 9 splits of 512 at batch 8, 6, ragged 2..9, 18
 # (five groups of four in the combine) and 34 (two rounds of its
-# eight-group fold)
+# eight-group fold); at batch 1 with 6, 9 and 14 splits the grid is small
+# enough for the two-waves-per-SIMD split kernel
 _SPLIT_SHAPES = [(8, [4100 - 7 * b for b in range(8)]), (1, [3000]), (3, [2600, 700, 4500]), (2, [9000, 5000]),
-                 (1, [17000])]
+                 (1, [17000]), (1, [4100]), (1, [7000])]
 
 
 def test_split_workspace_shared_across_shapes():
@@ -323,9 +324,10 @@ def test_split_workspace_shared_across_shapes():
                 assert err < 2e-2, (i, err)
 
 
-@pytest.mark.parametrize("shape", ["split", "tiled"])
+@pytest.mark.parametrize("shape", ["split", "split_b1", "tiled"])
 def test_split_graph_replays_match_eager(shape):
-    """A split-path call (split kernel + combine; or, at batch 8, one tiled
+    """A split-path call (split kernel + combine, at batch 2 or, with the
+    two-waves-per-SIMD split kernel, at batch 1; or, at batch 8, one tiled
     launch) captured in a HIP graph: each replay -- with eager calls of
     another shape on the same workspace in between -- gives the eager
     bits."""
@@ -333,6 +335,8 @@ def test_split_graph_replays_match_eager(shape):
 
     if shape == "split":
         cache, step, q, _ = _filled(2, [5000, 2600], seed=61)
+    elif shape == "split_b1":
+        cache, step, q, _ = _filled(1, [4100], seed=64)
     else:
         cache, step, q, _ = _filled(8, [3000 + 100 * b for b in range(8)], seed=63)
     other = _filled(3, [2600, 700, 4500], seed=62)[:3]
