@@ -291,7 +291,11 @@ int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,
  * heads are rotated in registers, and each workgroup first writes the new
  * tokens' rotated k and their v for its kv head and split into the paged
  * pools (identical values where workgroups overlap), so one launch per layer
- * replaces two.  Same rounding as the two separate kernels.
+ * replaces two.  Same rounding as the two separate kernels; qkv itself is
+ * not modified.  bf16 calls of more than 16 new tokens per row (a prompt)
+ * append the new tokens' k and v in a launch of their own first (one
+ * workgroup per 16 positions and kv head), then run one workgroup per
+ * eight query tiles over its causal keys.
  * With `hidden` not null, the layer's input RMSNorm is finished here too:
  * qkv is then a projection of hidden [batch, width, hidden_dim] bf16 (the
  * unnormalised residual stream) with the norm weight folded into the

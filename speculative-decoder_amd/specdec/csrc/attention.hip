@@ -98,19 +98,30 @@ struct TileInfo {
   bool overflow;  // the row's keys need more splits than max_kv_len allows
 };
 
-__device__ __forceinline__ bool tile_info_at(const AttnArgs &a, int unit, TileInfo &ti, bool any_split) {
+// A unit's coordinates from the grid alone (no memory read): query tile,
+// kv head, batch entry, query heads per kv head.
+__device__ __forceinline__ void tile_coords(const AttnArgs &a, int unit, TileInfo &ti) {
   ti.unit = unit;
   ti.qt = unit % a.n_qtiles;
   const int bh = unit / a.n_qtiles;
   ti.h = bh % a.Hkv;
   ti.b = bh / a.Hkv;
   ti.group = a.H / a.Hkv;
-  // the row's three metadata words in one scalar round trip: the empty asm
-  // uses all three here, so none of the loads is sunk past the early exits
-  // below into a round trip of its own
-  ti.row = a.meta[ti.b];
-  ti.past = a.meta[a.batch + ti.b];
-  ti.nnew = a.meta[2 * a.batch + ti.b];
+}
+
+// The row metadata of a unit whose coordinates are set; false when the
+// tile holds no live query row (or needs more splits than max_kv_len
+// allows: ti.overflow).  The three words are read through the constant
+// address space (the host writes them before the launch), as one scalar
+// round trip that vector loads issued earlier do not hold up.
+__device__ __forceinline__ bool tile_meta(const AttnArgs &a, TileInfo &ti, bool any_split) {
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const_i32 *meta = (const_i32 *)a.meta;
+  ti.row = meta[ti.b];
+  ti.past = meta[a.batch + ti.b];
+  ti.nnew = meta[2 * a.batch + ti.b];
+  // the empty asm uses all three here, so none of the loads is sunk past
+  // the early exits below into a round trip of its own
   __asm__ volatile("" ::"s"(ti.row), "s"(ti.past), "s"(ti.nnew));
   ti.nrows = ti.nnew * ti.group;
   ti.overflow = false;
@@ -123,6 +134,11 @@ __device__ __forceinline__ bool tile_info_at(const AttnArgs &a, int unit, TileIn
   if (ti.overflow) return false;
   if (!any_split && (int)blockIdx.y >= ti.nsplit) return false;
   return true;
+}
+
+__device__ __forceinline__ bool tile_info_at(const AttnArgs &a, int unit, TileInfo &ti, bool any_split) {
+  tile_coords(a, unit, ti);
+  return tile_meta(a, ti, any_split);
 }
 
 __device__ __forceinline__ bool tile_info(const AttnArgs &a, TileInfo &ti, bool any_split = false) {
@@ -582,8 +598,61 @@ template <int MODE, int NW, bool TILED = false, bool PF = false>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(PF ? 2 : 4, PF ? 2 : 4))) void
 attention_bf16_kernel(
     AttnArgs a) {
+  typedef unsigned short u16;
+  constexpr int kThreads = NW * kWave;
+  constexpr int kKT = (kStage * (kD / 2) + kThreads - 1) / kThreads;  // k pairs per thread
+  constexpr int kVT = (kStage * kD + kThreads - 1) / kThreads;        // v elements per thread
   TileInfo ti;
-  if (!tile_info(a, ti, /*any_split=*/NW == 16)) {
+  tile_coords(a, blockIdx.x, ti);
+  // ---- loads that need the grid coordinates only, in flight while the
+  // row metadata is read: the q rows of the call's tokens (rows past a
+  // row's new tokens are dropped below), and with 16 waves (one workgroup
+  // takes every new token of its rows) the new tokens' hidden rows for the
+  // norm and their k / v values for the append
+  const int tid0 = threadIdx.x, lane0 = tid0 & 63;
+  const int r_call = ti.qt * kRows + (lane0 & 15);
+  const bool r_in = r_call < a.width * ti.group;
+  u32x4 qraw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (r_in) {
+    const u16 *qr = reinterpret_cast<const u16 *>(a.q) +
+                    ((int64_t)ti.b * a.width + r_call / ti.group) * a.q_stride +
+                    (int64_t)(ti.h * ti.group + r_call % ti.group) * kD + 8 * (lane0 >> 4);
+    qraw[0] = *reinterpret_cast<const u32x4 *>(qr);
+    qraw[1] = *reinterpret_cast<const u32x4 *>(qr + 32);
+  }
+  const bool pre_norm = NW == 16 && MODE != 0 && a.hidden && a.hdim <= 4 * kWave * 8;
+  const int pre_tok = tid0 >> 6;
+  u32x4 hv_pre[4];
+  if (pre_norm && pre_tok < min(a.width, kStage)) {
+    const int nvec = a.hdim / 8;
+    const u32x4 *hr = reinterpret_cast<const u32x4 *>(a.hidden) + ((int64_t)ti.b * a.width + pre_tok) * nvec;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hv_pre[k] = hr[min(lane0 + kWave * k, nvec - 1)];
+  }
+  const bool pre_kv = NW == 16 && MODE != 0 && a.rope && a.width <= kStage;
+  u16 sk1[kKT], sk2[kKT], svv[kVT];
+  if (pre_kv) {
+    const u16 *qkv16 = reinterpret_cast<const u16 *>(a.q);
+#pragma unroll
+    for (int u = 0; u < kKT; ++u) {
+      const int task = tid0 + u * kThreads;
+      if (task < a.width * (kD / 2)) {
+        const int tk = task / (kD / 2), i = task % (kD / 2);
+        const u16 *kx = qkv16 + ((int64_t)ti.b * a.width + tk) * a.q_stride + (int64_t)(a.H + ti.h) * kD;
+        sk1[u] = kx[i];
+        sk2[u] = kx[i + kD / 2];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kVT; ++u) {
+      const int task = tid0 + u * kThreads;
+      if (task < a.width * kD) {
+        const int tk = task / kD, dd = task % kD;
+        svv[u] = qkv16[((int64_t)ti.b * a.width + tk) * a.q_stride + (int64_t)(a.H + a.Hkv + ti.h) * kD + dd];
+      }
+    }
+  }
+  if (!tile_meta(a, ti, /*any_split=*/NW == 16)) {
     poison_tile<__hip_bfloat16>(a, ti);
     return;
   }
@@ -598,11 +667,8 @@ attention_bf16_kernel(
   const int hq = ti.h * ti.group + (row_ok ? r % ti.group : 0);
   const int qpos = ti.past + t;
 
-  typedef unsigned short u16;
   const u16 *kp = reinterpret_cast<const u16 *>(a.k);
   const u16 *vp = reinterpret_cast<const u16 *>(a.v);
-  const u16 *qrow =
-      reinterpret_cast<const u16 *>(a.q) + ((int64_t)ti.b * a.width + t) * a.q_stride + (int64_t)hq * kD;
 
   const int Hkv = a.Hkv;
   const float c2 = a.scale * 1.4426950408889634f;  // scores in log2 units
@@ -640,15 +706,11 @@ attention_bf16_kernel(
   int bj = 0, bj1 = 0;  // bj1: the second step's (PF)
   if (MODE != 0 && c_first < s_hi) bj = trow[min((c_first + 16 * (lane & 3)) / bs, last_blk)];
   if (PF && c_first + wstride < s_hi) bj1 = trow[min((c_first + wstride + 16 * (lane & 3)) / bs, last_blk)];
-  constexpr int kThreads = NW * kWave;
-  constexpr int kKT = (kStage * (kD / 2) + kThreads - 1) / kThreads;  // k pairs per thread
-  constexpr int kVT = (kStage * kD + kThreads - 1) / kThreads;        // v elements per thread
   // k halves kept as raw bf16 bits until the rotation, so no wait for them
-  // comes before the q and cos/sin loads below are issued
-  u16 sk1[kKT], sk2[kKT];
+  // comes before the q and cos/sin loads below are issued (with 16 waves
+  // they are in flight already: pos - past of a task is its token index)
   float scs[kKT], ssn[kKT];
   int skb[kKT], svb[kVT];
-  u16 svv[kVT];
   const u16 *qkv16 = reinterpret_cast<const u16 *>(a.q);
   auto new_row = [&](int pos) { return qkv16 + ((int64_t)ti.b * a.width + (pos - ti.past)) * a.q_stride; };
   if (staged) {
@@ -657,9 +719,11 @@ attention_bf16_kernel(
       const int task = tid + u * kThreads;
       if (task < n_in * (kD / 2)) {
         const int pos = p0 + task / (kD / 2), i = task % (kD / 2);
-        const u16 *kx = new_row(pos) + (int64_t)(a.H + ti.h) * kD;
-        sk1[u] = kx[i];
-        sk2[u] = kx[i + kD / 2];
+        if (!pre_kv) {
+          const u16 *kx = new_row(pos) + (int64_t)(a.H + ti.h) * kD;
+          sk1[u] = kx[i];
+          sk2[u] = kx[i + kD / 2];
+        }
         scs[u] = a.cos_t[(int64_t)pos * (kD / 2) + i];
         ssn[u] = a.sin_t[(int64_t)pos * (kD / 2) + i];
         skb[u] = trow[pos / bs];
@@ -670,7 +734,7 @@ attention_bf16_kernel(
       const int task = tid + u * kThreads;
       if (task < n_in * kD) {
         const int pos = p0 + task / kD, dd = task % kD;
-        svv[u] = new_row(pos)[(int64_t)(a.H + Hkv + ti.h) * kD + dd];
+        if (!pre_kv) svv[u] = new_row(pos)[(int64_t)(a.H + Hkv + ti.h) * kD + dd];
         svb[u] = trow[pos / bs];
       }
     }
@@ -678,15 +742,13 @@ attention_bf16_kernel(
 
   // Q operand: lane (query c, group g) holds dims 8g..8g+7 (kk = 0) and
   // 32+8g..32+8g+7 (kk = 1) -- the two halves of 8 RoPE pairs
+  // (loaded above for the call's rows; zeros for rows past the row's new
+  // tokens, as those lanes never load)
   bf16x8 qop[2];
   {
-    u32x4 raw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-    if (row_ok) {
-      raw[0] = *reinterpret_cast<const u32x4 *>(qrow + 8 * g);
-      raw[1] = *reinterpret_cast<const u32x4 *>(qrow + 32 + 8 * g);
-    }
-    qop[0] = __builtin_bit_cast(bf16x8, raw[0]);
-    qop[1] = __builtin_bit_cast(bf16x8, raw[1]);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    qop[0] = __builtin_bit_cast(bf16x8, row_ok ? qraw[0] : zero);
+    qop[1] = __builtin_bit_cast(bf16x8, row_ok ? qraw[1] : zero);
   }
   // the rotation's cos/sin, loaded before the norm's barrier below
   float qcs[8], qsn[8];
@@ -716,7 +778,8 @@ attention_bf16_kernel(
       for (int base = 0; base < nvec; base += 4 * kWave) {
         u32x4 hv[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) hv[k] = hr[min(base + lane + kWave * k, nvec - 1)];
+        for (int k = 0; k < 4; ++k)
+          hv[k] = (pre_norm && base == 0) ? hv_pre[k] : hr[min(base + lane + kWave * k, nvec - 1)];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const bool in = base + lane + kWave * k < nvec;
@@ -1452,9 +1515,13 @@ static int run_attention(AttnArgs &a, const AttnPlan &plan, int dtype, int32_t b
   dim3 grid((unsigned)units, (unsigned)a.parts);
   if (plan.prefill) {
     if (a.rope) {  // the new tokens' rotated K and V into the pools, once; q is rotated in registers
-      const int st = launch_rope_append(const_cast<void *>(a.q), SPECDEC_BF16, a.q_stride, a.H, a.Hkv, kD, a.cos_t,
-                                        a.sin_t, a.meta, a.batch, a.width, a.tables, a.table_stride, block_size,
-                                        const_cast<void *>(a.k), const_cast<void *>(a.v), /*kv_only=*/true, s);
+      int st = launch_rope_append_groups(const_cast<void *>(a.q), a.q_stride, a.H, a.Hkv, a.cos_t, a.sin_t, a.meta,
+                                         a.batch, a.width, a.tables, a.table_stride, block_size,
+                                         const_cast<void *>(a.k), const_cast<void *>(a.v), s);
+      if (st == SPECDEC_EUNSUPPORTED)  // unaligned operands: the per-element kernel
+        st = launch_rope_append(const_cast<void *>(a.q), SPECDEC_BF16, a.q_stride, a.H, a.Hkv, kD, a.cos_t, a.sin_t,
+                                a.meta, a.batch, a.width, a.tables, a.table_stride, block_size,
+                                const_cast<void *>(a.k), const_cast<void *>(a.v), /*kv_only=*/true, s);
       if (st != SPECDEC_OK) return st;
     }
     const int64_t blocks = (int64_t)a.batch * a.Hkv * ((a.n_qtiles + kPrefillTiles - 1) / kPrefillTiles);

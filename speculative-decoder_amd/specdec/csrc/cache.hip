@@ -200,11 +200,100 @@ __global__ void kv_gather_kernel(const T *__restrict__ kpool, const T *__restric
   }
 }
 
+// The new tokens' K (rotated) and V of a prompt-sized bf16 call, head_dim
+// 64, block_size % 16 == 0: one workgroup per (batch entry, kv head,
+// 16-position group aligned to 16), so the group's tokens share one block
+// and its V is written as 8-byte runs of four tokens per dim (the pool
+// keeps V dim-major within a block, where one token's values lie bs
+// elements apart).  Thread (token tid / 16, pairs 2 (tid % 16) ..) rotates
+// K as rope_append_kernel does (rope_pair, then one rounding) into the pool
+// (qkv is left as it is, as in the fused decode-sized calls); thread (dim
+// tid / 4, tokens 4 (tid % 4) ..) copies V.  Positions outside
+// [past, past + n_new) are left alone.
+__global__ __launch_bounds__(256) void rope_append_groups_kernel(__hip_bfloat16 *__restrict__ qkv,
+                                                                 int64_t token_stride, int32_t H, int32_t Hkv,
+                                                                 const float *__restrict__ cos_t,
+                                                                 const float *__restrict__ sin_t,
+                                                                 const int32_t *__restrict__ meta, int32_t batch,
+                                                                 int32_t width, const int32_t *__restrict__ tables,
+                                                                 int64_t table_stride, int32_t bs,
+                                                                 __hip_bfloat16 *__restrict__ kpool,
+                                                                 __hip_bfloat16 *__restrict__ vpool) {
+  constexpr int d = 64, half = 32;
+  typedef unsigned short u16;
+  const int b = blockIdx.x / Hkv, h = blockIdx.x % Hkv;
+  const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
+  const int first = past / 16 * 16 + 16 * (int)blockIdx.y;
+  if (first >= past + n) return;
+  const int64_t blk = tables[(int64_t)row * table_stride + first / bs];
+  const int off0 = first % bs;
+  u16 *q16 = reinterpret_cast<u16 *>(qkv);
+  const int tid = threadIdx.x;
+  {  // K
+    const int tt = tid >> 4, i = 2 * (tid & 15);
+    const int pos = first + tt;
+    if (pos >= past && pos < past + n) {
+      const u16 *x = q16 + ((int64_t)b * width + (pos - past)) * token_stride + (int64_t)(H + h) * d;
+      const uint32_t w1 = *reinterpret_cast<const uint32_t *>(x + i);
+      const uint32_t w2 = *reinterpret_cast<const uint32_t *>(x + i + half);
+      const float2 cs = *reinterpret_cast<const float2 *>(cos_t + (int64_t)pos * half + i);
+      const float2 sn = *reinterpret_cast<const float2 *>(sin_t + (int64_t)pos * half + i);
+      float y1a, y2a, y1b, y2b;
+      rope_pair(__uint_as_float(w1 << 16), __uint_as_float(w2 << 16), cs.x, sn.x, y1a, y2a);
+      rope_pair(__uint_as_float(w1 & 0xFFFF0000u), __uint_as_float(w2 & 0xFFFF0000u), cs.y, sn.y, y1b, y2b);
+      auto bits = [](float v) { return (uint32_t)__builtin_bit_cast(u16, from_f32<__hip_bfloat16>(v)); };
+      const uint32_t o1 = bits(y1a) | (bits(y1b) << 16), o2 = bits(y2a) | (bits(y2b) << 16);
+      u16 *dst = reinterpret_cast<u16 *>(kpool) + ((blk * Hkv + h) * bs + off0 + tt) * d;
+      *reinterpret_cast<uint32_t *>(dst + i) = o1;
+      *reinterpret_cast<uint32_t *>(dst + i + half) = o2;
+    }
+  }
+  {  // V
+    const int dim = tid >> 2, t4 = 4 * (tid & 3);
+    u16 v[4];
+    bool all = true;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = first + t4 + j;
+      const bool in = pos >= past && pos < past + n;
+      all = all && in;
+      v[j] = in ? q16[((int64_t)b * width + (pos - past)) * token_stride + (int64_t)(H + Hkv + h) * d + dim] : 0;
+    }
+    u16 *dst = reinterpret_cast<u16 *>(vpool) + ((blk * Hkv + h) * d + dim) * bs + off0 + t4;
+    if (all) {
+      *reinterpret_cast<uint2 *>(dst) =
+          make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pos = first + t4 + j;
+        if (pos >= past && pos < past + n) dst[j] = v[j];
+      }
+    }
+  }
+}
+
 inline unsigned grid_for(int64_t n, int threads) {
   int64_t g = (n + threads - 1) / threads;
   if (g < 1) g = 1;
   if (g > 1 << 20) g = 1 << 20;
   return (unsigned)g;
+}
+
+int launch_rope_append_groups(void *qkv, int64_t token_stride, int32_t H, int32_t Hkv, const float *cos_t,
+                              const float *sin_t, const int32_t *meta, int32_t batch, int32_t width,
+                              const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
+                              hipStream_t s) {
+  // 4- and 8-byte accesses: even token stride, 8-byte aligned bases
+  const uintptr_t bases = (uintptr_t)qkv | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)cos_t | (uintptr_t)sin_t;
+  if (bs % 16 != 0 || token_stride % 2 != 0 || (bases & 7)) return SPECDEC_EUNSUPPORTED;
+  // a row's new positions [past, past + n) meet at most (15 + width + 15) / 16
+  // aligned groups (past % 16 <= 15 positions before the first new one)
+  dim3 grid((unsigned)((int64_t)batch * Hkv), (unsigned)((width + 30) / 16)), block(256);
+  rope_append_groups_kernel<<<grid, block, 0, s>>>((__hip_bfloat16 *)qkv, token_stride, H, Hkv, cos_t, sin_t, meta,
+                                                   batch, width, tables, table_stride, bs,
+                                                   (__hip_bfloat16 *)k_pool, (__hip_bfloat16 *)v_pool);
+  return launch_status();
 }
 
 int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, int32_t Hkv, int32_t d,

@@ -42,6 +42,13 @@ int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, in
                        const float *cos_t, const float *sin_t, const int32_t *meta, int32_t batch, int32_t width,
                        const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
                        bool kv_only, hipStream_t s);
+// The same for the k and v heads only of a prompt-sized bf16 call (head_dim
+// 64, block_size % 16 == 0), one workgroup per 16-position group and kv
+// head, V stored in 8-byte runs (cache.hip).
+int launch_rope_append_groups(void *qkv, int64_t token_stride, int32_t H, int32_t Hkv, const float *cos_t,
+                              const float *sin_t, const int32_t *meta, int32_t batch, int32_t width,
+                              const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
+                              hipStream_t s);
 
 // ---- element conversion -------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }

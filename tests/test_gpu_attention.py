@@ -512,13 +512,14 @@ def _rope_host(x: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("width", [256, 1024])
+@pytest.mark.parametrize("width,bs", [(256, 16), (1024, 16), (256, 32)])
 @pytest.mark.parametrize("heads", [(32, 32), (9, 3)])
 @pytest.mark.parametrize("past", [[0, 0], [100, 0]])
-def test_bf16_prefill_matches_oracle(width, heads, past):
+def test_bf16_prefill_matches_oracle(width, bs, heads, past):
     """A prompt-sized append (256 or 1024 new tokens, right-padded rows of
-    different lengths, from an empty cache or after a cached chunk) through
-    the fused RoPE + append + attention launch, in bf16, against the
+    different lengths, from an empty cache or after a cached chunk that
+    ends inside a 16-position group) through the fused RoPE + append +
+    attention launch, in bf16, with blocks of 16 and 32, against the
     reference's prefill step restated on the host (lm/forward.py:40-49,
     53, 60-63): RoPE of q and k, the new K/V appended after the cached
     ones, causal SDPA.  The pool must hold the host's rotated k and v bit
@@ -526,7 +527,7 @@ def test_bf16_prefill_matches_oracle(width, heads, past):
     from lm.model import LlamaShape, rope_tables
 
     h, hkv = heads
-    d, bs, batch = 64, 16, 2
+    d, batch = 64, 2
     n_new = [width, width - 37]
     theta = 130000.0 if h == 32 else 100000.0
     shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
