@@ -72,6 +72,24 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
   const unsigned wbase = (unsigned)(((int64_t)row * a.w_stride + 8 * g) * 2);
   const unsigned xbase = (unsigned)(((int64_t)c * a.x_stride + 8 * g) * 2);
   const unsigned xtile = (unsigned)(16 * a.x_stride * 2);  // bytes between column tiles
+  // accumulate: the values added before the rounding, loaded now for the
+  // first column tile this wave stores (wave w stores tiles w, w + nw, ...),
+  // so their round trip overlaps the weight's
+  // (through a buffer resource, by every wave and call, with no branch --
+  // a branch would make the compiler convert, and so wait for, the values
+  // right there: rows past M read zeros, features past N are read but never
+  // stored, and waves past NCT read tile NCT - 1's and do not use them)
+  const int f0 = n0 + 4 * g;
+  uint16_t pre[4];
+  {
+    // (without accumulate the resource is empty: every read is out of range,
+    // returns zero and touches no memory)
+    const int obytes = a.accumulate ? (int)(((int64_t)(a.M - 1) * a.out_stride + a.N) * 2) : 0;
+    const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, obytes, 0x00020000);
+    const unsigned obase = (unsigned)(((int64_t)(min(wave, NCT - 1) * 16 + c) * a.out_stride + f0) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[i] = __builtin_amdgcn_raw_buffer_load_b16(ob, obase + 2u * i, 0, 0);
+  }
   f32x4 acc[NCT];
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -128,7 +146,6 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
   __syncthreads();
   // the sums of the waves, in wave order: wave w stores column tiles w,
   // w + nw, ...
-  const int f0 = n0 + 4 * g;
   for (int ct = wave; ct < NCT; ct += nw) {
     const int r = ct * 16 + c;
     if (r >= a.M) continue;
@@ -139,7 +156,7 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float v = t[i];
-      if (a.accumulate && f0 + i < a.N) v += bf16_bits_to_f32(dst[i]);
+      if (a.accumulate && f0 + i < a.N) v += bf16_bits_to_f32(ct == wave ? pre[i] : dst[i]);
       o[i] = __builtin_bit_cast(uint16_t, __float2bfloat16(v));  // round to nearest even
     }
     if (f0 + 3 < a.N && ((uintptr_t)dst & 7) == 0) {
@@ -165,7 +182,7 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
   if (rows > kLinRows || in_features % 32 != 0 || in_features / 32 > kLinMaxSteps) return SPECDEC_EUNSUPPORTED;
   // one buffer resource addresses W, another the rows of x (32-bit offsets)
   if (out_features * w_stride * 2 > INT32_MAX || out_features > INT32_MAX / 2) return SPECDEC_EUNSUPPORTED;
-  if ((int64_t)kLinRows * x_stride * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  if ((int64_t)kLinRows * std::max(x_stride, out_stride) * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
   if (!x || !w || !out || x_stride < in_features || w_stride < in_features || out_stride < out_features)
     return SPECDEC_EINVAL;
   if (x_stride % 8 || w_stride % 8 || ((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)out & 1))
