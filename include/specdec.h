@@ -332,6 +332,23 @@ int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_str
                    int64_t rows, int64_t in_features, int64_t out_features, void *out,
                    int64_t out_stride, int32_t accumulate, void *stream);
 
+/* specdec_linear of x and the fused gate/up weight w [2*inter, in_features]
+ * followed by specdec_rms_silu_mul, in one launch: out [rows, inter] bf16 =
+ * SiLU(bf16(s * g)) * bf16(s * u), where g and u are the bf16 projections
+ * of the gate half (w rows 0 .. inter-1) and the up half, with the bits
+ * specdec_linear gives them, and s = rsqrt(mean(hidden_row^2) + eps) of the
+ * row's residual `hidden` [rows, hidden_dim] bf16 (hidden_stride apart) as
+ * specdec_rms_silu_mul computes it -- the same bits as the two calls, and
+ * the [rows, 2*inter] intermediate is never written.  Limits as
+ * specdec_linear; hidden_dim % 8 == 0 and at most 4096, hidden 16-byte
+ * aligned with hidden_stride % 8 == 0.
+ * Replaces lm/forward.py:64 (post_attention_layernorm, gate/up projection
+ * and act_fn(gate) * up of transformers' LlamaMLP) at decode sizes. */
+int specdec_linear_silu(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                        int64_t rows, int64_t in_features, int64_t inter, const void *hidden,
+                        int64_t hidden_stride, int64_t hidden_dim, float eps, void *out,
+                        int64_t out_stride, void *stream);
+
 /* ------------------------------------------------------------------ head --- */
 
 /* Output head: logits [rows, vocab] fp32 (logits_stride apart) = x [rows,

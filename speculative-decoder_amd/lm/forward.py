@@ -116,7 +116,10 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
                                  hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
                                  split_tokens, norm_of=hidden if in_attn else None, eps=eps)
         _project_add(hidden, attn, layer.wo, gemv)
-        ops.rms_silu_mul(_project(hidden, layer.wgu, gemv), hidden, act, eps)
+        if _small(hidden, layer.wgu):  # gate/up and the MLP's norm + activation in one launch
+            ops.linear_silu(hidden, layer.wgu, hidden, act, eps)
+        else:
+            ops.rms_silu_mul(_project(hidden, layer.wgu, gemv), hidden, act, eps)
         if i + 1 == len(layers):
             ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.norm, x, eps)
         elif in_attn:

@@ -109,6 +109,72 @@ template <typename T> __device__ __forceinline__ T wave_max(T v) {
   return v;
 }
 
+// ---- the post-attention norm finished after the gate/up projection -------
+// (rms_silu_mul_vec_kernel in norm.hip and linear_silu_kernel in linear.hip
+// share these, so a row's activation has the same bits from either.)
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+// s = rsqrt(mean(h^2) + eps) of one bf16 row of `dim` elements stored as
+// nvec 16-byte vectors: lane l adds the squares of its vectors l, l + 64,
+// ... (NV per pass) in order, eight elements each in order, then
+// wave_sum_dpp -- one fixed order, so every wave that computes it gets the
+// same bits.  Contraction is off: each square and each sum is rounded on
+// its own wherever the function is inlined.
+template <int NV>
+__device__ __forceinline__ void row_squares_pass_bf16(const u32x4 (&hv)[NV], int base, int nvec, int lane,
+                                                      float &ss) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const bool in = base + lane + kWave * k < nvec;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const unsigned w = hv[k][e >> 1];
+      const float x = __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+      const float sq = x * x;
+      ss += in ? sq : 0.0f;
+    }
+  }
+}
+template <int NV>
+__device__ __forceinline__ void row_pass_loads(const u32x4 *h, int base, int nvec, int lane, u32x4 (&hv)[NV]) {
+#pragma unroll
+  for (int k = 0; k < NV; ++k) hv[k] = h[min(base + lane + kWave * k, nvec - 1)];
+}
+// The rest of the row after its first pass (hv: that pass's vectors, which
+// a caller may have loaded early), then the wave sum and the scale.
+template <int NV>
+__device__ __forceinline__ float row_rms_scale_bf16_from(const u32x4 *h, const u32x4 (&hv)[NV], int nvec, int dim,
+                                                         float eps, int lane) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+  row_squares_pass_bf16<NV>(hv, 0, nvec, lane, ss);
+  for (int base = kWave * NV; base < nvec; base += kWave * NV) {
+    u32x4 hn[NV];
+    row_pass_loads<NV>(h, base, nvec, lane, hn);
+    row_squares_pass_bf16<NV>(hn, base, nvec, lane, ss);
+  }
+  ss = wave_sum_dpp(ss);
+  return rsqrtf(ss / (float)dim + eps);
+}
+template <int NV>
+__device__ __forceinline__ float row_rms_scale_bf16(const u32x4 *h, int nvec, int dim, float eps, int lane) {
+  u32x4 hv[NV];
+  row_pass_loads<NV>(h, 0, nvec, lane, hv);
+  return row_rms_scale_bf16_from<NV>(h, hv, nvec, dim, eps, lane);
+}
+
+// SiLU(bf16(s g)) * bf16(s u), rounded to bf16 (raw bits): the gate and up
+// values scaled by the row's norm scale and rounded as a projection's output
+// is, then transformers' act_fn(gate) * up with each step rounded to bf16.
+__device__ __forceinline__ unsigned short silu_mul_scaled_bf16(float g, float u, float s) {
+#pragma clang fp contract(off)
+  const float x = to_f32(from_f32<__hip_bfloat16>(s * g));
+  const float up = to_f32(from_f32<__hip_bfloat16>(s * u));
+  const __hip_bfloat16 a = from_f32<__hip_bfloat16>(x / (1.0f + expf(-x)));
+  return __builtin_bit_cast(unsigned short, from_f32<__hip_bfloat16>(to_f32(a) * up));
+}
+
 // Workgroup-wide sum with a fixed reduction order (lane tree, then waves in
 // index order), so repeated launches give identical bits.
 // `scratch` holds at least blockDim.x / 64 elements.

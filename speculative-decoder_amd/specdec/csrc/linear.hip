@@ -170,6 +170,151 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
   }
 }
 
+// The gate/up projection with the MLP's activation in its epilogue: a
+// workgroup computes feature tile t of the gate half (W rows 16 t ..) and
+// of the up half (W rows inter + 16 t ..) of the fused [2 inter, K] weight
+// with the k-split the plain projection of that weight takes, so each of
+// its sums has the plain projection's bits; the sums are rounded to bf16
+// (the projection's output) and turned into act = SiLU(bf16(s g)) *
+// bf16(s u) with the row's post-attention norm scale s computed here from
+// the residual row (row_rms_scale_bf16, the MLP norm kernel's arithmetic).
+// So act has the bits of the projection followed by rms_silu_mul, in one
+// launch, and the [rows, 2 inter] intermediate is never written.
+template <int NCT, int KB, int NVH>
+__global__ __launch_bounds__(kLinMaxWaves * 64) void linear_silu_kernel(LinArgs a, const uint16_t *hid,
+                                                                         int64_t hid_stride, int hdim, float eps,
+                                                                         int inter) {
+  __shared__ f32x4 s_acc[kLinMaxWaves][2][NCT][64];
+  __shared__ float s_scale[kLinRows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int s_lo = wave * a.per_wave;
+  const int cnt = max(min(a.per_wave, a.steps - s_lo), 0);
+  const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.w), 0, (int)((int64_t)a.N * a.w_stride * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.x), 0, (int)(((int64_t)(a.M - 1) * a.x_stride + a.K) * 2), 0x00020000);
+  const int rg = min(n0 + c, inter - 1);  // past the gate half: its last row, never stored
+  const unsigned gbase = (unsigned)(((int64_t)rg * a.w_stride + 8 * g) * 2);
+  const unsigned ubase = (unsigned)(((int64_t)(inter + rg) * a.w_stride + 8 * g) * 2);
+  const unsigned xbase = (unsigned)(((int64_t)c * a.x_stride + 8 * g) * 2);
+  const unsigned xtile = (unsigned)(16 * a.x_stride * 2);
+  // the first pass over this wave's first residual row (row `wave`), loaded
+  // now so its round trip overlaps the weight's (rows past M: not used)
+  const int nvh = hdim / 8;
+  const u32x4 *h0 = reinterpret_cast<const u32x4 *>(hid + (int64_t)min(wave, a.M - 1) * hid_stride);
+  u32x4 hv0[NVH];
+  row_pass_loads<NVH>(h0, 0, nvh, lane, hv0);
+  f32x4 accg[NCT], accu[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) accg[ct] = accu[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 G0[KB], G1[KB], U0[KB], U1[KB], B0[KB][NCT], B1[KB][NCT];
+  auto issue = [&](u32x4 (&G)[KB], u32x4 (&U)[KB], u32x4 (&B)[KB][NCT], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
+      G[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, gbase + s * 64u, 0, 0);
+      U[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, ubase + s * 64u, 0, 0);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        B[j][ct] = __builtin_amdgcn_raw_buffer_load_b128(xb, xbase + ct * xtile + s * 64u, 0, 0);
+    }
+  };
+  auto consume = [&](const u32x4 (&G)[KB], const u32x4 (&U)[KB], const u32x4 (&B)[KB][NCT], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (b * KB + j < cnt) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          accg[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, G[j]),
+                                                             __builtin_bit_cast(bf16x8, B[j][ct]), accg[ct], 0, 0, 0);
+          accu[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, U[j]),
+                                                             __builtin_bit_cast(bf16x8, B[j][ct]), accu[ct], 0, 0, 0);
+        }
+      }
+  };
+  if (cnt > 0) {
+    const int nb = (cnt + KB - 1) / KB;
+    issue(G0, U0, B0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+      issue(G1, U1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(G0, U0, B0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(G0, U0, B0, b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(G1, U1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b + 1 < nb) {
+      issue(G1, U1, B1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(G0, U0, B0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(G1, U1, B1, b + 1);
+    } else {
+      consume(G0, U0, B0, b);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    s_acc[wave][0][ct][lane] = accg[ct];
+    s_acc[wave][1][ct][lane] = accu[ct];
+  }
+  // the rows' norm scales, wave w taking rows w, w + nw, ...
+  for (int r = wave; r < a.M; r += nw) {
+    const u32x4 *hr = reinterpret_cast<const u32x4 *>(hid + (int64_t)r * hid_stride);
+    const float sc = r == wave ? row_rms_scale_bf16_from<NVH>(hr, hv0, nvh, hdim, eps, lane)
+                               : row_rms_scale_bf16<NVH>(hr, nvh, hdim, eps, lane);
+    if (lane == 0) s_scale[r] = sc;
+  }
+  __syncthreads();
+  const int f0 = n0 + 4 * g;
+  for (int ct = wave; ct < NCT; ct += nw) {
+    const int r = ct * 16 + c;
+    if (r >= a.M) continue;
+    f32x4 tg = s_acc[0][0][ct][lane], tu = s_acc[0][1][ct][lane];
+    for (int w = 1; w < nw; ++w) {
+      tg += s_acc[w][0][ct][lane];
+      tu += s_acc[w][1][ct][lane];
+    }
+    const float sc = s_scale[r];
+    uint16_t *dst = a.out + (int64_t)r * a.out_stride + f0;
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the projection's bf16 outputs, then the activation
+      const float gv = to_f32(from_f32<__hip_bfloat16>(tg[i]));
+      const float uv = to_f32(from_f32<__hip_bfloat16>(tu[i]));
+      o[i] = silu_mul_scaled_bf16(gv, uv, sc);
+    }
+    if (f0 + 3 < inter && ((uintptr_t)dst & 7) == 0) {
+      *reinterpret_cast<u32x2 *>(dst) =
+          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (f0 + i < inter) dst[i] = o[i];
+    }
+  }
+}
+
+// The k-split of a [N, K] weight: waves per workgroup and k-steps per wave.
+static void linear_split(LinArgs &a, int64_t tiles, int &waves) {
+  // The k-split depends on the weight's shape only (never on the rows), so
+  // a row's sums are the same in every call.  Up to 8 k-steps per wave
+  // (one load batch) while that takes at most 8 waves; with a feature tile
+  // for every compute unit, 4 waves of up to 16 steps (more workgroups
+  // resident at once, the whole weight requested in one pass); the steps of
+  // wider weights spread evenly over 8 waves.
+  const int max_waves = tiles >= cu_count() ? 4 : kLinMaxWaves;
+  waves = std::min(max_waves, (a.steps + 7) / 8);
+  a.per_wave = (a.steps + waves - 1) / waves;
+}
+
 }  // namespace specdec
 
 using namespace specdec;
@@ -201,19 +346,59 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
   a.accumulate = accumulate != 0;
   const int64_t tiles = (out_features + 15) / 16;
   if (tiles > INT32_MAX) return SPECDEC_EUNSUPPORTED;
-  // The k-split depends on the weight's shape only (never on the rows), so
-  // a row's sums are the same in every call.  Up to 8 k-steps per wave
-  // (one load batch) while that takes at most 8 waves; with a feature tile
-  // for every compute unit, 4 waves of up to 16 steps (more workgroups
-  // resident at once, the whole weight requested in one pass); the steps of
-  // wider weights spread evenly over 8 waves.
-  const int max_waves = tiles >= cu_count() ? 4 : kLinMaxWaves;
-  const int waves = std::min(max_waves, (a.steps + 7) / 8);
-  a.per_wave = (a.steps + waves - 1) / waves;
+  int waves = 0;
+  linear_split(a, tiles, waves);
   const dim3 grid((unsigned)tiles), block((unsigned)(64 * waves));
   hipStream_t s = as_stream(stream);
   if (rows <= 16) linear_kernel<1, 8><<<grid, block, 0, s>>>(a);
   else if (rows <= 32) linear_kernel<2, 4><<<grid, block, 0, s>>>(a);
   else linear_kernel<4, 2><<<grid, block, 0, s>>>(a);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_linear_silu(const void *x, int64_t x_stride, const void *w, int64_t w_stride, int64_t rows,
+                                    int64_t in_features, int64_t inter, const void *hidden, int64_t hidden_stride,
+                                    int64_t hidden_dim, float eps, void *out, int64_t out_stride, void *stream) {
+  if (rows < 0 || in_features <= 0 || inter <= 0 || hidden_dim <= 0) return SPECDEC_EINVAL;
+  if (rows == 0) return SPECDEC_OK;
+  if (rows > kLinRows || in_features % 32 != 0 || in_features / 32 > kLinMaxSteps) return SPECDEC_EUNSUPPORTED;
+  if (hidden_dim % 8 != 0 || hidden_dim > 8 * 64 * 8) return SPECDEC_EUNSUPPORTED;
+  const int64_t n = 2 * inter;
+  if (n * w_stride * 2 > INT32_MAX || n > INT32_MAX / 2) return SPECDEC_EUNSUPPORTED;
+  if ((int64_t)kLinRows * x_stride * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  if (!x || !w || !out || !hidden || x_stride < in_features || w_stride < in_features || out_stride < inter ||
+      hidden_stride < hidden_dim)
+    return SPECDEC_EINVAL;
+  if (x_stride % 8 || w_stride % 8 || hidden_stride % 8 || ((uintptr_t)x & 15) || ((uintptr_t)w & 15) ||
+      ((uintptr_t)hidden & 15) || ((uintptr_t)out & 1))
+    return SPECDEC_EINVAL;
+  LinArgs a{};
+  a.x = (const uint16_t *)x;
+  a.x_stride = x_stride;
+  a.w = (const uint16_t *)w;
+  a.w_stride = w_stride;
+  a.out = (uint16_t *)out;
+  a.out_stride = out_stride;
+  a.M = (int)rows;
+  a.K = (int)in_features;
+  a.N = (int)n;
+  a.steps = (int)(in_features / 32);
+  // the plain projection's k-split for this [2 inter, K] weight
+  int waves = 0;
+  linear_split(a, (n + 15) / 16, waves);
+  const dim3 grid((unsigned)((inter + 15) / 16)), block((unsigned)(64 * waves));
+  const uint16_t *h = (const uint16_t *)hidden;
+  const int hd = (int)hidden_dim, nvec = hd / 8;
+  hipStream_t s = as_stream(stream);
+#define SPECDEC_LINEAR_SILU(NCT, KB)                                                                          \
+  do {                                                                                                    \
+    if (nvec <= 2 * 64) linear_silu_kernel<NCT, KB, 2><<<grid, block, 0, s>>>(a, h, hidden_stride, hd, eps, (int)inter); \
+    else if (nvec <= 4 * 64) linear_silu_kernel<NCT, KB, 4><<<grid, block, 0, s>>>(a, h, hidden_stride, hd, eps, (int)inter); \
+    else linear_silu_kernel<NCT, KB, 8><<<grid, block, 0, s>>>(a, h, hidden_stride, hd, eps, (int)inter); \
+  } while (0)
+  if (rows <= 16) SPECDEC_LINEAR_SILU(1, 4);
+  else if (rows <= 32) SPECDEC_LINEAR_SILU(2, 2);
+  else SPECDEC_LINEAR_SILU(4, 1);
+#undef SPECDEC_LINEAR_SILU
   return launch_status();
 }

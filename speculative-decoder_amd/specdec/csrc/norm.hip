@@ -181,6 +181,17 @@ __global__ __launch_bounds__(256) void rms_silu_mul_vec_kernel(const T *__restri
   const u32x4 u = reinterpret_cast<const u32x4 *>(gu + r * 2 * inter + inter)[ic];
   const u32x4 *h = reinterpret_cast<const u32x4 *>(hidden + r * dim);
   const int nvec = (int)(dim / E);
+  if constexpr (sizeof(T) == 2) {
+    // bf16: the helpers linear_silu_kernel shares (same bits for a row)
+    const float s = row_rms_scale_bf16<NV>(h, nvec, (int)dim, eps, lane);
+    if (!live) return;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      vec_set<T>(o, e, __builtin_bit_cast(T, silu_mul_scaled_bf16(vec_elem<T>(g, e), vec_elem<T>(u, e), s)));
+    reinterpret_cast<u32x4 *>(out + r * inter)[i] = o;
+    return;
+  }
   float ss = 0.0f;
   for (int base = 0; base < nvec; base += kWave * NV) {
     u32x4 hv[NV];

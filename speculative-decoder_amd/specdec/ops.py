@@ -313,6 +313,33 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, ac
     return o2.view(*x.shape[:-1], n) if out is None else out
 
 
+def linear_silu(x: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor, out: torch.Tensor, eps: float) -> torch.Tensor:
+    """rms_silu_mul(linear(x, w), hidden, out, eps) in one launch, with the
+    same bits: w is the fused [2 I, K] gate/up weight, out bf16 [..., I]."""
+    gpu(w, "w")
+    _on(w.device, x, "x", torch.bfloat16)
+    _on(w.device, hidden, "hidden", torch.bfloat16)
+    _on(w.device, out, "out", torch.bfloat16)
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous() or w.shape[0] % 2:
+        raise ValueError("w must be a contiguous bf16 [2 I, K] tensor")
+    n2, k = w.shape
+    inter = n2 // 2
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    h2 = hidden.reshape(rows, -1)
+    if h2.stride(-1) != 1 or h2.stride(0) % 8 or h2.data_ptr() % 16:
+        h2 = h2.contiguous()
+    o2 = out.view(rows, inter) if out.dim() != 2 else out
+    if tuple(o2.shape) != (rows, inter) or o2.stride(-1) != 1:
+        raise ValueError("out must be bf16 [rows, I] with unit inner stride")
+    st = lib().specdec_linear_silu(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, rows, k, inter, h2.data_ptr(),
+                                   h2.stride(0), h2.shape[1], float(eps), o2.data_ptr(), o2.stride(0), stream())
+    _check(st, "linear_silu")
+    return out
+
+
 def head_logits(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., H] bf16 times the head w [V, H] bf16, accumulated in fp32:
     fp32 logits [..., V].  A row's logits do not depend on the other rows

@@ -123,3 +123,30 @@ def test_unsupported_shapes_are_refused():
     x, w = operands(2, 48, 16, seed=1)  # K not a multiple of 32
     with pytest.raises(NotImplementedError):
         ops.linear(x.to(DEV), w.to(DEV))
+
+
+@pytest.mark.parametrize("rows,k,inter,hdim,same", [(1, 576, 1536, 576, True), (5, 2048, 8192, 2048, True),
+                                                     (16, 576, 1536, 576, True), (3, 64, 104, 64, False),
+                                                     (40, 576, 1536, 576, True), (7, 96, 48, 1024, False)])
+def test_linear_silu_equals_linear_then_rms_silu_mul(rows, k, inter, hdim, same):
+    """The gate/up projection with the MLP's norm scale and SiLU·up in its
+    epilogue has the bits of specdec_linear followed by rms_silu_mul (the
+    decode-sized MLP of lm/forward.py: x is the residual row itself), also
+    for a gate half that ends inside a 16-feature tile."""
+    g = torch.Generator().manual_seed(rows * 13 + inter)
+    w = (torch.randn(2 * inter, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    hidden = (torch.randn(rows, hdim, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    x = hidden if same else (torch.randn(rows, k, generator=g)).to(torch.bfloat16).to(DEV)
+    eps = 1e-5
+    fused = torch.full((rows, inter), 7.0, dtype=torch.bfloat16, device=DEV)
+    ops.linear_silu(x, w, hidden, fused, eps)
+    two = torch.empty(rows, inter, dtype=torch.bfloat16, device=DEV)
+    ops.rms_silu_mul(ops.linear(x, w), hidden, two, eps)
+    assert torch.equal(fused, two)
+    # and the activation is what transformers computes from the same bf16 gate/up values
+    gu = ops.linear(x, w).float().cpu()
+    s = torch.rsqrt(hidden.float().cpu().pow(2).mean(-1, keepdim=True) + eps)
+    gate = (s * gu[:, :inter]).to(torch.bfloat16).float()
+    up = (s * gu[:, inter:]).to(torch.bfloat16).float()
+    want = (torch.nn.functional.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16)
+    assert (fused.cpu().float() - want.float()).abs().max().item() <= 2 ** -6 * want.float().abs().max().item()
