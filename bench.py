@@ -180,6 +180,38 @@ def bench_e2e(steps, warmup):
     return result, (target, draft, t_state, d_state, prompt, outs[0])
 
 
+def bench_e2e_torch_projections(target, draft, prompt, want, steps=2):
+    """The same request with every dense projection on torch's GEMMs
+    (hipBLASLt; torch matrix-vector products for the draft's single rows)
+    instead of specdec_linear: fresh caches, so the graphs are captured
+    anew with torch's projections."""
+    import lm.forward as fwd
+
+    saved = fwd.LINEAR_KERNEL
+    fwd.LINEAR_KERNEL = False
+    try:
+        caches = caches_for(target, draft)
+        run_e2e(target, draft, prompt, caches)  # warm-up, graph capture
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out, stats = run_e2e(target, draft, prompt, caches)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        # the greedy identity holds in this configuration too (its bf16
+        # projections round differently, so its tokens may differ from the
+        # headline path's on these random weights)
+        from baselines.cached_autoregressive import generate as plain
+
+        plain_out = plain(target, caches_for(target, None)[0], prompt, NEW_TOKENS)
+    finally:
+        fwd.LINEAR_KERNEL = saved
+    del caches
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": len(out) * steps / dt, "ms_per_step": 1000 * dt / steps, "rounds": stats.rounds,
+            "identical_to_plain_greedy": out == plain_out, "same_tokens_as_headline_path": out == want}
+
+
 def bench_truncated_drafts(target, t_state, prompt, depths=(4, 12, 18, 22), noise=0.002):
     """Config 4's second variant: the draft is the target's first n layers
     (embeddings, final norm and head shared) plus N(0, noise^2) on every matrix
@@ -1049,6 +1081,8 @@ def main():
 
     e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
     log(f"e2e {e2e}")
+    e2e["torch_projections"] = bench_e2e_torch_projections(target, draft, prompt, gpu_tokens)
+    log(f"torch projections {e2e['torch_projections']}")
     e2e["truncated_drafts"] = bench_truncated_drafts(target, t_state, prompt)
     e2e["copy_draft"] = bench_copy_draft(target, prompt, gpu_tokens)
     log(f"copy draft {e2e['copy_draft']}")

@@ -24,6 +24,8 @@ The device part reads everything it needs from device memory, so a fixed
 """
 from __future__ import annotations
 
+import os
+
 import torch
 import torch.nn.functional as F
 
@@ -43,13 +45,15 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 # specdec_linear (one pass over the weight with every load in flight; a
 # row's bits do not depend on the other rows); wider inner sizes (the 8192
 # of the 1.7B's down projection) and more rows run on torch's GEMM, which
-# is faster there
+# is faster there.  SPECDEC_TORCH_PROJECTIONS=1 (or LINEAR_KERNEL = False
+# before a model's graphs are captured) keeps every projection on torch.
 LINEAR_ROWS, LINEAR_K = 16, 2048
+LINEAR_KERNEL = os.environ.get("SPECDEC_TORCH_PROJECTIONS", "0") != "1"
 
 
 def _small(x: torch.Tensor, w: torch.Tensor) -> bool:
     k = w.shape[-1]
-    return k <= LINEAR_K and x.numel() <= LINEAR_ROWS * k and ops.linear_fits(x, w)
+    return LINEAR_KERNEL and k <= LINEAR_K and x.numel() <= LINEAR_ROWS * k and ops.linear_fits(x, w)
 
 
 def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool) -> torch.Tensor:
