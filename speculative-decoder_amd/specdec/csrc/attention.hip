@@ -1035,6 +1035,235 @@ attention_bf16_kernel(
   else finish_grouped<__hip_bfloat16>(a, ti, m, l, o, s_pool);
 }
 
+// ------------------------------------------------------------- decode -----
+// Latency decode steps of one new token per row (the draft model's steps,
+// split_tokens < 0: results that need not match other calls), bf16, block
+// size a multiple of 16, q/k/v from the fused projection, at most 16 query
+// heads per kv head: one 4-wave workgroup per (row, kv head).  Compared with
+// the 16-wave flat grid it takes no barrier before its fold:
+//   - the loads that need only the grid coordinates (q, the new token's k
+//     and v, the residual row for the input norm) go out before the row
+//     metadata is read;
+//   - every wave computes the norm scale itself (the same lane order for
+//     all), rotates q and the new k in registers and takes the new token's
+//     K and V from registers inside its step (the pool copy is written for
+//     later calls, not read back);
+//   - wave w takes the 64-token steps w, w+4, ..., two at a time with both
+//     steps' loads in flight, then the four waves fold in LDS (fold_wg4).
+template <int MODE>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_decode_kernel(
+    AttnArgs a) {
+  typedef unsigned short u16;
+  TileInfo ti;
+  tile_coords(a, blockIdx.x, ti);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const bool row_in = c < ti.group;  // this lane's query row exists (one token per row)
+  const u16 *xrow = reinterpret_cast<const u16 *>(a.q) + (int64_t)ti.b * a.width * a.q_stride;
+  // ---- loads that need the grid coordinates only
+  u32x4 qraw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (row_in) {
+    const u16 *qr = xrow + (int64_t)(ti.h * ti.group + c) * kD + 8 * g;
+    qraw[0] = *reinterpret_cast<const u32x4 *>(qr);
+    qraw[1] = *reinterpret_cast<const u32x4 *>(qr + 32);
+  }
+  const u16 *kx = xrow + (int64_t)(a.H + ti.h) * kD + 8 * g;
+  const u32x4 kraw0 = *reinterpret_cast<const u32x4 *>(kx);
+  const u32x4 kraw1 = *reinterpret_cast<const u32x4 *>(kx + 32);
+  const u16 *vx = xrow + (int64_t)(a.H + a.Hkv + ti.h) * kD + c;
+  u16 vraw[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) vraw[tt] = vx[16 * tt];
+  const bool norm_in = a.hidden != nullptr;
+  const int nvh = a.hdim / 8;
+  const u32x4 *hr = norm_in ? reinterpret_cast<const u32x4 *>(a.hidden) + (int64_t)ti.b * a.width * nvh : nullptr;
+  u32x4 hv[4];
+  if (norm_in) row_pass_loads<4>(hr, 0, nvh, lane, hv);
+  if (!tile_meta(a, ti, /*any_split=*/true)) {
+    poison_tile<__hip_bfloat16>(a, ti);
+    return;
+  }
+  const int p = ti.past;  // the new token's position, and the query's
+  const int kv_len = ti.kv_len;
+  const int bs = (MODE == 1) ? 16 : a.bs;
+  const int Hkv = a.Hkv;
+  const int64_t tile_elems = (int64_t)bs * kD;
+  const int32_t *trow = a.tables + (int64_t)ti.row * a.table_stride;
+  const int last_blk = (kv_len - 1) / bs;
+  const u16 *kp = reinterpret_cast<const u16 *>(a.k);
+  const u16 *vp = reinterpret_cast<const u16 *>(a.v);
+  // the first two steps' block ids (lane j & 3: tokens c0 + 16j ..), RoPE tables at p
+  const int c_first = 64 * wave;
+  auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
+  int bj0 = 0, bj1 = 0;
+  if (c_first < kv_len) bj0 = step_blocks(c_first);
+  if (c_first + 256 < kv_len) bj1 = step_blocks(c_first + 256);
+  float cs8[8], sn8[8];
+  {
+    const float *cs = a.cos_t + (int64_t)p * (kD / 2) + 8 * g;
+    const float *sn = a.sin_t + (int64_t)p * (kD / 2) + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cs8[j] = cs[j], sn8[j] = sn[j];
+  }
+  // ---- the input norm's scale, RoPE of q and of the new k (registers)
+  const float sc = norm_in ? row_rms_scale_bf16_from<4>(hr, hv, nvh, a.hdim, a.eps, lane) : 1.0f;
+  auto scaled = [&](unsigned short bits) -> float {
+    const float x = __uint_as_float((unsigned)bits << 16);
+    return norm_in ? to_f32(from_f32<__hip_bfloat16>(sc * x)) : x;
+  };
+  auto half_of = [](const u32x4 &v, int j) -> unsigned short {
+    return (unsigned short)((j & 1) ? (v[j >> 1] >> 16) : (v[j >> 1] & 0xFFFFu));
+  };
+  bf16x8 qop[2], knew[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float y1, y2;
+    rope_pair(scaled(half_of(qraw[0], j)), scaled(half_of(qraw[1], j)), cs8[j], sn8[j], y1, y2);
+    qop[0][j] = row_in ? (__bf16)y1 : (__bf16)0.0f;
+    qop[1][j] = row_in ? (__bf16)y2 : (__bf16)0.0f;
+    rope_pair(scaled(half_of(kraw0, j)), scaled(half_of(kraw1, j)), cs8[j], sn8[j], y1, y2);
+    knew[0][j] = (__bf16)y1;
+    knew[1][j] = (__bf16)y2;
+  }
+  u16 vnew[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+    vnew[tt] = norm_in ? __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(sc * __uint_as_float((unsigned)vraw[tt] << 16)))
+                       : vraw[tt];
+  // the pool copy of the new token, for later calls (lanes of wave 0)
+  const int64_t pblk = trow[p / bs];
+  if (wave == 0) {
+    const int64_t ptile = (pblk * Hkv + ti.h) * tile_elems;
+    if (c == 0) {
+      u16 *kd = const_cast<u16 *>(kp) + ptile + (int64_t)(p % bs) * kD + 8 * g;
+      *reinterpret_cast<u32x4 *>(kd) = __builtin_bit_cast(u32x4, knew[0]);
+      *reinterpret_cast<u32x4 *>(kd + 32) = __builtin_bit_cast(u32x4, knew[1]);
+    }
+    if (g == 0) {
+      u16 *vd = const_cast<u16 *>(vp) + ptile + p % bs;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) vd[(int64_t)(16 * tt + c) * bs] = vnew[tt];
+    }
+  }
+
+  struct StepRegs {
+    u32x4 k[2][2][2];  // [chunk][half][kk]
+    u32x4 v[2][4];     // [chunk][dim tile]
+  };
+  auto issue = [&](int c0, int bjv, StepRegs &r) {
+    const int64_t t0 = ((int64_t)__builtin_amdgcn_readlane(bjv, 0) * Hkv + ti.h) * tile_elems;
+    const int64_t t1 = ((int64_t)__builtin_amdgcn_readlane(bjv, 1) * Hkv + ti.h) * tile_elems;
+    const int64_t t2 = ((int64_t)__builtin_amdgcn_readlane(bjv, 2) * Hkv + ti.h) * tile_elems;
+    const int64_t t3 = ((int64_t)__builtin_amdgcn_readlane(bjv, 3) * Hkv + ti.h) * tile_elems;
+    auto group_tile = [&](int ch, bool upper) -> int64_t { return ch == 0 ? (upper ? t1 : t0) : (upper ? t3 : t2); };
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cs = c0 + 32 * ch;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
+        r.k[ch][hf][0] = r.k[ch][hf][1] = u32x4{0u, 0u, 0u, 0u};
+        if ((tok / bs) * bs < kv_len) {
+          const u16 *kb = kp + group_tile(ch, (c >> 3) != 0) + (int64_t)(tok % bs) * kD + 8 * g;
+          r.k[ch][hf][0] = *reinterpret_cast<const u32x4 *>(kb);
+          r.k[ch][hf][1] = *reinterpret_cast<const u32x4 *>(kb + 32);
+        }
+      }
+      const int vt = cs + 8 * g;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) r.v[ch][tt] = u32x4{0u, 0u, 0u, 0u};
+      if ((vt / bs) * bs < kv_len) {
+        const u16 *vb = vp + group_tile(ch, (g >> 1) != 0) + vt % bs;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) r.v[ch][tt] = *reinterpret_cast<const u32x4 *>(vb + (int64_t)(16 * tt + c) * bs);
+      }
+    }
+  };
+  const float c2 = a.scale * 1.4426950408889634f;
+  f32x4 o[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+  auto compute = [&](int c0, StepRegs &r) {
+    if (c0 + 64 > p) {  // the step holding the new token: its K and V from registers
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        const int cs = c0 + 32 * ch;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int tok = cs + 8 * (c >> 2) + 4 * hf + (c & 3);
+          if (tok == p) {
+            r.k[ch][hf][0] = __builtin_bit_cast(u32x4, knew[0]);
+            r.k[ch][hf][1] = __builtin_bit_cast(u32x4, knew[1]);
+          }
+        }
+        const int i = p - (cs + 8 * g);
+        if (i >= 0 && i < 8) {
+          const unsigned sh = 16 * (i & 1);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              if (w == (i >> 1)) r.v[ch][tt][w] = (r.v[ch][tt][w] & ~(0xFFFFu << sh)) | ((unsigned)vnew[tt] << sh);
+          }
+        }
+      }
+    }
+    float sv[16];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[ch][hf][0]), qop[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[ch][hf][1]), qop[1], acc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[8 * ch + 4 * hf + i] = acc[i] * c2;
+      }
+    }
+    if (c0 + 64 > p) {  // keys past the query (the new token is the last key)
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (!(row_in && c0 + 32 * ch + 8 * g + j <= p)) sv[8 * ch + j] = -INFINITY;
+    } else if (!row_in) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sv[j] = -INFINITY;
+    }
+    online_update<16>(sv, m, l, o);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      bf16x8 pop;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pop[j] = (__bf16)sv[8 * ch + j];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.v[ch][tt]), pop, o[tt], 0, 0, 0);
+    }
+  };
+  // two steps at a time (c0 and c0 + 256), both steps' loads in flight
+  for (int c0 = c_first; c0 < kv_len; c0 += 512) {
+    const bool two = c0 + 256 < kv_len;
+    StepRegs r0, r1;
+    issue(c0, bj0, r0);
+    if (two) issue(c0 + 256, bj1, r1);
+    if (c0 + 512 < kv_len) bj0 = step_blocks(c0 + 512);
+    if (c0 + 768 < kv_len) bj1 = step_blocks(c0 + 768);
+    compute(c0, r0);
+    if (two) compute(c0 + 256, r1);
+  }
+  float M, L, O[4];
+  fold_wg4(m, l, o, M, L, O);
+  const int qq = tid >> 4, d0 = (tid & 15) * 4;
+  if (qq < ti.group) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
+    store_row4<__hip_bfloat16>(a, ti, qq, d0, v);
+  }
+}
+
 // ------------------------------------------------------------- prefill ----
 // Wide bf16 calls (more than kStage new tokens per row: a prompt), with the
 // new K/V already in the pools (rope_append ran first, or the caller wrote
@@ -1450,6 +1679,7 @@ struct AttnPlan {
   int64_t need_floats = 0; // workspace floats this call reads and writes
   bool single = false;     // one 16-wave workgroup per unit, no combine
   bool prefill = false;    // wide bf16 call: attention_prefill_kernel (after rope_append)
+  bool decode = false;     // latency decode step: attention_decode_kernel
   bool nothing = false;    // no work: the call returns at once
 };
 
@@ -1501,6 +1731,12 @@ static int plan_attention(AttnArgs &a, AttnPlan &plan, int dtype, int32_t batch,
     a.tiled = 0;
     plan.single = true;
   }
+  // one new token per row, latency split, fused RoPE (+ norm), a kv head's
+  // queries in one tile, contexts up to 2048 (at most two rounds of two
+  // steps per wave): the 4-wave decode kernel
+  plan.decode = a.flat && a.rope && width == 1 && block_size % 16 == 0 && max_kv_len <= 2048 &&
+                n_heads / n_kv_heads <= kRows && (!a.hidden || a.hdim <= 4 * kWave * 8);
+  if (plan.decode) a.tiled = 0;
   a.parts = plan.single ? 1 : a.max_splits;
   if (units > INT32_MAX || a.max_splits > 65535) return SPECDEC_EUNSUPPORTED;
   plan.units = units;
@@ -1529,6 +1765,12 @@ static int run_attention(AttnArgs &a, const AttnPlan &plan, int dtype, int32_t b
     dim3 pgrid((unsigned)blocks), pblock(kPrefillThreads);
     if (block_size == 16) attention_prefill_kernel<1><<<pgrid, pblock, 0, s>>>(a);
     else attention_prefill_kernel<2><<<pgrid, pblock, 0, s>>>(a);
+    return launch_status();
+  }
+  if (plan.decode) {
+    dim3 block(kAttnThreads);
+    if (block_size == 16) attention_decode_kernel<1><<<grid, block, 0, s>>>(a);
+    else attention_decode_kernel<2><<<grid, block, 0, s>>>(a);
     return launch_status();
   }
   if (a.tiled) {

@@ -491,6 +491,66 @@ def test_input_norm_in_attention_equals_prescaled_qkv(batch, lengths, heads, hid
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("lengths", [[300, 37], [1500, 700], [2000, 1]])
+@pytest.mark.parametrize("heads,hidden_dim", [((9, 3), 576), ((32, 32), 2048), ((8, 1), 512)])
+def test_latency_decode_step_input_norm_equals_prescaled_qkv(lengths, heads, hidden_dim):
+    """A draft-style decode step (one new token per row, split -1: the 4-wave
+    decode kernel, whose waves each compute the norm scale and take the new
+    token's K and V from registers) with the norm finished inside equals the
+    same step on pre-scaled q/k/v, output and pool contents bit for bit."""
+    ref, got = _norm_case(len(lengths), lengths, heads[0], heads[1], hidden_dim, -1, t_new=1, seed=len(lengths) + heads[0])
+    for a, b in zip(ref, got):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("lengths", [[300, 37, 1], [1500, 2040]])
+@pytest.mark.parametrize("heads", [(9, 3), (32, 32)])
+def test_latency_decode_step_matches_oracle(bs, lengths, heads):
+    """The decode kernel against the reference's decode step on the host
+    (lm/forward.py:40-49, 53, 60-63 with one new token): RoPE of q and k at
+    the row's position, the new K/V appended, SDPA over every cached key.
+    The pool holds the host's rotated k and v bit for bit."""
+    from lm.model import LlamaShape, rope_tables
+
+    h, hkv = heads
+    d, batch = 64, len(lengths)
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=100000.0)
+    cos_h, sin_h = rope_tables(shape, 2112)
+    cos, sin = cos_h.cuda(), sin_h.cuda()
+    g = torch.Generator().manual_seed(bs + h + lengths[0])
+    cache = make_cache(1, hkv, d, sum(n // bs + 3 for n in lengths) + 8, bs, torch.bfloat16, 11)
+    ids = list(range(batch))
+    for s_ in ids:
+        cache.add(s_)
+    hist_k = [torch.randn(hkv, n, d, generator=g).to(torch.bfloat16) for n in lengths]
+    hist_v = [torch.randn(hkv, n, d, generator=g).to(torch.bfloat16) for n in lengths]
+    step = cache.append(ids, lengths)
+    cache.write(0, step, padded(hist_k, max(lengths)).to(torch.bfloat16).cuda(),
+                padded(hist_v, max(lengths)).to(torch.bfloat16).cuda())
+    step = cache.append(ids, [1] * batch)
+    qkv = torch.randn(batch, 1, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16)
+    out = torch.zeros(batch, 1, h * d, dtype=torch.bfloat16, device="cuda")
+    ops.rope_paged_attention(qkv.cuda(), cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta, batch, 1, h,
+                             hkv, d, bs, 0.125, step.max_total, out, out.stride(1), split_tokens=-1)
+    q_all = qkv[..., : h * d].view(batch, 1, h, d).transpose(1, 2)
+    k_new = qkv[..., h * d:(h + hkv) * d].view(batch, 1, hkv, d).transpose(1, 2)
+    v_new = qkv[..., (h + hkv) * d:].view(batch, 1, hkv, d).transpose(1, 2)
+    host_k, host_v, q_rot = [], [], torch.zeros(batch, h, 1, d)
+    for b in range(batch):
+        pos = torch.tensor([lengths[b]])
+        q_rot[b] = _rope_host(q_all[b], pos, cos_h, sin_h).float()
+        host_k.append(torch.cat([hist_k[b], _rope_host(k_new[b], pos, cos_h, sin_h)], dim=1))
+        host_v.append(torch.cat([hist_v[b], v_new[b]], dim=1))
+    k_all, v_all = padded(host_k, step.max_total), padded(host_v, step.max_total)
+    dev_k, dev_v = cache.gather(0, step)
+    assert torch.equal(dev_k.cpu().float(), k_all) and torch.equal(dev_v.cpu().float(), v_all)
+    want = of.attention(q_rot, k_all, v_all, torch.tensor(lengths), torch.tensor(step.total), 0.125)
+    got = out.view(batch, 1, h, d).transpose(1, 2).float().cpu()
+    assert (got - want).abs().max().item() < 2e-2
+
+
 def test_input_norm_in_attention_rejects_other_shapes():
     cache, step, q, _ = _filled(1, [40], 0)
     h = torch.zeros(1, 20, 64, dtype=torch.bfloat16, device="cuda")
