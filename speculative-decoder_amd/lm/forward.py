@@ -3,21 +3,26 @@
 A forward is split in two:
   * host part: `cache.append` decides block growth (one block-plan launch)
     and uploads the per-row metadata (table row, past length, new tokens);
-  * device part, `forward_core`: six launches per layer for decode,
-    verification and draft steps (seven when the attention needs its split
-    combine): the fused QKV projection (specdec_linear at decode sizes,
-    else torch/hipBLASLt) of the unnormalised residual stream; the paged verify-attention kernel, which finishes the
-    input RMSNorm (each token's q/k/v scaled by its row's rsqrt(mean(x^2) +
-    eps)), applies RoPE, appends the new K/V to the paged pools and reads
-    K/V blocks in place (no gather copy, no materialised mask); o_proj
-    accumulated into the residual stream by the GEMM itself (beta = 1); the
-    gate/up GEMM of the unnormalised stream; one kernel that finishes the
-    post-attention norm and applies SiLU*up; the down GEMM, again
-    accumulated into the stream -- then the final norm and the fp32 output
-    projection (lm/forward.py:71-84).  The norm weights live in the
-    projections' columns (lm/model.py:Layer).  Prefill (more than 16 new
-    tokens) and fp32 models normalise in a kernel of their own instead,
-    without the weight.
+  * device part, `forward_core`: five launches per layer for decode,
+    verification and draft steps (six when the attention needs its split
+    combine):
+      - the fused QKV projection (specdec_linear at decode sizes, else
+        torch/hipBLASLt) of the unnormalised residual stream;
+      - the paged attention kernel, which finishes the input RMSNorm (each
+        token's q/k/v scaled by its row's rsqrt(mean(x^2) + eps)), applies
+        RoPE, appends the new K/V to the paged pools and reads K/V blocks in
+        place (no gather copy, no materialised mask) -- for a draft step,
+        as split partials over four CUs per kv head;
+      - o_proj accumulated into the residual stream by the projection itself
+        (folding the draft step's partials first);
+      - gate/up of the unnormalised stream with the post-attention norm and
+        SiLU*up in its epilogue (specdec_linear_silu; a separate kernel
+        after a torch GEMM for wider calls);
+      - the down projection, again accumulated into the stream;
+    then the final norm and the fp32 output projection (lm/forward.py:71-84).
+    The norm weights live in the projections' columns (lm/model.py:Layer).
+    Prefill (more than 16 new tokens) and fp32 models normalise in a kernel
+    of their own instead, without the weight.
 The device part reads everything it needs from device memory, so a fixed
 (batch, width) shape can be captured once in a HIP graph and replayed
 (lm/graphs.py).
@@ -114,12 +119,24 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
         ops.add_rmsnorm(hidden, None, llama.unit_norm, x, eps)
     attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
     act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
+    # a draft step's attention spread over four CUs per kv head, its partials
+    # folded by the o_proj launch (the same bits as attention, then o_proj)
+    parts = None
+    if (in_attn and LINEAR_KERNEL and _small(attn, layers[0].wo) and
+            ops.decode_parts_fit(hidden.dtype, b, t, h, hk, d, cache.block_size, max_kv_len, split_tokens)):
+        parts = ops.decode_parts_buffer(b, h, hidden.device)
     for i, layer in enumerate(layers):
         qkv = _project(hidden if in_attn else x, layer.wqkv, gemv)
-        ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t, h,
-                                 hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1), workspace,
-                                 split_tokens, norm_of=hidden if in_attn else None, eps=eps)
-        _project_add(hidden, attn, layer.wo, gemv)
+        if parts is not None:
+            ops.rope_paged_attention_parts(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta,
+                                           b, h, hk, d, cache.block_size, llama.scaling, max_kv_len, parts,
+                                           norm_of=hidden, eps=eps)
+            ops.linear_attn_parts(parts, b, h, layer.wo, hidden.view(b, -1), accumulate=True)
+        else:
+            ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t,
+                                     h, hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1),
+                                     workspace, split_tokens, norm_of=hidden if in_attn else None, eps=eps)
+            _project_add(hidden, attn, layer.wo, gemv)
         if _small(hidden, layer.wgu):  # gate/up and the MLP's norm + activation in one launch
             ops.linear_silu(hidden, layer.wgu, hidden, act, eps)
         else:

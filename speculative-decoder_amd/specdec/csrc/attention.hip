@@ -1039,50 +1039,60 @@ attention_bf16_kernel(
 // Latency decode steps of one new token per row (the draft model's steps,
 // split_tokens < 0: results that need not match other calls), bf16, block
 // size a multiple of 16, q/k/v from the fused projection, at most 16 query
-// heads per kv head: one 4-wave workgroup per (row, kv head).  Compared with
-// the 16-wave flat grid it takes no barrier before its fold:
+// heads per kv head.  A (row, kv head)'s keys are taken by 4 waves, wave w
+// taking the 64-token steps w, w+4, ... two at a time with both steps'
+// loads in flight (decode_wave); the waves are either one workgroup that
+// folds them in LDS (attention_decode_kernel) or four one-wave workgroups on
+// four compute units that write their (m, l, O) for the output projection to
+// fold (attention_decode_parts_kernel).  Compared with the 16-wave flat grid
+// it takes no barrier before its fold:
 //   - the loads that need only the grid coordinates (q, the new token's k
 //     and v, the residual row for the input norm) go out before the row
-//     metadata is read;
+//     metadata is read (decode_early);
 //   - every wave computes the norm scale itself (the same lane order for
 //     all), rotates q and the new k in registers and takes the new token's
 //     K and V from registers inside its step (the pool copy is written for
-//     later calls, not read back);
-//   - wave w takes the 64-token steps w, w+4, ..., two at a time with both
-//     steps' loads in flight, then the four waves fold in LDS (fold_wg4).
-template <int MODE>
-__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_decode_kernel(
-    AttnArgs a) {
+//     later calls, not read back).
+struct DecodeEarly {
+  u32x4 qraw[2];
+  u32x4 kraw0, kraw1;
+  unsigned short vraw[4];
+  u32x4 hv[4];
+  const u32x4 *hr;
+};
+
+__device__ __forceinline__ void decode_early(const AttnArgs &a, const TileInfo &ti, int lane, DecodeEarly &e) {
   typedef unsigned short u16;
-  TileInfo ti;
-  tile_coords(a, blockIdx.x, ti);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const bool row_in = c < ti.group;  // this lane's query row exists (one token per row)
   const u16 *xrow = reinterpret_cast<const u16 *>(a.q) + (int64_t)ti.b * a.width * a.q_stride;
-  // ---- loads that need the grid coordinates only
-  u32x4 qraw[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-  if (row_in) {
+  e.qraw[0] = e.qraw[1] = u32x4{0u, 0u, 0u, 0u};
+  if (c < ti.group) {
     const u16 *qr = xrow + (int64_t)(ti.h * ti.group + c) * kD + 8 * g;
-    qraw[0] = *reinterpret_cast<const u32x4 *>(qr);
-    qraw[1] = *reinterpret_cast<const u32x4 *>(qr + 32);
+    e.qraw[0] = *reinterpret_cast<const u32x4 *>(qr);
+    e.qraw[1] = *reinterpret_cast<const u32x4 *>(qr + 32);
   }
   const u16 *kx = xrow + (int64_t)(a.H + ti.h) * kD + 8 * g;
-  const u32x4 kraw0 = *reinterpret_cast<const u32x4 *>(kx);
-  const u32x4 kraw1 = *reinterpret_cast<const u32x4 *>(kx + 32);
+  e.kraw0 = *reinterpret_cast<const u32x4 *>(kx);
+  e.kraw1 = *reinterpret_cast<const u32x4 *>(kx + 32);
   const u16 *vx = xrow + (int64_t)(a.H + a.Hkv + ti.h) * kD + c;
-  u16 vraw[4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) vraw[tt] = vx[16 * tt];
-  const bool norm_in = a.hidden != nullptr;
+  for (int tt = 0; tt < 4; ++tt) e.vraw[tt] = vx[16 * tt];
   const int nvh = a.hdim / 8;
-  const u32x4 *hr = norm_in ? reinterpret_cast<const u32x4 *>(a.hidden) + (int64_t)ti.b * a.width * nvh : nullptr;
-  u32x4 hv[4];
-  if (norm_in) row_pass_loads<4>(hr, 0, nvh, lane, hv);
-  if (!tile_meta(a, ti, /*any_split=*/true)) {
-    poison_tile<__hip_bfloat16>(a, ti);
-    return;
-  }
+  e.hr = a.hidden ? reinterpret_cast<const u32x4 *>(a.hidden) + (int64_t)ti.b * a.width * nvh : nullptr;
+  if (a.hidden) row_pass_loads<4>(e.hr, 0, nvh, lane, e.hv);
+}
+
+// Wave w (of kDecWaves) of kv head ti.h, row metadata read: its (m, l, O)
+// over its steps.  `writer`: this wave writes the new token's K and V to the
+// pools (one wave per (row, kv head) of the launch).
+template <int MODE>
+__device__ __forceinline__ void decode_wave(const AttnArgs &a, const TileInfo &ti, int wave, bool writer,
+                                            const DecodeEarly &e, float &m, float &l, f32x4 (&o)[4]) {
+  typedef unsigned short u16;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const bool row_in = c < ti.group;  // this lane's query row exists (one token per row)
+  const bool norm_in = a.hidden != nullptr;
   const int p = ti.past;  // the new token's position, and the query's
   const int kv_len = ti.kv_len;
   const int bs = (MODE == 1) ? 16 : a.bs;
@@ -1093,11 +1103,12 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   const u16 *kp = reinterpret_cast<const u16 *>(a.k);
   const u16 *vp = reinterpret_cast<const u16 *>(a.v);
   // the first two steps' block ids (lane j & 3: tokens c0 + 16j ..), RoPE tables at p
+  constexpr int kPair = 64 * kDecWaves;  // tokens from a wave's first step to its second
   const int c_first = 64 * wave;
   auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
   int bj0 = 0, bj1 = 0;
   if (c_first < kv_len) bj0 = step_blocks(c_first);
-  if (c_first + 256 < kv_len) bj1 = step_blocks(c_first + 256);
+  if (c_first + kPair < kv_len) bj1 = step_blocks(c_first + kPair);
   float cs8[8], sn8[8];
   {
     const float *cs = a.cos_t + (int64_t)p * (kD / 2) + 8 * g;
@@ -1106,7 +1117,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     for (int j = 0; j < 8; ++j) cs8[j] = cs[j], sn8[j] = sn[j];
   }
   // ---- the input norm's scale, RoPE of q and of the new k (registers)
-  const float sc = norm_in ? row_rms_scale_bf16_from<4>(hr, hv, nvh, a.hdim, a.eps, lane) : 1.0f;
+  const float sc = norm_in ? row_rms_scale_bf16_from<4>(e.hr, e.hv, a.hdim / 8, a.hdim, a.eps, lane) : 1.0f;
   auto scaled = [&](unsigned short bits) -> float {
     const float x = __uint_as_float((unsigned)bits << 16);
     return norm_in ? to_f32(from_f32<__hip_bfloat16>(sc * x)) : x;
@@ -1118,21 +1129,21 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     float y1, y2;
-    rope_pair(scaled(half_of(qraw[0], j)), scaled(half_of(qraw[1], j)), cs8[j], sn8[j], y1, y2);
+    rope_pair(scaled(half_of(e.qraw[0], j)), scaled(half_of(e.qraw[1], j)), cs8[j], sn8[j], y1, y2);
     qop[0][j] = row_in ? (__bf16)y1 : (__bf16)0.0f;
     qop[1][j] = row_in ? (__bf16)y2 : (__bf16)0.0f;
-    rope_pair(scaled(half_of(kraw0, j)), scaled(half_of(kraw1, j)), cs8[j], sn8[j], y1, y2);
+    rope_pair(scaled(half_of(e.kraw0, j)), scaled(half_of(e.kraw1, j)), cs8[j], sn8[j], y1, y2);
     knew[0][j] = (__bf16)y1;
     knew[1][j] = (__bf16)y2;
   }
   u16 vnew[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
-    vnew[tt] = norm_in ? __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(sc * __uint_as_float((unsigned)vraw[tt] << 16)))
-                       : vraw[tt];
-  // the pool copy of the new token, for later calls (lanes of wave 0)
+    vnew[tt] = norm_in ? __builtin_bit_cast(u16, from_f32<__hip_bfloat16>(sc * __uint_as_float((unsigned)e.vraw[tt] << 16)))
+                       : e.vraw[tt];
+  // the pool copy of the new token, for later calls
   const int64_t pblk = trow[p / bs];
-  if (wave == 0) {
+  if (writer) {
     const int64_t ptile = (pblk * Hkv + ti.h) * tile_elems;
     if (c == 0) {
       u16 *kd = const_cast<u16 *>(kp) + ptile + (int64_t)(p % bs) * kD + 8 * g;
@@ -1145,7 +1156,6 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
       for (int tt = 0; tt < 4; ++tt) vd[(int64_t)(16 * tt + c) * bs] = vnew[tt];
     }
   }
-
   struct StepRegs {
     u32x4 k[2][2][2];  // [chunk][half][kk]
     u32x4 v[2][4];     // [chunk][dim tile]
@@ -1180,10 +1190,10 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     }
   };
   const float c2 = a.scale * 1.4426950408889634f;
-  f32x4 o[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f;
+  m = -INFINITY;
+  l = 0.0f;
   auto compute = [&](int c0, StepRegs &r) {
     if (c0 + 64 > p) {  // the step holding the new token: its K and V from registers
 #pragma unroll
@@ -1242,17 +1252,35 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
         o[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.v[ch][tt]), pop, o[tt], 0, 0, 0);
     }
   };
-  // two steps at a time (c0 and c0 + 256), both steps' loads in flight
-  for (int c0 = c_first; c0 < kv_len; c0 += 512) {
-    const bool two = c0 + 256 < kv_len;
+  // two steps at a time (c0 and c0 + kPair), both steps' loads in flight
+  for (int c0 = c_first; c0 < kv_len; c0 += 2 * kPair) {
+    const bool two = c0 + kPair < kv_len;
     StepRegs r0, r1;
     issue(c0, bj0, r0);
-    if (two) issue(c0 + 256, bj1, r1);
-    if (c0 + 512 < kv_len) bj0 = step_blocks(c0 + 512);
-    if (c0 + 768 < kv_len) bj1 = step_blocks(c0 + 768);
+    if (two) issue(c0 + kPair, bj1, r1);
+    if (c0 + 2 * kPair < kv_len) bj0 = step_blocks(c0 + 2 * kPair);
+    if (c0 + 3 * kPair < kv_len) bj1 = step_blocks(c0 + 3 * kPair);
     compute(c0, r0);
-    if (two) compute(c0 + 256, r1);
+    if (two) compute(c0 + kPair, r1);
   }
+}
+
+// One 4-wave workgroup per (row, kv head): the waves fold in LDS.
+template <int MODE>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_decode_kernel(
+    AttnArgs a) {
+  TileInfo ti;
+  tile_coords(a, blockIdx.x, ti);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  DecodeEarly e;
+  decode_early(a, ti, lane, e);
+  if (!tile_meta(a, ti, /*any_split=*/true)) {
+    poison_tile<__hip_bfloat16>(a, ti);
+    return;
+  }
+  float m, l;
+  f32x4 o[4];
+  decode_wave<MODE>(a, ti, wave, /*writer=*/wave == 0, e, m, l, o);
   float M, L, O[4];
   fold_wg4(m, l, o, M, L, O);
   const int qq = tid >> 4, d0 = (tid & 15) * 4;
@@ -1261,6 +1289,47 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = O[i] / L;
     store_row4<__hip_bfloat16>(a, ti, qq, d0, v);
+  }
+}
+
+// Four one-wave workgroups per (row, kv head), on four compute units (one
+// CU issuing all of a head's K/V loads is what bounds the 4-wave kernel):
+// workgroup w runs wave w of decode_wave and writes its (m, l, O), O not
+// divided by l, for the rows of its kv head to parts [batch, H, kDecWaves,
+// kDecPart] floats (m, l, then O's 64 dims).  Folding a row's four in wave
+// order with fold_waves' arithmetic and rounding O / L to bf16 gives the
+// bits of attention_decode_kernel's output (linear_parts_kernel does that
+// in its prologue).  A row past max_kv_len gets a partial that folds to
+// NaN; a row without a new token gets none.
+template <int MODE>
+__global__ __launch_bounds__(kWave) void attention_decode_parts_kernel(AttnArgs a, float *parts) {
+  TileInfo ti;
+  const int wave = blockIdx.x % kDecWaves;
+  tile_coords(a, blockIdx.x / kDecWaves, ti);
+  const int lane = threadIdx.x, g = lane >> 4, c = lane & 15;
+  DecodeEarly e;
+  decode_early(a, ti, lane, e);
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (tile_meta(a, ti, /*any_split=*/true)) {
+    decode_wave<MODE>(a, ti, wave, /*writer=*/wave == 0, e, m, l, o);
+  } else {
+    if (!ti.overflow) return;
+    m = 0.0f;
+    l = NAN;
+  }
+  if (c < ti.group) {
+    float *dst = parts + (((int64_t)ti.b * a.H + ti.h * ti.group + c) * kDecWaves + wave) * kDecPart;
+    if (g == 0) {
+      dst[0] = m;
+      dst[1] = l;
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[2 + 16 * tt + 4 * g + i] = o[tt][i];
   }
 }
 
@@ -1913,6 +1982,57 @@ SPECDEC_API int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token
   a.out_stride = out_token_stride;
   return launch_attention(a, dtype, batch, width, n_heads, n_kv_heads, head_dim, block_size, max_kv_len,
                           split_tokens, workspace, workspace_floats, stream);
+}
+
+SPECDEC_API int specdec_rope_paged_attention_parts(void *qkv, int64_t token_stride, const float *cos_table,
+                                                   const float *sin_table, const void *hidden, int64_t hidden_dim,
+                                                   float eps, void *k_pool, void *v_pool, const int32_t *tables,
+                                                   int64_t table_stride, const int32_t *meta, int32_t batch,
+                                                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                                   int32_t block_size, float scale, int32_t max_kv_len, float *parts,
+                                                   void *stream) {
+  if (batch < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || block_size <= 0 || max_kv_len < 0)
+    return SPECDEC_EINVAL;
+  if (batch == 0 || max_kv_len == 0) return SPECDEC_OK;
+  if (!qkv || !cos_table || !sin_table || !k_pool || !v_pool || !tables || !meta || !parts) return SPECDEC_EINVAL;
+  if (head_dim != kD || block_size % 16 != 0 || max_kv_len > 2048 || n_heads / n_kv_heads > kRows)
+    return SPECDEC_EUNSUPPORTED;
+  if (hidden && (hidden_dim <= 0 || hidden_dim % 8 != 0 || ((uintptr_t)hidden & 15))) return SPECDEC_EINVAL;
+  if (hidden && hidden_dim > 4 * kWave * 8) return SPECDEC_EUNSUPPORTED;
+  if (token_stride < (int64_t)(n_heads + 2 * n_kv_heads) * kD || token_stride % 8 || ((uintptr_t)qkv & 15))
+    return SPECDEC_EINVAL;
+  const int64_t wgs = (int64_t)batch * n_kv_heads * kDecWaves;
+  if (wgs > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  AttnArgs a{};
+  a.q = qkv;
+  a.q_stride = token_stride;
+  a.rope = 1;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.hidden = hidden;
+  a.hdim = hidden ? (int)hidden_dim : 0;
+  a.eps = eps;
+  a.k = k_pool;
+  a.v = v_pool;
+  a.tables = tables;
+  a.table_stride = table_stride;
+  a.meta = meta;
+  a.scale = scale;
+  a.batch = batch;
+  a.width = 1;
+  a.H = n_heads;
+  a.Hkv = n_kv_heads;
+  a.bs = block_size;
+  a.flat = 1;  // one split over every key
+  a.split = (max_kv_len + 63) / 64 * 64;
+  a.max_splits = 1;
+  a.n_qtiles = 1;
+  a.parts = 1;
+  hipStream_t s = as_stream(stream);
+  const dim3 grid((unsigned)wgs), block(kWave);
+  if (block_size == 16) attention_decode_parts_kernel<1><<<grid, block, 0, s>>>(a, parts);
+  else attention_decode_parts_kernel<2><<<grid, block, 0, s>>>(a, parts);
+  return launch_status();
 }
 
 SPECDEC_API int specdec_paged_attention_static(const void *q, int dtype, int64_t q_token_stride,

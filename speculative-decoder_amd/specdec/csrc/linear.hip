@@ -170,6 +170,130 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
   }
 }
 
+// linear_kernel<1, KB> of the attention rows a draft decode step left as
+// split partials (attention_decode_parts_kernel: kDecWaves per row and query
+// head): each workgroup first folds them into its LDS copy of the rows --
+// per (row, head, 4 dims) the max of the partials' m, then L and O summed
+// in wave order with the same exp2 and fma steps as the attention kernel's
+// own fold, O / L rounded to bf16, so the rows have that kernel's bits --
+// while the weight's first load batch is in flight, then projects them with
+// the plain projection's k-split (x read from LDS instead of memory): the
+// bits of the attention followed by specdec_linear.
+template <int KB>
+__global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs a, const float *parts, int heads) {
+  extern __shared__ __align__(16) uint16_t s_x[];  // [M][K] bf16
+  __shared__ f32x4 s_acc[kLinMaxWaves][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int s_lo = wave * a.per_wave;
+  const int cnt = max(min(a.per_wave, a.steps - s_lo), 0);
+  const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.w), 0, (int)((int64_t)a.N * a.w_stride * 2), 0x00020000);
+  const int row = min(n0 + c, a.N - 1);
+  const unsigned wbase = (unsigned)(((int64_t)row * a.w_stride + 8 * g) * 2);
+  const int f0 = n0 + 4 * g;
+  uint16_t pre[4];
+  {
+    const int obytes = a.accumulate ? (int)(((int64_t)(a.M - 1) * a.out_stride + a.N) * 2) : 0;
+    const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, obytes, 0x00020000);
+    const unsigned obase = (unsigned)(((int64_t)c * a.out_stride + f0) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pre[i] = __builtin_amdgcn_raw_buffer_load_b16(ob, obase + 2u * i, 0, 0);
+  }
+  u32x4 A0[KB], A1[KB];
+  auto issue = [&](u32x4 (&A)[KB], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
+      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * 64u, 0, 0);
+    }
+  };
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int xrow = c * a.K;  // this lane's row of x in LDS (rows past M are zero)
+  auto consume = [&](const u32x4 (&A)[KB], int b) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (b * KB + j < cnt) {
+        const int s = s_lo + b * KB + j;
+        u32x4 bv = u32x4{0u, 0u, 0u, 0u};
+        if (c < a.M) bv = *reinterpret_cast<const u32x4 *>(&s_x[xrow + 32 * s + 8 * g]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[j]), __builtin_bit_cast(bf16x8, bv),
+                                                      acc, 0, 0, 0);
+      }
+  };
+  if (cnt > 0) issue(A0, 0);
+  // ---- the fold: item (row r, head hq, dims d0 .. d0+3)
+  const int items = a.M * heads * 16;
+  for (int it = tid; it < items; it += blockDim.x) {
+    const int r = it / (heads * 16), hq = (it / 16) % heads, d0 = (it % 16) * 4;
+    const float *pp = parts + ((int64_t)r * heads + hq) * kDecWaves * kDecPart;
+    float M = pp[0];
+    for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, pp[w * kDecPart]);
+    float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w = 0; w < kDecWaves; ++w) {
+      const float mw = pp[w * kDecPart];
+      const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      L = __builtin_fmaf(f, pp[w * kDecPart + 1], L);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) O[i] = __builtin_fmaf(f, pp[w * kDecPart + 2 + d0 + i], O[i]);
+    }
+    uint16_t ob[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ob[i] = __builtin_bit_cast(uint16_t, from_f32<__hip_bfloat16>(O[i] / L));
+    *reinterpret_cast<u32x2 *>(&s_x[r * a.K + hq * 64 + d0]) =
+        u32x2{(uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16)};
+  }
+  __syncthreads();
+  if (cnt > 0) {
+    const int nb = (cnt + KB - 1) / KB;
+    int b = 0;
+    for (; b + 2 < nb; b += 2) {
+      issue(A1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(A0, b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b + 1 < nb) {
+      issue(A1, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A0, b);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A1, b + 1);
+    } else {
+      consume(A0, b);
+    }
+  }
+  s_acc[wave][lane] = acc;
+  __syncthreads();
+  // the sums of the waves, in wave order (wave 0 stores), then the value
+  // added before the rounding
+  if (wave == 0 && c < a.M) {
+    f32x4 t = s_acc[0][lane];
+    for (int w = 1; w < nw; ++w) t += s_acc[w][lane];
+    uint16_t *dst = a.out + (int64_t)c * a.out_stride + f0;
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = t[i];
+      if (a.accumulate && f0 + i < a.N) v += bf16_bits_to_f32(pre[i]);
+      o[i] = __builtin_bit_cast(uint16_t, __float2bfloat16(v));
+    }
+    if (f0 + 3 < a.N && ((uintptr_t)dst & 7) == 0) {
+      *reinterpret_cast<u32x2 *>(dst) =
+          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (f0 + i < a.N) dst[i] = o[i];
+    }
+  }
+}
+
 // The gate/up projection with the MLP's activation in its epilogue: a
 // workgroup computes feature tile t of the gate half (W rows 16 t ..) and
 // of the up half (W rows inter + 16 t ..) of the fused [2 inter, K] weight
@@ -353,6 +477,37 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
   if (rows <= 16) linear_kernel<1, 8><<<grid, block, 0, s>>>(a);
   else if (rows <= 32) linear_kernel<2, 4><<<grid, block, 0, s>>>(a);
   else linear_kernel<4, 2><<<grid, block, 0, s>>>(a);
+  return launch_status();
+}
+
+SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, const void *w,
+                                         int64_t w_stride, int64_t out_features, void *out, int64_t out_stride,
+                                         int32_t accumulate, void *stream) {
+  if (rows < 0 || n_heads <= 0 || out_features <= 0) return SPECDEC_EINVAL;
+  if (rows == 0) return SPECDEC_OK;
+  const int64_t k = n_heads * 64;
+  if (rows > 16 || k > 2048) return SPECDEC_EUNSUPPORTED;
+  if (out_features * w_stride * 2 > INT32_MAX || out_features > INT32_MAX / 2) return SPECDEC_EUNSUPPORTED;
+  if (16 * out_stride * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  if (!parts || !w || !out || w_stride < k || out_stride < out_features) return SPECDEC_EINVAL;
+  if (w_stride % 8 || ((uintptr_t)w & 15) || ((uintptr_t)out & 1)) return SPECDEC_EINVAL;
+  LinArgs a{};
+  a.w = (const uint16_t *)w;
+  a.w_stride = w_stride;
+  a.out = (uint16_t *)out;
+  a.out_stride = out_stride;
+  a.M = (int)rows;
+  a.K = (int)k;
+  a.N = (int)out_features;
+  a.steps = (int)(k / 32);
+  a.accumulate = accumulate != 0;
+  const int64_t tiles = (out_features + 15) / 16;
+  if (tiles > INT32_MAX) return SPECDEC_EUNSUPPORTED;
+  int waves = 0;
+  linear_split(a, tiles, waves);  // the plain projection's k-split
+  const dim3 grid((unsigned)tiles), block((unsigned)(64 * waves));
+  const size_t lds = (size_t)rows * k * 2;
+  linear_parts_kernel<8><<<grid, block, lds, as_stream(stream)>>>(a, parts, (int)n_heads);
   return launch_status();
 }
 

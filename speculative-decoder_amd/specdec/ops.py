@@ -617,6 +617,75 @@ def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_k
     return lib().specdec_attention_split(batch, width, n_heads, n_kv_heads, max_kv_len)
 
 
+DECODE_PARTS_MAX_ROWS = 16  # rows of a draft step whose attention goes through split partials
+DECODE_PARTS = 4  # partials per row and query head
+DECODE_PART_FLOATS = 2 + 64  # m, l, O
+
+
+def decode_parts_fit(dtype: torch.dtype, batch: int, width: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                     block_size: int, max_kv_len: int, split_tokens: int) -> bool:
+    """Shapes `rope_paged_attention_parts` + `linear_attn_parts` take: a
+    latency call (split_tokens < 0) of one new bf16 token per row, at most
+    16 rows, head_dim 64, block_size % 16 == 0, at most 2048 cached tokens,
+    at most 16 query heads per kv head and 2048 query features."""
+    return (dtype == torch.bfloat16 and width == 1 and split_tokens < 0 and 0 < batch <= DECODE_PARTS_MAX_ROWS
+            and head_dim == 64 and block_size % 16 == 0 and 0 < max_kv_len <= 2048 and n_kv_heads > 0
+            and n_heads % n_kv_heads == 0 and n_heads // n_kv_heads <= 16 and n_heads * head_dim <= 2048)
+
+
+def decode_parts_buffer(batch: int, n_heads: int, device) -> torch.Tensor:
+    """The fp32 [batch, H, 4, 66] buffer a draft step's attention partials go through."""
+    return torch.empty(batch, n_heads, DECODE_PARTS, DECODE_PART_FLOATS, dtype=torch.float32, device=device)
+
+
+def rope_paged_attention_parts(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, n_heads, n_kv_heads, head_dim,
+                               block_size, scale, max_kv_len, parts: torch.Tensor,
+                               norm_of: torch.Tensor | None = None, eps: float = 0.0) -> torch.Tensor:
+    """A draft-style decode step (rope_paged_attention of one new token per
+    row with split_tokens < 0, the same RoPE, norm and append) whose
+    attention is left as split partials: four one-wave workgroups per (row,
+    kv head), each writing its (m, l, O) to `parts` (`decode_parts_buffer`)
+    instead of folding them in one workgroup.  `linear_attn_parts` folds
+    them into the attention rows (the bits rope_paged_attention produces)
+    and projects them."""
+    dev = gpu(qkv, "qkv").device
+    _qkv_side(dev, qkv, cos, sin, meta, batch, 1, tables, k_pool, v_pool)
+    _on(dev, parts, "parts", torch.float32, True, batch * n_heads * DECODE_PARTS * DECODE_PART_FLOATS)
+    hidden_dim = 0
+    if norm_of is not None:
+        hidden_dim = norm_of.shape[-1]
+        _on(dev, norm_of, "norm_of", qkv.dtype, True, batch * hidden_dim)
+    st = lib().specdec_rope_paged_attention_parts(qkv.data_ptr(), qkv.stride(1), cos.data_ptr(), sin.data_ptr(),
+                                                  ptr(norm_of), hidden_dim, float(eps), k_pool.data_ptr(),
+                                                  v_pool.data_ptr(), tables.data_ptr(), tables.stride(0),
+                                                  meta.data_ptr(), batch, n_heads, n_kv_heads, head_dim, block_size,
+                                                  float(scale), max_kv_len, parts.data_ptr(), stream())
+    _check(st, "rope_paged_attention_parts")
+    return parts
+
+
+def linear_attn_parts(parts: torch.Tensor, rows: int, n_heads: int, w: torch.Tensor, out: torch.Tensor,
+                      accumulate: bool = False) -> torch.Tensor:
+    """`linear(attn, w, out, accumulate)` where attn [rows, H*64] are the
+    attention rows a `rope_paged_attention_parts` call left as partials:
+    each workgroup folds them (the attention-only kernel's arithmetic and
+    order) into LDS and projects them with specdec_linear's k-split, so
+    `out` gets the bits of rope_paged_attention followed by linear."""
+    gpu(w, "w")
+    _on(w.device, parts, "parts", torch.float32, True, rows * n_heads * DECODE_PARTS * DECODE_PART_FLOATS)
+    _on(w.device, out, "out", torch.bfloat16)
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or w.stride(1) != 1 or w.shape[1] != n_heads * 64:
+        raise ValueError(f"w must be a bf16 [N, {n_heads * 64}] tensor with unit inner stride")
+    n = w.shape[0]
+    o2 = out.view(rows, n) if out.dim() != 2 else out
+    if tuple(o2.shape) != (rows, n) or o2.stride(-1) != 1:
+        raise ValueError("out must be bf16 [rows, N] with unit inner stride")
+    st = lib().specdec_linear_attn_parts(parts.data_ptr(), rows, n_heads, w.data_ptr(), w.stride(0), n,
+                                         o2.data_ptr(), o2.stride(0), int(accumulate), stream())
+    _check(st, "linear_attn_parts")
+    return out
+
+
 def latency_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_kv_len: int) -> int:
     """A split for calls whose bits need not match any other call (the draft
     model).  With few (row, head) units: -1, one 16-wave workgroup per unit

@@ -551,6 +551,88 @@ def test_latency_decode_step_matches_oracle(bs, lengths, heads):
     assert (got - want).abs().max().item() < 2e-2
 
 
+def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumulate=True):
+    """A draft-style step (one new token per row, the norm finished inside) on
+    two identical caches: rope_paged_attention (split -1) then linear(attn,
+    wo) on the first; rope_paged_attention_parts then linear_attn_parts on
+    the second.  Returns both outputs and both caches' gathered K/V."""
+    from lm.model import LlamaShape, rope_tables
+
+    d, batch = 64, len(lengths)
+    shape = LlamaShape(vocab_size=8, hidden_size=h * d, num_hidden_layers=1, num_attention_heads=h,
+                       num_key_value_heads=hkv, intermediate_size=8, rope_theta=100000.0)
+    cos, sin = (x.cuda() for x in rope_tables(shape, 2112))
+    g = torch.Generator().manual_seed(seed)
+    hist_k = [torch.randn(hkv, n, d, generator=g).to(torch.bfloat16) for n in lengths]
+    hist_v = [torch.randn(hkv, n, d, generator=g).to(torch.bfloat16) for n in lengths]
+    hidden = torch.randn(batch, 1, hidden_dim, generator=g).to(torch.bfloat16).cuda()
+    qkv = torch.randn(batch, 1, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16).cuda()
+    wo = (torch.randn(hidden_dim, h * d, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    ids = list(range(batch))
+    res = []
+    for which in range(2):
+        cache = make_cache(1, hkv, d, sum(n // bs + 3 for n in lengths) + 8, bs, torch.bfloat16, 11)
+        for s_ in ids:
+            cache.add(s_)
+        step = cache.append(ids, lengths)
+        cache.write(0, step, padded(hist_k, max(lengths)).to(torch.bfloat16).cuda(),
+                    padded(hist_v, max(lengths)).to(torch.bfloat16).cuda())
+        step = cache.append(ids, [1] * batch)
+        kv_max = step.max_total if max_kv_len is None else max_kv_len
+        out = hidden.clone() if accumulate else torch.zeros_like(hidden)
+        if which == 0:
+            attn = torch.zeros(batch, 1, h * d, dtype=torch.bfloat16, device="cuda")
+            ops.rope_paged_attention(qkv.clone(), cos, sin, cache.k[0], cache.v[0], cache.table_tensor, step.meta,
+                                     batch, 1, h, hkv, d, bs, 0.125, kv_max, attn, attn.stride(1), split_tokens=-1,
+                                     norm_of=hidden, eps=1e-5)
+            ops.linear(attn.view(batch, h * d), wo, out=out.view(batch, hidden_dim), accumulate=accumulate)
+        else:
+            parts = ops.decode_parts_buffer(batch, h, "cuda")
+            ops.rope_paged_attention_parts(qkv.clone(), cos, sin, cache.k[0], cache.v[0], cache.table_tensor,
+                                           step.meta, batch, h, hkv, d, bs, 0.125, kv_max, parts, norm_of=hidden,
+                                           eps=1e-5)
+            ops.linear_attn_parts(parts, batch, h, wo, out.view(batch, hidden_dim), accumulate=accumulate)
+        res.append((out, cache.gather(0, step)))
+    return res
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("lengths", [[300], [1], [63], [64], [1000], [2047], [300, 37, 1]])
+@pytest.mark.parametrize("heads,hidden_dim", [((9, 3), 576), ((4, 2), 256), ((8, 1), 512), ((32, 32), 2048)])
+def test_decode_parts_then_projection_equal_attention_then_linear(bs, lengths, heads, hidden_dim):
+    """The draft step through split partials (four one-wave workgroups per
+    kv head, folded by the o_proj launch) has the bits of the attention-only
+    decode kernel followed by specdec_linear: the residual row after o_proj
+    and the pools (the appended token) are equal bit for bit."""
+    (ref, kv_ref), (got, kv_got) = _parts_case(bs, lengths, heads[0], heads[1], hidden_dim, seed=bs + heads[0])
+    assert torch.equal(got, ref)
+    assert torch.equal(kv_got[0], kv_ref[0]) and torch.equal(kv_got[1], kv_ref[1])
+
+
+def test_decode_parts_without_accumulate_equal_plain_projection():
+    (ref, _), (got, _) = _parts_case(16, [300, 5], 9, 3, 576, seed=3, accumulate=False)
+    assert torch.equal(got, ref)
+
+
+def test_decode_parts_rows_beyond_max_kv_len_are_nan():
+    """A row whose cached length exceeds the call's max_kv_len (a broken
+    contract) gets NaN, as from the attention-only kernel."""
+    (ref, _), (got, _) = _parts_case(16, [300], 9, 3, 576, seed=5, max_kv_len=64)
+    assert torch.isnan(ref.float()).all() and torch.isnan(got.float()).all()
+
+
+def test_decode_parts_reject_other_shapes():
+    parts = ops.decode_parts_buffer(17, 9, "cuda")
+    wo = torch.zeros(576, 576, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(17, 576, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(NotImplementedError):  # more than 16 rows
+        ops.linear_attn_parts(parts, 17, 9, wo, out)
+    with pytest.raises(ValueError):  # w of another inner size
+        ops.linear_attn_parts(parts[:1], 1, 9, wo[:, :512], out[:1])
+    assert not ops.decode_parts_fit(torch.bfloat16, 1, 1, 9, 3, 64, 16, 4096, -1)
+    assert not ops.decode_parts_fit(torch.bfloat16, 1, 5, 9, 3, 64, 16, 512, -1)
+
+
 def test_input_norm_in_attention_rejects_other_shapes():
     cache, step, q, _ = _filled(1, [40], 0)
     h = torch.zeros(1, 20, 64, dtype=torch.bfloat16, device="cuda")
