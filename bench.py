@@ -433,36 +433,40 @@ def bench_head():
 def bench_linear():
     """specdec_linear at the decode-sized projections of the e2e models
     (draft SmolLM2-135M: one row; target SmolLM2-1.7B verify: five rows),
-    weights cycled over copies so they come from HBM, against torch (mv for
-    one row, linear otherwise)."""
+    weights cycled over copies so they come from HBM, in the tiled layout the
+    forward reads (and row-major beside it), against torch (mv for one row,
+    linear otherwise)."""
     from specdec import ops
 
     res = {}
     shapes = [("draft_qkv", 1, 576, 960), ("draft_o", 1, 576, 576), ("draft_gate_up", 1, 576, 3072),
               ("draft_down", 1, 1536, 576), ("target_qkv", 5, 2048, 6144), ("target_o", 5, 2048, 2048),
-              ("target_gate_up", 5, 2048, 16384)]
+              ("target_gate_up", 5, 2048, 16384), ("target_down", 5, 8192, 2048)]
     g = torch.Generator(device="cuda").manual_seed(5)
     for name, rows, k, n in shapes:
         copies = min(24, max(2, -(-3 * MALL_BYTES // (k * n * 2))))
         ws = [(torch.randn(n, k, generator=g, device="cuda") * 0.05).to(torch.bfloat16) for _ in range(copies)]
+        wts = [ops.tile_weight(w) for w in ws]
         x = torch.randn(rows, k, generator=g, device="cuda").to(torch.bfloat16)
         out = torch.empty(rows, n, dtype=torch.bfloat16, device="cuda")
         turn = [0]
 
-        def w():
+        def pick(lst):
             turn[0] += 1
-            return ws[turn[0] % copies]
+            return lst[turn[0] % copies]
 
-        us = time_fn(lambda: ops.linear(x, w(), out=out), graph=True)
+        us = time_fn(lambda: ops.linear(x, pick(wts), out=out), graph=True)
+        us_rows = time_fn(lambda: ops.linear(x, pick(ws), out=out), graph=True)
         if rows == 1:
-            us_torch = time_fn(lambda: torch.mv(w(), x.view(-1)), graph=True)
+            us_torch = time_fn(lambda: torch.mv(pick(ws), x.view(-1)), graph=True)
         else:
-            us_torch = time_fn(lambda: torch.nn.functional.linear(x, w()), graph=True)
+            us_torch = time_fn(lambda: torch.nn.functional.linear(x, pick(ws)), graph=True)
         nbytes = n * k * 2 + rows * (k + n) * 2
-        res[f"linear_{name}"] = {"rows": rows, "in": k, "out": n, "us": us, "torch_us": us_torch, "bytes": nbytes,
-                                 "gbs": nbytes / us / 1e3, "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
-        log(f"linear {name}: {us:.2f} us (torch {us_torch:.2f})")
-        del ws
+        res[f"linear_{name}"] = {"rows": rows, "in": k, "out": n, "us": us, "row_major_us": us_rows,
+                                 "torch_us": us_torch, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+                                 "frac_of_peak": nbytes / us / 1e3 / HBM_PEAK_GBS}
+        log(f"linear {name}: {us:.2f} us tiled, {us_rows:.2f} us row-major (torch {us_torch:.2f})")
+        del ws, wts
         torch.cuda.empty_cache()
     return res
 

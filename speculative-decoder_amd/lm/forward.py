@@ -46,43 +46,56 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return ops.add_rmsnorm(x.clone(), None, weight, out, eps)
 
 
-# bf16 projections of at most this many rows and this inner size run on
-# specdec_linear (one pass over the weight with every load in flight; a
-# row's bits do not depend on the other rows); wider inner sizes (the 8192
-# of the 1.7B's down projection) and more rows run on torch's GEMM, which
-# is faster there.  SPECDEC_TORCH_PROJECTIONS=1 (or LINEAR_KERNEL = False
-# before a model's graphs are captured) keeps every projection on torch.
+# bf16 projections of at most this many rows run on specdec_linear (one
+# pass over the weight with every load in flight; a row's bits do not
+# depend on the other rows), reading the weight's tiled copy where the
+# layer has one (any inner size up to 8192) and the row-major weight up to
+# LINEAR_K; more rows (prompts) run on torch's GEMM.  SPECDEC_TORCH_PROJECTIONS=1
+# (or LINEAR_KERNEL = False before a model's graphs are captured) keeps
+# every projection on torch.
 LINEAR_ROWS, LINEAR_K = 16, 2048
 LINEAR_KERNEL = os.environ.get("SPECDEC_TORCH_PROJECTIONS", "0") != "1"
 
 
-def _small(x: torch.Tensor, w: torch.Tensor) -> bool:
+def _linear_weight(x: torch.Tensor, w: torch.Tensor, wt: torch.Tensor | None = None) -> torch.Tensor | None:
+    """The weight specdec_linear reads for x @ w.T (w's tiled copy `wt` when
+    there is one, else w), or None when the call runs on torch.  Both forms
+    give the same bits."""
     k = w.shape[-1]
-    return LINEAR_KERNEL and k <= LINEAR_K and x.numel() <= LINEAR_ROWS * k and ops.linear_fits(x, w)
+    if not LINEAR_KERNEL or x.numel() > LINEAR_ROWS * k:
+        return None
+    if wt is not None and ops.linear_fits(x, wt):
+        return wt
+    if k <= LINEAR_K and ops.linear_fits(x, w):
+        return w
+    return None
 
 
-def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool) -> torch.Tensor:
+def _project(x: torch.Tensor, w: torch.Tensor, gemv: bool, wt: torch.Tensor | None = None) -> torch.Tensor:
     """x @ w.T: specdec_linear for small bf16 calls; else on torch, a
     matrix-vector product when asked for and x is a single row (about a
     microsecond less per call at decode sizes), else the GEMM.  torch's two
     may round differently, so a model uses one of them for every call whose
     bits must agree."""
-    if _small(x, w):
-        return ops.linear(x, w)
+    lw = _linear_weight(x, w, wt)
+    if lw is not None:
+        return ops.linear(x, lw)
     if gemv and x.numel() == x.shape[-1]:
         return torch.mv(w, x.reshape(-1)).view(*x.shape[:-1], w.shape[0])
     return F.linear(x, w)
 
 
-def _project_add(hidden: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemv: bool) -> None:
+def _project_add(hidden: torch.Tensor, x: torch.Tensor, w: torch.Tensor, gemv: bool,
+                 wt: torch.Tensor | None = None) -> None:
     """hidden += x @ w.T inside the projection (specdec_linear's accumulate,
     or torch's GEMM with beta = 1, in place), rounded once: a residual add
     without a kernel of its own.
     A 5-row call's rows have the bits of the same rows projected alone, as
     with `_project`."""
     n, k = w.shape
-    if _small(x, w):
-        ops.linear(x, w, out=hidden.view(-1, n), accumulate=True)
+    lw = _linear_weight(x, w, wt)
+    if lw is not None:
+        ops.linear(x, lw, out=hidden.view(-1, n), accumulate=True)
     elif gemv and x.numel() == k:
         hidden.view(n).addmv_(w, x.reshape(k))
     else:
@@ -122,31 +135,33 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
     # a draft step's attention spread over four CUs per kv head, its partials
     # folded by the o_proj launch (the same bits as attention, then o_proj)
     parts = None
-    if (in_attn and LINEAR_KERNEL and _small(attn, layers[0].wo) and
+    if (in_attn and _linear_weight(attn, layers[0].wo, layers[0].wo_t) is not None and
             ops.decode_parts_fit(hidden.dtype, b, t, h, hk, d, cache.block_size, max_kv_len, split_tokens)):
         parts = ops.decode_parts_buffer(b, h, hidden.device)
     for i, layer in enumerate(layers):
-        qkv = _project(hidden if in_attn else x, layer.wqkv, gemv)
+        qkv = _project(hidden if in_attn else x, layer.wqkv, gemv, layer.wqkv_t)
         if parts is not None:
             ops.rope_paged_attention_parts(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta,
                                            b, h, hk, d, cache.block_size, llama.scaling, max_kv_len, parts,
                                            norm_of=hidden, eps=eps)
-            ops.linear_attn_parts(parts, b, h, layer.wo, hidden.view(b, -1), accumulate=True)
+            ops.linear_attn_parts(parts, b, h, _linear_weight(attn, layer.wo, layer.wo_t), hidden.view(b, -1),
+                                  accumulate=True)
         else:
             ops.rope_paged_attention(qkv, llama.rope_cos, llama.rope_sin, cache.k[i], cache.v[i], tables, meta, b, t,
                                      h, hk, d, cache.block_size, llama.scaling, max_kv_len, attn, attn.stride(1),
                                      workspace, split_tokens, norm_of=hidden if in_attn else None, eps=eps)
-            _project_add(hidden, attn, layer.wo, gemv)
-        if _small(hidden, layer.wgu):  # gate/up and the MLP's norm + activation in one launch
-            ops.linear_silu(hidden, layer.wgu, hidden, act, eps)
+            _project_add(hidden, attn, layer.wo, gemv, layer.wo_t)
+        gw = _linear_weight(hidden, layer.wgu, layer.wgu_t)
+        if gw is not None:  # gate/up and the MLP's norm + activation in one launch
+            ops.linear_silu(hidden, gw, hidden, act, eps)
         else:
             ops.rms_silu_mul(_project(hidden, layer.wgu, gemv), hidden, act, eps)
         if i + 1 == len(layers):
-            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.norm, x, eps)
+            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv, layer.wd_t), llama.norm, x, eps)
         elif in_attn:
-            _project_add(hidden, act, layer.wd, gemv)
+            _project_add(hidden, act, layer.wd, gemv, layer.wd_t)
         else:
-            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv), llama.unit_norm, x, eps)
+            ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv, layer.wd_t), llama.unit_norm, x, eps)
     if last is not None:
         x = x[torch.arange(b, device=x.device), last]
     if temperature is None:

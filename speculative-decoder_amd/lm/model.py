@@ -17,6 +17,8 @@ from dataclasses import dataclass, field
 
 import torch
 
+from specdec import ops
+
 
 @dataclass(frozen=True)
 class LlamaShape:
@@ -118,6 +120,22 @@ class Layer:
     ln2: torch.Tensor
     wgu: torch.Tensor  # gate/up [2 * intermediate, hidden], ln2 folded in
     wd: torch.Tensor
+    # the same four in the decode-sized projections' tiled layout
+    # (ops.tile_weight: the same bits, contiguous loads), made for bf16
+    # weights on the GPU; None otherwise (prompt-sized GEMMs read the above)
+    wqkv_t: torch.Tensor | None = field(default=None, repr=False)
+    wo_t: torch.Tensor | None = field(default=None, repr=False)
+    wgu_t: torch.Tensor | None = field(default=None, repr=False)
+    wd_t: torch.Tensor | None = field(default=None, repr=False)
+
+    def __post_init__(self):
+        def tiled(w: torch.Tensor) -> torch.Tensor | None:
+            if not (w.is_cuda and w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[0] % 16 == 0
+                    and w.shape[1] % 32 == 0):
+                return None
+            return ops.tile_weight(w)
+        if self.wqkv_t is None:
+            self.wqkv_t, self.wo_t, self.wgu_t, self.wd_t = (tiled(w) for w in (self.wqkv, self.wo, self.wgu, self.wd))
 
 
 def fold_norm(w: torch.Tensor, ln: torch.Tensor) -> torch.Tensor:

@@ -49,9 +49,29 @@ struct LinArgs {
   int steps;     // K / 32
   int per_wave;  // k-steps per wave (the last waves may take fewer or none)
   int accumulate;
+  int w_tiled;  // W in the tiled layout (w_lane below), w_stride = K
 };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// The byte offset in W of lane (c = lane % 16, g = lane / 16)'s 16 bytes at
+// k-step 0 of feature row `row` (row c of feature tile `tile`), and the
+// bytes from one k-step to the next.  Row-major W [N, w_stride]: row `row`,
+// k 8g .. 8g+7.  Tiled W (N % 16 == 0): the 16 x 32 block of each (tile,
+// k-step) is 1 KB contiguous in lane order, block (t, s) at (t * K/32 + s) KB,
+// lane (c, g) holding row 16t + c, k 32s + 8g .. 32s + 8g + 7 -- every
+// load instruction of a wave reads one contiguous KB instead of 64 bytes
+// from each of 16 rows.
+__device__ __forceinline__ void w_lane(const LinArgs &a, int tile, int row, int lane, unsigned &base,
+                                       unsigned &step) {
+  if (a.w_tiled) {
+    base = (unsigned)(((int64_t)tile * a.steps * 64 + lane) * 16);
+    step = 1024u;
+  } else {
+    base = (unsigned)(((int64_t)row * a.w_stride + 8 * (lane >> 4)) * 2);
+    step = 64u;
+  }
+}
 
 // NCT 16-row column tiles of x per wave (each W load feeds NCT MFMAs),
 // KB k-steps per load batch (8 / NCT: the same registers for every NCT).
@@ -69,7 +89,8 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
   const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(a.x), 0, (int)(((int64_t)(a.M - 1) * a.x_stride + a.K) * 2), 0x00020000);
   const int row = min(n0 + c, a.N - 1);
-  const unsigned wbase = (unsigned)(((int64_t)row * a.w_stride + 8 * g) * 2);
+  unsigned wbase, wstep;
+  w_lane(a, blockIdx.x, row, lane, wbase, wstep);
   const unsigned xbase = (unsigned)(((int64_t)c * a.x_stride + 8 * g) * 2);
   const unsigned xtile = (unsigned)(16 * a.x_stride * 2);  // bytes between column tiles
   // accumulate: the values added before the rounding, loaded now for the
@@ -100,7 +121,7 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
-      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * 64u, 0, 0);
+      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * wstep, 0, 0);
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct)
         B[j][ct] = __builtin_amdgcn_raw_buffer_load_b128(xb, xbase + ct * xtile + s * 64u, 0, 0);
@@ -191,7 +212,8 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs
   const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(a.w), 0, (int)((int64_t)a.N * a.w_stride * 2), 0x00020000);
   const int row = min(n0 + c, a.N - 1);
-  const unsigned wbase = (unsigned)(((int64_t)row * a.w_stride + 8 * g) * 2);
+  unsigned wbase, wstep;
+  w_lane(a, blockIdx.x, row, lane, wbase, wstep);
   const int f0 = n0 + 4 * g;
   uint16_t pre[4];
   {
@@ -206,7 +228,7 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
-      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * 64u, 0, 0);
+      A[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, wbase + s * wstep, 0, 0);
     }
   };
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -320,8 +342,9 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_silu_kernel(LinArgs 
   const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(a.x), 0, (int)(((int64_t)(a.M - 1) * a.x_stride + a.K) * 2), 0x00020000);
   const int rg = min(n0 + c, inter - 1);  // past the gate half: its last row, never stored
-  const unsigned gbase = (unsigned)(((int64_t)rg * a.w_stride + 8 * g) * 2);
-  const unsigned ubase = (unsigned)(((int64_t)(inter + rg) * a.w_stride + 8 * g) * 2);
+  unsigned gbase, ubase, wstep;
+  w_lane(a, blockIdx.x, rg, lane, gbase, wstep);
+  w_lane(a, inter / 16 + blockIdx.x, inter + rg, lane, ubase, wstep);
   const unsigned xbase = (unsigned)(((int64_t)c * a.x_stride + 8 * g) * 2);
   const unsigned xtile = (unsigned)(16 * a.x_stride * 2);
   // the first pass over this wave's first residual row (row `wave`), loaded
@@ -338,8 +361,8 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_silu_kernel(LinArgs 
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       const unsigned s = (unsigned)(s_lo + min(b * KB + j, cnt - 1));
-      G[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, gbase + s * 64u, 0, 0);
-      U[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, ubase + s * 64u, 0, 0);
+      G[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, gbase + s * wstep, 0, 0);
+      U[j] = __builtin_amdgcn_raw_buffer_load_b128(wb, ubase + s * wstep, 0, 0);
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct)
         B[j][ct] = __builtin_amdgcn_raw_buffer_load_b128(xb, xbase + ct * xtile + s * 64u, 0, 0);
@@ -443,10 +466,15 @@ static void linear_split(LinArgs &a, int64_t tiles, int &waves) {
 
 using namespace specdec;
 
-SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_stride, int64_t rows,
-                               int64_t in_features, int64_t out_features, void *out, int64_t out_stride,
-                               int32_t accumulate, void *stream) {
+SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_stride, int32_t w_layout,
+                               int64_t rows, int64_t in_features, int64_t out_features, void *out,
+                               int64_t out_stride, int32_t accumulate, void *stream) {
   if (rows < 0 || in_features <= 0 || out_features <= 0) return SPECDEC_EINVAL;
+  if (w_layout != SPECDEC_W_ROWS && w_layout != SPECDEC_W_TILED) return SPECDEC_EINVAL;
+  if (w_layout == SPECDEC_W_TILED) {
+    if (out_features % 16 != 0) return SPECDEC_EINVAL;
+    w_stride = in_features;
+  }
   if (rows == 0) return SPECDEC_OK;
   if (rows > kLinRows || in_features % 32 != 0 || in_features / 32 > kLinMaxSteps) return SPECDEC_EUNSUPPORTED;
   // one buffer resource addresses W, another the rows of x (32-bit offsets)
@@ -468,6 +496,7 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
   a.N = (int)out_features;
   a.steps = (int)(in_features / 32);
   a.accumulate = accumulate != 0;
+  a.w_tiled = w_layout == SPECDEC_W_TILED;
   const int64_t tiles = (out_features + 15) / 16;
   if (tiles > INT32_MAX) return SPECDEC_EUNSUPPORTED;
   int waves = 0;
@@ -481,11 +510,16 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
 }
 
 SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, const void *w,
-                                         int64_t w_stride, int64_t out_features, void *out, int64_t out_stride,
-                                         int32_t accumulate, void *stream) {
+                                         int64_t w_stride, int32_t w_layout, int64_t out_features, void *out,
+                                         int64_t out_stride, int32_t accumulate, void *stream) {
   if (rows < 0 || n_heads <= 0 || out_features <= 0) return SPECDEC_EINVAL;
+  if (w_layout != SPECDEC_W_ROWS && w_layout != SPECDEC_W_TILED) return SPECDEC_EINVAL;
   if (rows == 0) return SPECDEC_OK;
   const int64_t k = n_heads * 64;
+  if (w_layout == SPECDEC_W_TILED) {
+    if (out_features % 16 != 0) return SPECDEC_EINVAL;
+    w_stride = k;
+  }
   if (rows > 16 || k > 2048) return SPECDEC_EUNSUPPORTED;
   if (out_features * w_stride * 2 > INT32_MAX || out_features > INT32_MAX / 2) return SPECDEC_EUNSUPPORTED;
   if (16 * out_stride * 2 > INT32_MAX) return SPECDEC_EUNSUPPORTED;
@@ -501,6 +535,7 @@ SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int6
   a.N = (int)out_features;
   a.steps = (int)(k / 32);
   a.accumulate = accumulate != 0;
+  a.w_tiled = w_layout == SPECDEC_W_TILED;
   const int64_t tiles = (out_features + 15) / 16;
   if (tiles > INT32_MAX) return SPECDEC_EUNSUPPORTED;
   int waves = 0;
@@ -511,10 +546,16 @@ SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int6
   return launch_status();
 }
 
-SPECDEC_API int specdec_linear_silu(const void *x, int64_t x_stride, const void *w, int64_t w_stride, int64_t rows,
-                                    int64_t in_features, int64_t inter, const void *hidden, int64_t hidden_stride,
-                                    int64_t hidden_dim, float eps, void *out, int64_t out_stride, void *stream) {
+SPECDEC_API int specdec_linear_silu(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                                    int32_t w_layout, int64_t rows, int64_t in_features, int64_t inter,
+                                    const void *hidden, int64_t hidden_stride, int64_t hidden_dim, float eps,
+                                    void *out, int64_t out_stride, void *stream) {
   if (rows < 0 || in_features <= 0 || inter <= 0 || hidden_dim <= 0) return SPECDEC_EINVAL;
+  if (w_layout != SPECDEC_W_ROWS && w_layout != SPECDEC_W_TILED) return SPECDEC_EINVAL;
+  if (w_layout == SPECDEC_W_TILED) {
+    if (inter % 16 != 0) return SPECDEC_EINVAL;
+    w_stride = in_features;
+  }
   if (rows == 0) return SPECDEC_OK;
   if (rows > kLinRows || in_features % 32 != 0 || in_features / 32 > kLinMaxSteps) return SPECDEC_EUNSUPPORTED;
   if (hidden_dim % 8 != 0 || hidden_dim > 8 * 64 * 8) return SPECDEC_EUNSUPPORTED;
@@ -538,6 +579,7 @@ SPECDEC_API int specdec_linear_silu(const void *x, int64_t x_stride, const void 
   a.K = (int)in_features;
   a.N = (int)n;
   a.steps = (int)(in_features / 32);
+  a.w_tiled = w_layout == SPECDEC_W_TILED;
   // the plain projection's k-split for this [2 inter, K] weight
   int waves = 0;
   linear_split(a, (n + 15) / 16, waves);

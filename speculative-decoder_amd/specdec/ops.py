@@ -272,26 +272,51 @@ def _rows_out(out: torch.Tensor | None, rows: int, v: int, dev: torch.device, na
 
 
 LINEAR_ROWS = 64  # rows of a specdec_linear call, at most
+W_ROWS, W_TILED = 0, 1  # weight layouts of the linear entries
+
+
+def tile_weight(w: torch.Tensor) -> torch.Tensor:
+    """W [N, K] (N % 16 == 0, K % 32 == 0) in the tiled layout, as
+    [N/16, K/32, 4, 16, 8]: the 16 x 32 block of feature tile t and k-step
+    s is 1 KB contiguous, lane (c, g) of a wave holding row 16t + c at
+    k = 32s + 8g .. 32s + 8g + 7, so each load instruction of the linear
+    kernels reads one contiguous KB.  The projection's bits are the same as
+    with W itself.  Made once per weight; prompt-sized GEMMs keep W."""
+    n, k = w.shape
+    if n % 16 or k % 32:
+        raise ValueError(f"a tiled weight needs N % 16 == 0 and K % 32 == 0 (got {n} x {k})")
+    return w.reshape(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+
+
+def _weight(w: torch.Tensor) -> tuple[int, int, int]:
+    """(N, K, layout) of a linear weight: W [N, K] row-major (contiguous) or
+    its `tile_weight` form."""
+    if w.dim() == 5 and tuple(w.shape[2:]) == (4, 16, 8) and w.is_contiguous():
+        return w.shape[0] * 16, w.shape[1] * 32, W_TILED
+    if w.dim() == 2 and w.is_contiguous():
+        return w.shape[0], w.shape[1], W_ROWS
+    raise ValueError("w must be a contiguous [N, K] tensor or a tile_weight() result")
 
 
 def linear_fits(x: torch.Tensor, w: torch.Tensor) -> bool:
     """Whether `linear` takes x @ w.T: bf16, at most LINEAR_ROWS rows, the
-    inner size a multiple of 32 up to 8192, a contiguous weight."""
-    k = w.shape[-1]
-    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_contiguous()
-            and k % 32 == 0 and k <= 8192 and x.numel() // k <= LINEAR_ROWS and x.is_cuda)
+    inner size a multiple of 32 up to 8192, a contiguous (or tiled) weight."""
+    if w.dtype != torch.bfloat16 or not (w.dim() == 2 and w.is_contiguous() or w.dim() == 5):
+        return False
+    k = _weight(w)[1]
+    return x.dtype == torch.bfloat16 and k % 32 == 0 and k <= 8192 and x.numel() // k <= LINEAR_ROWS and x.is_cuda
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
-    """x [..., K] bf16 times w [N, K] bf16 transposed, accumulated in fp32
-    and rounded once: bf16 [..., N].  With `accumulate`, out += x @ w.T
-    inside that rounding.  A row's result does not depend on the other rows
-    of the call."""
+    """x [..., K] bf16 times w [N, K] bf16 (or its `tile_weight` form)
+    transposed, accumulated in fp32 and rounded once: bf16 [..., N].  With
+    `accumulate`, out += x @ w.T inside that rounding.  A row's result does
+    not depend on the other rows of the call."""
     gpu(w, "w")
     _on(w.device, x, "x", torch.bfloat16)
-    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous():
-        raise ValueError("w must be a contiguous bf16 [N, K] tensor")
-    n, k = w.shape
+    if w.dtype != torch.bfloat16:
+        raise ValueError("w must be bf16")
+    n, k, layout = _weight(w)
     if x.shape[-1] != k:
         raise ValueError(f"x rows have {x.shape[-1]} features, w {k}")
     x2 = x.reshape(-1, k)
@@ -307,7 +332,8 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, ac
         o2 = out.view(rows, n) if out.dim() != 2 else out
         if tuple(o2.shape) != (rows, n) or o2.stride(-1) != 1:
             raise ValueError("out must be bf16 [rows, N] with unit inner stride")
-    st = lib().specdec_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, rows, k, n, o2.data_ptr(), o2.stride(0),
+    st = lib().specdec_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, layout, rows, k, n, o2.data_ptr(),
+                              o2.stride(0),
                               int(accumulate), stream())
     _check(st, "linear")
     return o2.view(*x.shape[:-1], n) if out is None else out
@@ -315,14 +341,15 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, ac
 
 def linear_silu(x: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor, out: torch.Tensor, eps: float) -> torch.Tensor:
     """rms_silu_mul(linear(x, w), hidden, out, eps) in one launch, with the
-    same bits: w is the fused [2 I, K] gate/up weight, out bf16 [..., I]."""
+    same bits: w is the fused [2 I, K] gate/up weight (or its `tile_weight`
+    form), out bf16 [..., I]."""
     gpu(w, "w")
     _on(w.device, x, "x", torch.bfloat16)
     _on(w.device, hidden, "hidden", torch.bfloat16)
     _on(w.device, out, "out", torch.bfloat16)
-    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_contiguous() or w.shape[0] % 2:
-        raise ValueError("w must be a contiguous bf16 [2 I, K] tensor")
-    n2, k = w.shape
+    n2, k, layout = _weight(w)
+    if w.dtype != torch.bfloat16 or n2 % 2:
+        raise ValueError("w must be a bf16 [2 I, K] tensor")
     inter = n2 // 2
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
@@ -334,7 +361,7 @@ def linear_silu(x: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor, out: tor
     o2 = out.view(rows, inter) if out.dim() != 2 else out
     if tuple(o2.shape) != (rows, inter) or o2.stride(-1) != 1:
         raise ValueError("out must be bf16 [rows, I] with unit inner stride")
-    st = lib().specdec_linear_silu(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, rows, k, inter, h2.data_ptr(),
+    st = lib().specdec_linear_silu(x2.data_ptr(), x2.stride(0), w.data_ptr(), k, layout, rows, k, inter, h2.data_ptr(),
                                    h2.stride(0), h2.shape[1], float(eps), o2.data_ptr(), o2.stride(0), stream())
     _check(st, "linear_silu")
     return out
@@ -674,13 +701,17 @@ def linear_attn_parts(parts: torch.Tensor, rows: int, n_heads: int, w: torch.Ten
     gpu(w, "w")
     _on(w.device, parts, "parts", torch.float32, True, rows * n_heads * DECODE_PARTS * DECODE_PART_FLOATS)
     _on(w.device, out, "out", torch.bfloat16)
-    if w.dtype != torch.bfloat16 or w.dim() != 2 or w.stride(1) != 1 or w.shape[1] != n_heads * 64:
-        raise ValueError(f"w must be a bf16 [N, {n_heads * 64}] tensor with unit inner stride")
-    n = w.shape[0]
+    if w.dim() == 2 and w.stride(1) == 1:
+        n, k, layout, w_stride = w.shape[0], w.shape[1], W_ROWS, w.stride(0)
+    else:
+        n, k, layout = _weight(w)
+        w_stride = k
+    if w.dtype != torch.bfloat16 or k != n_heads * 64:
+        raise ValueError(f"w must be bf16 [N, {n_heads * 64}] (unit inner stride) or its tile_weight form")
     o2 = out.view(rows, n) if out.dim() != 2 else out
     if tuple(o2.shape) != (rows, n) or o2.stride(-1) != 1:
         raise ValueError("out must be bf16 [rows, N] with unit inner stride")
-    st = lib().specdec_linear_attn_parts(parts.data_ptr(), rows, n_heads, w.data_ptr(), w.stride(0), n,
+    st = lib().specdec_linear_attn_parts(parts.data_ptr(), rows, n_heads, w.data_ptr(), w_stride, layout, n,
                                          o2.data_ptr(), o2.stride(0), int(accumulate), stream())
     _check(st, "linear_attn_parts")
     return out

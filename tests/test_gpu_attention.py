@@ -551,11 +551,12 @@ def test_latency_decode_step_matches_oracle(bs, lengths, heads):
     assert (got - want).abs().max().item() < 2e-2
 
 
-def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumulate=True):
+def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumulate=True, tiled=True):
     """A draft-style step (one new token per row, the norm finished inside) on
     two identical caches: rope_paged_attention (split -1) then linear(attn,
     wo) on the first; rope_paged_attention_parts then linear_attn_parts on
-    the second.  Returns both outputs and both caches' gathered K/V."""
+    the second (reading o_proj's weight in its tiled layout unless `tiled`
+    is false).  Returns both outputs and both caches' gathered K/V."""
     from lm.model import LlamaShape, rope_tables
 
     d, batch = 64, len(lengths)
@@ -591,7 +592,8 @@ def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumula
             ops.rope_paged_attention_parts(qkv.clone(), cos, sin, cache.k[0], cache.v[0], cache.table_tensor,
                                            step.meta, batch, h, hkv, d, bs, 0.125, kv_max, parts, norm_of=hidden,
                                            eps=1e-5)
-            ops.linear_attn_parts(parts, batch, h, wo, out.view(batch, hidden_dim), accumulate=accumulate)
+            ops.linear_attn_parts(parts, batch, h, ops.tile_weight(wo) if tiled else wo, out.view(batch, hidden_dim),
+                                  accumulate=accumulate)
         res.append((out, cache.gather(0, step)))
     return res
 
@@ -611,6 +613,12 @@ def test_decode_parts_then_projection_equal_attention_then_linear(bs, lengths, h
 
 def test_decode_parts_without_accumulate_equal_plain_projection():
     (ref, _), (got, _) = _parts_case(16, [300, 5], 9, 3, 576, seed=3, accumulate=False)
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("heads,hidden_dim", [((9, 3), 576), ((32, 32), 2048)])
+def test_decode_parts_with_row_major_weight(heads, hidden_dim):
+    (ref, _), (got, _) = _parts_case(16, [300, 37], heads[0], heads[1], hidden_dim, seed=4, tiled=False)
     assert torch.equal(got, ref)
 
 

@@ -150,3 +150,33 @@ def test_linear_silu_equals_linear_then_rms_silu_mul(rows, k, inter, hdim, same)
     up = (s * gu[:, inter:]).to(torch.bfloat16).float()
     want = (torch.nn.functional.silu(gate).to(torch.bfloat16).float() * up).to(torch.bfloat16)
     assert (fused.cpu().float() - want.float()).abs().max().item() <= 2 ** -6 * want.float().abs().max().item()
+
+
+@pytest.mark.parametrize("rows,k,n", [(1, 576, 960), (1, 1536, 576), (5, 2048, 6144), (5, 8192, 2048), (16, 96, 48),
+                                      (40, 576, 1008), (64, 8192, 48)])
+def test_tiled_weight_gives_the_same_bits(rows, k, n):
+    """The weight in its tiled layout (each 16 x 32 block 1 KB contiguous in
+    the lanes' order) is the same arithmetic as the row-major weight: plain
+    and accumulating projections are equal bit for bit, at every row count
+    and instance."""
+    x, w = operands(rows, k, n, seed=rows + k + n)
+    xd, wd = x.to(DEV), w.to(DEV)
+    wt = ops.tile_weight(wd)
+    assert torch.equal(ops.linear(xd, wt), ops.linear(xd, wd))
+    base = (torch.randn(rows, n, generator=torch.Generator().manual_seed(n)) * 2).to(torch.bfloat16).to(DEV)
+    a, b = base.clone(), base.clone()
+    ops.linear(xd, wd, out=a, accumulate=True)
+    ops.linear(xd, wt, out=b, accumulate=True)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rows,k,inter", [(1, 576, 1536), (5, 2048, 8192), (40, 576, 1536)])
+def test_linear_silu_tiled_weight_gives_the_same_bits(rows, k, inter):
+    g = torch.Generator().manual_seed(rows + inter)
+    w = (torch.randn(2 * inter, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    hidden = (torch.randn(rows, k, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    a = torch.empty(rows, inter, dtype=torch.bfloat16, device=DEV)
+    b = torch.empty_like(a)
+    ops.linear_silu(hidden, w, hidden, a, 1e-5)
+    ops.linear_silu(hidden, ops.tile_weight(w), hidden, b, 1e-5)
+    assert torch.equal(a, b)

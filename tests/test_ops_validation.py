@@ -45,3 +45,17 @@ def test_checker_names_device_dtype_and_size():
         ops._on(t.device, torch.zeros(4, 4)[:, 0], "t", contiguous=True)
     with pytest.raises(RuntimeError, match="must be on"):
         ops._on(torch.device("meta"), t, "t")
+
+
+def test_tile_weight_layout():
+    """ops.tile_weight puts W[n, k] at ((n // 16 * (K // 32) + k // 32) * 64
+    + (k % 32) // 8 * 16 + n % 16) * 8 + k % 8, the layout the C ABI documents
+    (SPECDEC_W_TILED): every element checked by its index."""
+    n, k = 48, 96
+    w = torch.arange(n * k, dtype=torch.float32).reshape(n, k)
+    flat = ops.tile_weight(w).reshape(-1)
+    nn, kk = torch.meshgrid(torch.arange(n), torch.arange(k), indexing="ij")
+    pos = ((nn // 16 * (k // 32) + kk // 32) * 64 + (kk % 32) // 8 * 16 + nn % 16) * 8 + kk % 8
+    assert torch.equal(flat[pos.reshape(-1)], w.reshape(-1))
+    with pytest.raises(ValueError):
+        ops.tile_weight(torch.zeros(40, 96))
