@@ -332,14 +332,15 @@ int specdec_rope_paged_attention(void *qkv, int dtype, int64_t token_stride,
 
 /* A latency decode step (specdec_rope_paged_attention with width 1,
  * split_tokens < 0: the same norm, RoPE and append) whose attention is left
- * as split partials for the output projection to fold: four one-wave
- * workgroups per (row, kv head), on four compute units, workgroup w taking
- * the 64-token steps w, w+4, ... of the keys and writing its (m, l, O) -- the
- * running max in log2 units, the sum of 2^(s - m) and O = sum 2^(s - m) v,
- * not divided -- for each query head of the kv head to parts [batch,
- * n_heads, 4, 66] fp32 (m, l, then O's 64 dims).  Folding a row's four
- * partials in order (specdec_linear_attn_parts) gives the bits
- * specdec_rope_paged_attention writes.  A row whose cached length exceeds
+ * as split partials for the output projection to fold: nparts (4, 8 or 16)
+ * one-wave workgroups per (row, kv head), on as many compute units,
+ * workgroup w taking the 64-token steps w, w + nparts, ... of the keys and
+ * writing its (m, l, O) -- the running max in log2 units, the sum of
+ * 2^(s - m) and O = sum 2^(s - m) v, not divided -- for each query head of
+ * the kv head to parts [batch, n_heads, nparts, 68] fp32 (m, l, two unused,
+ * then O's 64 dims; 16-byte aligned).  Folding a row's partials in order (specdec_linear_attn_parts)
+ * gives, with nparts = 4, the bits specdec_rope_paged_attention writes
+ * (with more parts, the same attention folded in another order).  A row whose cached length exceeds
  * max_kv_len gets partials that fold to NaN.  Needs head_dim 64, block_size
  * % 16 == 0, max_kv_len <= 2048, n_heads / n_kv_heads <= 16 and hidden_dim
  * <= 2048 (else SPECDEC_EUNSUPPORTED); qkv and hidden 16-byte aligned.
@@ -351,7 +352,7 @@ int specdec_rope_paged_attention_parts(void *qkv, int64_t token_stride, const fl
                                        int64_t table_stride, const int32_t *meta, int32_t batch,
                                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                        int32_t block_size, float scale, int32_t max_kv_len,
-                                       float *parts, void *stream);
+                                       int32_t nparts, float *parts, void *stream);
 
 /* ---------------------------------------------------------------- linear --- */
 
@@ -372,16 +373,19 @@ int specdec_linear(const void *x, int64_t x_stride, const void *w, int64_t w_str
 
 /* specdec_linear of the attention rows a specdec_rope_paged_attention_parts
  * call left as partials: out [rows, out_features] (+)= attn w^T, with attn
- * [rows, n_heads * 64] folded from parts [rows, n_heads, 4, 66] by each
- * workgroup in its prologue (the attention kernel's own fold, so attn has
- * specdec_rope_paged_attention's bits) and w [out_features, n_heads * 64]
- * bf16.  The k-split is specdec_linear's for that weight, so out has the
+ * [rows, n_heads * 64] folded from parts [rows, n_heads, nparts, 68] by
+ * each workgroup in its prologue (the attention kernel's own fold order, so
+ * with 4 parts attn has specdec_rope_paged_attention's bits) and w
+ * [out_features, n_heads * 64] bf16 (w_layout as for specdec_linear).  With
+ * attn_out not null the folded rows are written there too (bf16 [rows,
+ * n_heads * 64], 8-byte aligned).  The k-split is specdec_linear's for that weight, so out has the
  * bits of specdec_rope_paged_attention followed by specdec_linear.
  * rows <= 16, n_heads * 64 <= 2048 (else SPECDEC_EUNSUPPORTED).  Replaces
  * lm/forward.py:60-63 (o_proj and the residual add) for the draft's steps. */
-int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, const void *w,
-                              int64_t w_stride, int32_t w_layout, int64_t out_features, void *out, int64_t out_stride,
-                              int32_t accumulate, void *stream);
+int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, int32_t nparts,
+                              const void *w, int64_t w_stride, int32_t w_layout, int64_t out_features,
+                              void *out, int64_t out_stride, int32_t accumulate, void *attn_out,
+                              void *stream);
 
 /* specdec_linear of x and the fused gate/up weight w [2*inter, in_features]
  * followed by specdec_rms_silu_mul, in one launch: out [rows, inter] bf16 =

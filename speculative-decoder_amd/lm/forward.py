@@ -12,7 +12,7 @@ A forward is split in two:
         token's q/k/v scaled by its row's rsqrt(mean(x^2) + eps)), applies
         RoPE, appends the new K/V to the paged pools and reads K/V blocks in
         place (no gather copy, no materialised mask) -- for a draft step,
-        as split partials over four CUs per kv head;
+        as split partials over up to 16 CUs per kv head;
       - o_proj accumulated into the residual stream by the projection itself
         (folding the draft step's partials first);
       - gate/up of the unnormalised stream with the post-attention norm and
@@ -132,12 +132,12 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
         ops.add_rmsnorm(hidden, None, llama.unit_norm, x, eps)
     attn = torch.empty(b, t, h * d, dtype=hidden.dtype, device=hidden.device)
     act = torch.empty(b, t, inter, dtype=hidden.dtype, device=hidden.device)
-    # a draft step's attention spread over four CUs per kv head, its partials
-    # folded by the o_proj launch (the same bits as attention, then o_proj)
+    # a draft step's attention spread over a CU per 64 keys of each kv head
+    # (4 to 16), its partials folded by the o_proj launch
     parts = None
     if (in_attn and _linear_weight(attn, layers[0].wo, layers[0].wo_t) is not None and
             ops.decode_parts_fit(hidden.dtype, b, t, h, hk, d, cache.block_size, max_kv_len, split_tokens)):
-        parts = ops.decode_parts_buffer(b, h, hidden.device)
+        parts = ops.decode_parts_buffer(b, h, hidden.device, ops.decode_parts_count(max_kv_len))
     for i, layer in enumerate(layers):
         qkv = _project(hidden if in_attn else x, layer.wqkv, gemv, layer.wqkv_t)
         if parts is not None:

@@ -39,8 +39,8 @@ SIGNATURES: dict[str, list] = {
     "specdec_rope_paged_attention": [P, c_int, I64, P, P, P, I64, c_float, P, P, P, I64, P, I32, I32, I32, I32, I32,
                                      I32, c_float, I32, I32, P, I64, P, I64, P],
     "specdec_rope_paged_attention_parts": [P, I64, P, P, P, I64, c_float, P, P, P, I64, P, I32, I32, I32, I32, I32,
-                                           c_float, I32, P, P],
-    "specdec_linear_attn_parts": [P, I64, I64, P, I64, I32, I64, P, I64, I32, P],
+                                           c_float, I32, I32, P, P],
+    "specdec_linear_attn_parts": [P, I64, I64, I32, P, I64, I32, I64, P, I64, I32, P, P],
     "specdec_head_workspace": [P],
     "specdec_head_logits": [P, I64, P, I64, I64, I64, I64, P, I64, P],
     "specdec_linear": [P, I64, P, I64, I32, I64, I64, I64, P, I64, I32, P],
@@ -53,7 +53,7 @@ SIGNATURES: dict[str, list] = {
 # fp32 split partials the library holds per GPU for specdec_paged_attention_static
 STATIC_PARTIAL_FLOATS = 2 * 1024 * 1024
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 _lib: ctypes.CDLL | None = None
 
 

@@ -861,7 +861,7 @@ __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64
 
 using namespace specdec;
 
-SPECDEC_API int specdec_abi_version(void) { return 13; }
+SPECDEC_API int specdec_abi_version(void) { return 14; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,

@@ -1082,11 +1082,12 @@ __device__ __forceinline__ void decode_early(const AttnArgs &a, const TileInfo &
   if (a.hidden) row_pass_loads<4>(e.hr, 0, nvh, lane, e.hv);
 }
 
-// Wave w (of kDecWaves) of kv head ti.h, row metadata read: its (m, l, O)
-// over its steps.  `writer`: this wave writes the new token's K and V to the
-// pools (one wave per (row, kv head) of the launch).
+// Wave w (of nwaves) of kv head ti.h, row metadata read: its (m, l, O)
+// over the 64-token steps w, w + nwaves, ...  `writer`: this wave writes the
+// new token's K and V to the pools (one wave per (row, kv head) of the
+// launch).
 template <int MODE>
-__device__ __forceinline__ void decode_wave(const AttnArgs &a, const TileInfo &ti, int wave, bool writer,
+__device__ __forceinline__ void decode_wave(const AttnArgs &a, const TileInfo &ti, int wave, int nwaves, bool writer,
                                             const DecodeEarly &e, float &m, float &l, f32x4 (&o)[4]) {
   typedef unsigned short u16;
   const int lane = threadIdx.x & 63;
@@ -1103,7 +1104,7 @@ __device__ __forceinline__ void decode_wave(const AttnArgs &a, const TileInfo &t
   const u16 *kp = reinterpret_cast<const u16 *>(a.k);
   const u16 *vp = reinterpret_cast<const u16 *>(a.v);
   // the first two steps' block ids (lane j & 3: tokens c0 + 16j ..), RoPE tables at p
-  constexpr int kPair = 64 * kDecWaves;  // tokens from a wave's first step to its second
+  const int kPair = 64 * nwaves;  // tokens from a wave's first step to its second
   const int c_first = 64 * wave;
   auto step_blocks = [&](int c0) -> int { return trow[min((c0 + 16 * (lane & 3)) / bs, last_blk)]; };
   int bj0 = 0, bj1 = 0;
@@ -1280,7 +1281,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   }
   float m, l;
   f32x4 o[4];
-  decode_wave<MODE>(a, ti, wave, /*writer=*/wave == 0, e, m, l, o);
+  decode_wave<MODE>(a, ti, wave, kDecWaves, /*writer=*/wave == 0, e, m, l, o);
   float M, L, O[4];
   fold_wg4(m, l, o, M, L, O);
   const int qq = tid >> 4, d0 = (tid & 15) * 4;
@@ -1292,20 +1293,21 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
-// Four one-wave workgroups per (row, kv head), on four compute units (one
-// CU issuing all of a head's K/V loads is what bounds the 4-wave kernel):
-// workgroup w runs wave w of decode_wave and writes its (m, l, O), O not
-// divided by l, for the rows of its kv head to parts [batch, H, kDecWaves,
-// kDecPart] floats (m, l, then O's 64 dims).  Folding a row's four in wave
-// order with fold_waves' arithmetic and rounding O / L to bf16 gives the
-// bits of attention_decode_kernel's output (linear_parts_kernel does that
-// in its prologue).  A row past max_kv_len gets a partial that folds to
-// NaN; a row without a new token gets none.
-template <int MODE>
+// NP (4, 8 or 16) one-wave workgroups per (row, kv head), on as many
+// compute units (one CU issuing all of a head's K/V loads is what bounds the
+// 4-wave kernel; with a part per 64-token step no wave waits for a second
+// step): workgroup w runs wave w of decode_wave and writes its (m, l, O), O
+// not divided by l, for the rows of its kv head to parts [batch, H, NP,
+// kDecPart] floats (m, l, two unused, then O's 64 dims).  Folding a row's parts in
+// order with fold_waves' arithmetic and rounding O / L to bf16
+// (linear_parts_kernel's prologue) gives, for kDecWaves parts, the bits of
+// attention_decode_kernel's output.  A row past max_kv_len gets a partial
+// that folds to NaN; a row without a new token gets none.
+template <int MODE, int NP>
 __global__ __launch_bounds__(kWave) void attention_decode_parts_kernel(AttnArgs a, float *parts) {
   TileInfo ti;
-  const int wave = blockIdx.x % kDecWaves;
-  tile_coords(a, blockIdx.x / kDecWaves, ti);
+  const int wave = blockIdx.x % NP;
+  tile_coords(a, blockIdx.x / NP, ti);
   const int lane = threadIdx.x, g = lane >> 4, c = lane & 15;
   DecodeEarly e;
   decode_early(a, ti, lane, e);
@@ -1314,22 +1316,20 @@ __global__ __launch_bounds__(kWave) void attention_decode_parts_kernel(AttnArgs 
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) o[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (tile_meta(a, ti, /*any_split=*/true)) {
-    decode_wave<MODE>(a, ti, wave, /*writer=*/wave == 0, e, m, l, o);
+    decode_wave<MODE>(a, ti, wave, NP, /*writer=*/wave == 0, e, m, l, o);
   } else {
     if (!ti.overflow) return;
     m = 0.0f;
     l = NAN;
   }
   if (c < ti.group) {
-    float *dst = parts + (((int64_t)ti.b * a.H + ti.h * ti.group + c) * kDecWaves + wave) * kDecPart;
+    float *dst = parts + (((int64_t)ti.b * a.H + ti.h * ti.group + c) * NP + wave) * kDecPart;
     if (g == 0) {
       dst[0] = m;
       dst[1] = l;
     }
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[2 + 16 * tt + 4 * g + i] = o[tt][i];
+    for (int tt = 0; tt < 4; ++tt) *reinterpret_cast<f32x4 *>(dst + 4 + 16 * tt + 4 * g) = o[tt];
   }
 }
 
@@ -1989,19 +1989,21 @@ SPECDEC_API int specdec_rope_paged_attention_parts(void *qkv, int64_t token_stri
                                                    float eps, void *k_pool, void *v_pool, const int32_t *tables,
                                                    int64_t table_stride, const int32_t *meta, int32_t batch,
                                                    int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
-                                                   int32_t block_size, float scale, int32_t max_kv_len, float *parts,
-                                                   void *stream) {
+                                                   int32_t block_size, float scale, int32_t max_kv_len,
+                                                   int32_t nparts, float *parts, void *stream) {
   if (batch < 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads || block_size <= 0 || max_kv_len < 0)
     return SPECDEC_EINVAL;
   if (batch == 0 || max_kv_len == 0) return SPECDEC_OK;
   if (!qkv || !cos_table || !sin_table || !k_pool || !v_pool || !tables || !meta || !parts) return SPECDEC_EINVAL;
+  if (nparts != 4 && nparts != 8 && nparts != 16) return SPECDEC_EINVAL;
+  if (((uintptr_t)parts & 15)) return SPECDEC_EINVAL;
   if (head_dim != kD || block_size % 16 != 0 || max_kv_len > 2048 || n_heads / n_kv_heads > kRows)
     return SPECDEC_EUNSUPPORTED;
   if (hidden && (hidden_dim <= 0 || hidden_dim % 8 != 0 || ((uintptr_t)hidden & 15))) return SPECDEC_EINVAL;
   if (hidden && hidden_dim > 4 * kWave * 8) return SPECDEC_EUNSUPPORTED;
   if (token_stride < (int64_t)(n_heads + 2 * n_kv_heads) * kD || token_stride % 8 || ((uintptr_t)qkv & 15))
     return SPECDEC_EINVAL;
-  const int64_t wgs = (int64_t)batch * n_kv_heads * kDecWaves;
+  const int64_t wgs = (int64_t)batch * n_kv_heads * nparts;
   if (wgs > INT32_MAX) return SPECDEC_EUNSUPPORTED;
   AttnArgs a{};
   a.q = qkv;
@@ -2030,8 +2032,15 @@ SPECDEC_API int specdec_rope_paged_attention_parts(void *qkv, int64_t token_stri
   a.parts = 1;
   hipStream_t s = as_stream(stream);
   const dim3 grid((unsigned)wgs), block(kWave);
-  if (block_size == 16) attention_decode_parts_kernel<1><<<grid, block, 0, s>>>(a, parts);
-  else attention_decode_parts_kernel<2><<<grid, block, 0, s>>>(a, parts);
+#define SPECDEC_PARTS(NP)                                                                  \
+  do {                                                                                     \
+    if (block_size == 16) attention_decode_parts_kernel<1, NP><<<grid, block, 0, s>>>(a, parts); \
+    else attention_decode_parts_kernel<2, NP><<<grid, block, 0, s>>>(a, parts);           \
+  } while (0)
+  if (nparts == 4) SPECDEC_PARTS(4);
+  else if (nparts == 8) SPECDEC_PARTS(8);
+  else SPECDEC_PARTS(16);
+#undef SPECDEC_PARTS
   return launch_status();
 }
 

@@ -43,10 +43,14 @@ int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, in
                        const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
                        bool kv_only, hipStream_t s);
 // A draft decode step's attention as split partials
-// (attention_decode_parts_kernel, folded by linear_parts_kernel): kDecWaves
-// per (row, query head), each m, l and the 64 dims of O not divided by l.
+// (attention_decode_parts_kernel, folded by linear_parts_kernel): 4, 8 or
+// 16 one-wave workgroups per (row, kv head), each leaving per query head
+// kDecPart floats: m, l, two unused, then the 64 dims of O not divided by l
+// (16-byte aligned).  With kDecWaves of them the fold has the bits of
+// attention_decode_kernel's.
 constexpr int kDecWaves = 4;
-constexpr int kDecPart = 2 + 64;
+constexpr int kDecMaxParts = 16;
+constexpr int kDecPart = 4 + 64;
 
 // The same for the k and v heads only of a prompt-sized bf16 call (head_dim
 // 64, block_size % 16 == 0), one workgroup per 16-position group and kv

@@ -33,6 +33,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
 
 constexpr int kLinRows = 64;        // rows of a call, at most (four 16-row column tiles)
 constexpr int kLinMaxWaves = 8;     // waves per workgroup (k-step split)
@@ -192,16 +193,18 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_kernel(LinArgs a) {
 }
 
 // linear_kernel<1, KB> of the attention rows a draft decode step left as
-// split partials (attention_decode_parts_kernel: kDecWaves per row and query
+// split partials (attention_decode_parts_kernel: `nparts` per row and query
 // head): each workgroup first folds them into its LDS copy of the rows --
 // per (row, head, 4 dims) the max of the partials' m, then L and O summed
-// in wave order with the same exp2 and fma steps as the attention kernel's
-// own fold, O / L rounded to bf16, so the rows have that kernel's bits --
-// while the weight's first load batch is in flight, then projects them with
-// the plain projection's k-split (x read from LDS instead of memory): the
-// bits of the attention followed by specdec_linear.
-template <int KB>
-__global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs a, const float *parts, int heads) {
+// in part order with the same exp2 and fma steps as the attention kernel's
+// own fold, O / L rounded to bf16 (with kDecWaves parts, that kernel's
+// bits) -- while the weight's first load batch is in flight, then projects
+// them with the plain projection's k-split (x read from LDS instead of
+// memory): the bits of those rows followed by specdec_linear.  Workgroup 0
+// also writes the rows to attn_out when that is given.
+template <int KB, int NP>
+__global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs a, const float *parts, int heads,
+                                                                          uint16_t *attn_out) {
   extern __shared__ __align__(16) uint16_t s_x[];  // [M][K] bf16
   __shared__ f32x4 s_acc[kLinMaxWaves][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -249,22 +252,35 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs
   const int items = a.M * heads * 16;
   for (int it = tid; it < items; it += blockDim.x) {
     const int r = it / (heads * 16), hq = (it / 16) % heads, d0 = (it % 16) * 4;
-    const float *pp = parts + ((int64_t)r * heads + hq) * kDecWaves * kDecPart;
-    float M = pp[0];
-    for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, pp[w * kDecPart]);
-    float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int w = 0; w < kDecWaves; ++w) {
-      const float mw = pp[w * kDecPart];
-      const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-      L = __builtin_fmaf(f, pp[w * kDecPart + 1], L);
+    const float *pp = parts + ((int64_t)r * heads + hq) * NP * kDecPart;
+    // every part's values first, in one round trip
+    float mw[NP], lw[NP];
+    f32x4 ow[NP];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) O[i] = __builtin_fmaf(f, pp[w * kDecPart + 2 + d0 + i], O[i]);
+    for (int w = 0; w < NP; ++w) {
+      const f32x2 ml = *reinterpret_cast<const f32x2 *>(pp + w * kDecPart);
+      mw[w] = ml[0];
+      lw[w] = ml[1];
+      ow[w] = *reinterpret_cast<const f32x4 *>(pp + w * kDecPart + 4 + d0);
+    }
+    float M = mw[0];
+#pragma unroll
+    for (int w = 1; w < NP; ++w) M = fmaxf(M, mw[w]);
+    float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < NP; ++w) {
+      const float f = (mw[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+      L = __builtin_fmaf(f, lw[w], L);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) O[i] = __builtin_fmaf(f, ow[w][i], O[i]);
     }
     uint16_t ob[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ob[i] = __builtin_bit_cast(uint16_t, from_f32<__hip_bfloat16>(O[i] / L));
-    *reinterpret_cast<u32x2 *>(&s_x[r * a.K + hq * 64 + d0]) =
-        u32x2{(uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16)};
+    const u32x2 packed = u32x2{(uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16)};
+    *reinterpret_cast<u32x2 *>(&s_x[r * a.K + hq * 64 + d0]) = packed;
+    if (attn_out && blockIdx.x == 0)
+      *reinterpret_cast<u32x2 *>(attn_out + (int64_t)r * a.K + hq * 64 + d0) = packed;
   }
   __syncthreads();
   if (cnt > 0) {
@@ -509,10 +525,13 @@ SPECDEC_API int specdec_linear(const void *x, int64_t x_stride, const void *w, i
   return launch_status();
 }
 
-SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, const void *w,
-                                         int64_t w_stride, int32_t w_layout, int64_t out_features, void *out,
-                                         int64_t out_stride, int32_t accumulate, void *stream) {
+SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int64_t n_heads, int32_t nparts,
+                                         const void *w, int64_t w_stride, int32_t w_layout, int64_t out_features,
+                                         void *out, int64_t out_stride, int32_t accumulate, void *attn_out,
+                                         void *stream) {
   if (rows < 0 || n_heads <= 0 || out_features <= 0) return SPECDEC_EINVAL;
+  if (nparts != 4 && nparts != 8 && nparts != 16) return SPECDEC_EINVAL;
+  if (((uintptr_t)parts & 15) || (attn_out && ((uintptr_t)attn_out & 7))) return SPECDEC_EINVAL;
   if (w_layout != SPECDEC_W_ROWS && w_layout != SPECDEC_W_TILED) return SPECDEC_EINVAL;
   if (rows == 0) return SPECDEC_OK;
   const int64_t k = n_heads * 64;
@@ -542,7 +561,11 @@ SPECDEC_API int specdec_linear_attn_parts(const float *parts, int64_t rows, int6
   linear_split(a, tiles, waves);  // the plain projection's k-split
   const dim3 grid((unsigned)tiles), block((unsigned)(64 * waves));
   const size_t lds = (size_t)rows * k * 2;
-  linear_parts_kernel<8><<<grid, block, lds, as_stream(stream)>>>(a, parts, (int)n_heads);
+  hipStream_t s = as_stream(stream);
+  uint16_t *ao = (uint16_t *)attn_out;
+  if (nparts == 4) linear_parts_kernel<8, 4><<<grid, block, lds, s>>>(a, parts, (int)n_heads, ao);
+  else if (nparts == 8) linear_parts_kernel<8, 8><<<grid, block, lds, s>>>(a, parts, (int)n_heads, ao);
+  else linear_parts_kernel<8, 16><<<grid, block, lds, s>>>(a, parts, (int)n_heads, ao);
   return launch_status();
 }
 

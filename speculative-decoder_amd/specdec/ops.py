@@ -645,8 +645,18 @@ def attention_split(batch: int, width: int, n_heads: int, n_kv_heads: int, max_k
 
 
 DECODE_PARTS_MAX_ROWS = 16  # rows of a draft step whose attention goes through split partials
-DECODE_PARTS = 4  # partials per row and query head
-DECODE_PART_FLOATS = 2 + 64  # m, l, O
+DECODE_PARTS_COUNTS = (4, 8, 16)  # partials per row and query head a launch may use
+DECODE_PART_FLOATS = 4 + 64  # m, l, two unused, O
+
+
+def decode_parts_count(max_kv_len: int) -> int:
+    """Partials per (row, kv head) for a draft step of at most max_kv_len
+    keys (the graphs' bucket, not the row's length): 4 up to 256 keys, else
+    8.  Measured at the draft's shape (attention + o_proj, one row): 8 parts
+    take 8.5 us at 256-384 keys against 9.3 with 4 and 9.7 with 16, and
+    stay within 0.8 us of 16 parts up to 2048 keys, while 16 cost 1.3 us
+    more than 8 at short contexts (idle parts, a longer fold)."""
+    return 4 if max_kv_len <= 256 else 8
 
 
 def decode_parts_fit(dtype: torch.dtype, batch: int, width: int, n_heads: int, n_kv_heads: int, head_dim: int,
@@ -660,9 +670,19 @@ def decode_parts_fit(dtype: torch.dtype, batch: int, width: int, n_heads: int, n
             and n_heads % n_kv_heads == 0 and n_heads // n_kv_heads <= 16 and n_heads * head_dim <= 2048)
 
 
-def decode_parts_buffer(batch: int, n_heads: int, device) -> torch.Tensor:
-    """The fp32 [batch, H, 4, 66] buffer a draft step's attention partials go through."""
-    return torch.empty(batch, n_heads, DECODE_PARTS, DECODE_PART_FLOATS, dtype=torch.float32, device=device)
+def decode_parts_buffer(batch: int, n_heads: int, device, nparts: int = 4) -> torch.Tensor:
+    """The fp32 [batch, H, nparts, 68] buffer a draft step's attention partials go through."""
+    if nparts not in DECODE_PARTS_COUNTS:
+        raise ValueError(f"nparts must be one of {DECODE_PARTS_COUNTS}")
+    return torch.empty(batch, n_heads, nparts, DECODE_PART_FLOATS, dtype=torch.float32, device=device)
+
+
+def _parts_of(parts: torch.Tensor, dev, batch: int, n_heads: int) -> int:
+    """nparts of a `decode_parts_buffer`, checked."""
+    if parts.dim() != 4 or tuple(parts.shape[:2]) != (batch, n_heads) or parts.shape[3] != DECODE_PART_FLOATS:
+        raise ValueError(f"parts must be fp32 [{batch}, {n_heads}, nparts, {DECODE_PART_FLOATS}]")
+    _on(dev, parts, "parts", torch.float32, True)
+    return parts.shape[2]
 
 
 def rope_paged_attention_parts(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, n_heads, n_kv_heads, head_dim,
@@ -670,14 +690,14 @@ def rope_paged_attention_parts(qkv, cos, sin, k_pool, v_pool, tables, meta, batc
                                norm_of: torch.Tensor | None = None, eps: float = 0.0) -> torch.Tensor:
     """A draft-style decode step (rope_paged_attention of one new token per
     row with split_tokens < 0, the same RoPE, norm and append) whose
-    attention is left as split partials: four one-wave workgroups per (row,
-    kv head), each writing its (m, l, O) to `parts` (`decode_parts_buffer`)
-    instead of folding them in one workgroup.  `linear_attn_parts` folds
-    them into the attention rows (the bits rope_paged_attention produces)
-    and projects them."""
+    attention is left as split partials: nparts (parts.shape[2]) one-wave
+    workgroups per (row, kv head), each writing its (m, l, O) to `parts`
+    (`decode_parts_buffer`) instead of folding them in one workgroup.
+    `linear_attn_parts` folds them into the attention rows (with 4 parts the
+    bits rope_paged_attention produces) and projects them."""
     dev = gpu(qkv, "qkv").device
     _qkv_side(dev, qkv, cos, sin, meta, batch, 1, tables, k_pool, v_pool)
-    _on(dev, parts, "parts", torch.float32, True, batch * n_heads * DECODE_PARTS * DECODE_PART_FLOATS)
+    nparts = _parts_of(parts, dev, batch, n_heads)
     hidden_dim = 0
     if norm_of is not None:
         hidden_dim = norm_of.shape[-1]
@@ -686,21 +706,25 @@ def rope_paged_attention_parts(qkv, cos, sin, k_pool, v_pool, tables, meta, batc
                                                   ptr(norm_of), hidden_dim, float(eps), k_pool.data_ptr(),
                                                   v_pool.data_ptr(), tables.data_ptr(), tables.stride(0),
                                                   meta.data_ptr(), batch, n_heads, n_kv_heads, head_dim, block_size,
-                                                  float(scale), max_kv_len, parts.data_ptr(), stream())
+                                                  float(scale), max_kv_len, nparts, parts.data_ptr(), stream())
     _check(st, "rope_paged_attention_parts")
     return parts
 
 
 def linear_attn_parts(parts: torch.Tensor, rows: int, n_heads: int, w: torch.Tensor, out: torch.Tensor,
-                      accumulate: bool = False) -> torch.Tensor:
+                      accumulate: bool = False, attn_out: torch.Tensor | None = None) -> torch.Tensor:
     """`linear(attn, w, out, accumulate)` where attn [rows, H*64] are the
     attention rows a `rope_paged_attention_parts` call left as partials:
     each workgroup folds them (the attention-only kernel's arithmetic and
     order) into LDS and projects them with specdec_linear's k-split, so
-    `out` gets the bits of rope_paged_attention followed by linear."""
+    `out` gets the bits of those rows followed by linear (with 4 parts, of
+    rope_paged_attention followed by linear).  `attn_out` (bf16 [rows,
+    H*64]) receives the folded rows when given."""
     gpu(w, "w")
-    _on(w.device, parts, "parts", torch.float32, True, rows * n_heads * DECODE_PARTS * DECODE_PART_FLOATS)
+    nparts = _parts_of(parts, w.device, rows, n_heads)
     _on(w.device, out, "out", torch.bfloat16)
+    if attn_out is not None:
+        _on(w.device, attn_out, "attn_out", torch.bfloat16, True, rows * n_heads * 64)
     if w.dim() == 2 and w.stride(1) == 1:
         n, k, layout, w_stride = w.shape[0], w.shape[1], W_ROWS, w.stride(0)
     else:
@@ -711,8 +735,8 @@ def linear_attn_parts(parts: torch.Tensor, rows: int, n_heads: int, w: torch.Ten
     o2 = out.view(rows, n) if out.dim() != 2 else out
     if tuple(o2.shape) != (rows, n) or o2.stride(-1) != 1:
         raise ValueError("out must be bf16 [rows, N] with unit inner stride")
-    st = lib().specdec_linear_attn_parts(parts.data_ptr(), rows, n_heads, w.data_ptr(), w_stride, layout, n,
-                                         o2.data_ptr(), o2.stride(0), int(accumulate), stream())
+    st = lib().specdec_linear_attn_parts(parts.data_ptr(), rows, n_heads, nparts, w.data_ptr(), w_stride, layout, n,
+                                         o2.data_ptr(), o2.stride(0), int(accumulate), ptr(attn_out), stream())
     _check(st, "linear_attn_parts")
     return out
 

@@ -551,12 +551,15 @@ def test_latency_decode_step_matches_oracle(bs, lengths, heads):
     assert (got - want).abs().max().item() < 2e-2
 
 
-def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumulate=True, tiled=True):
+def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumulate=True, tiled=True, nparts=4,
+                attn_rows=None, extras=None):
     """A draft-style step (one new token per row, the norm finished inside) on
     two identical caches: rope_paged_attention (split -1) then linear(attn,
     wo) on the first; rope_paged_attention_parts then linear_attn_parts on
     the second (reading o_proj's weight in its tiled layout unless `tiled`
-    is false).  Returns both outputs and both caches' gathered K/V."""
+    is false; `nparts` partials per kv head; the folded rows to `attn_rows`
+    when given).  Returns both outputs and both caches' gathered K/V; `extras`
+    (a dict, when given) receives wo and the attention-only kernel's rows."""
     from lm.model import LlamaShape, rope_tables
 
     d, batch = 64, len(lengths)
@@ -587,13 +590,15 @@ def _parts_case(bs, lengths, h, hkv, hidden_dim, seed, max_kv_len=None, accumula
                                      batch, 1, h, hkv, d, bs, 0.125, kv_max, attn, attn.stride(1), split_tokens=-1,
                                      norm_of=hidden, eps=1e-5)
             ops.linear(attn.view(batch, h * d), wo, out=out.view(batch, hidden_dim), accumulate=accumulate)
+            if extras is not None:
+                extras.update(wo=wo, attn=attn.view(batch, h * d))
         else:
-            parts = ops.decode_parts_buffer(batch, h, "cuda")
+            parts = ops.decode_parts_buffer(batch, h, "cuda", nparts)
             ops.rope_paged_attention_parts(qkv.clone(), cos, sin, cache.k[0], cache.v[0], cache.table_tensor,
                                            step.meta, batch, h, hkv, d, bs, 0.125, kv_max, parts, norm_of=hidden,
                                            eps=1e-5)
             ops.linear_attn_parts(parts, batch, h, ops.tile_weight(wo) if tiled else wo, out.view(batch, hidden_dim),
-                                  accumulate=accumulate)
+                                  accumulate=accumulate, attn_out=attn_rows)
         res.append((out, cache.gather(0, step)))
     return res
 
@@ -620,6 +625,30 @@ def test_decode_parts_without_accumulate_equal_plain_projection():
 def test_decode_parts_with_row_major_weight(heads, hidden_dim):
     (ref, _), (got, _) = _parts_case(16, [300, 37], heads[0], heads[1], hidden_dim, seed=4, tiled=False)
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("nparts", [8, 16])
+@pytest.mark.parametrize("lengths", [[300], [1], [1000, 64], [2047]])
+def test_decode_parts_of_other_counts(nparts, lengths):
+    """More partials per kv head (8 or 16, one per 64-token step): the
+    folded attention rows agree with the attention-only kernel's to bf16
+    rounding (another fold order), o_proj of them has specdec_linear's bits
+    on those rows, and the pools are the same bit for bit."""
+    h, hkv, hidden_dim = 9, 3, 576
+    batch = len(lengths)
+    rows = torch.zeros(batch, h * 64, dtype=torch.bfloat16, device="cuda")
+    extras = {}
+    (ref, kv_ref), (got, kv_got) = _parts_case(16, lengths, h, hkv, hidden_dim, seed=nparts + lengths[0],
+                                               accumulate=False, nparts=nparts, attn_rows=rows, extras=extras)
+    assert (rows.float() - extras["attn"].float()).abs().max().item() < 2e-2
+    assert torch.equal(got.view(batch, hidden_dim), ops.linear(rows, extras["wo"]))
+    assert torch.equal(kv_got[0], kv_ref[0]) and torch.equal(kv_got[1], kv_ref[1])
+
+
+def test_decode_parts_counts_follow_the_context():
+    assert [ops.decode_parts_count(n) for n in (1, 256, 257, 300, 512, 1024, 2048)] == [4, 4, 8, 8, 8, 8, 8]
+    with pytest.raises(ValueError):
+        ops.decode_parts_buffer(1, 9, "cuda", 5)
 
 
 def test_decode_parts_rows_beyond_max_kv_len_are_nan():
