@@ -67,7 +67,7 @@ extern "C" {
 #define SPECDEC_W_TILED 1
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 9). */
+ * below changes (currently 14). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
