@@ -41,9 +41,9 @@ def _gpu_device(device) -> torch.device:
 
 
 def _upload_i32(values: list[int], device: torch.device) -> torch.Tensor:
-    """An int32 device copy of `values`, staged straight into pinned memory."""
-    host = torch.tensor(values, dtype=torch.int32, pin_memory=True)
-    return host.to(device, non_blocking=True)
+    """An int32 device copy of `values` (a few hundred bytes: from pageable
+    memory, which costs the host less here than pinning a fresh buffer)."""
+    return torch.tensor(values, dtype=torch.int32).to(device, non_blocking=True)
 
 
 class _TableStore:

@@ -57,6 +57,7 @@ def sample_inverse_cdf(probs: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 class Verdict:
     n_accepted: torch.Tensor  # [B] leading draft tokens kept, 0..k
     next_token: torch.Tensor  # [B] residual sample at the first rejection, or the bonus token
+    draft: torch.Tensor | None = None  # [B, k] host copy of the draft, brought back with the verdict
 
 
 _BAD_DRAFT = ("a drafted token has zero draft probability or lies outside the vocabulary; q is not what it "
@@ -95,11 +96,12 @@ def accept_reject(
     ua = _cuda(u_accept.to(p.dtype)).contiguous()
     ur = _cuda(u_residual.to(p.dtype)).contiguous()
     if residual is residual_distribution:
-        out = ops.accept_reject(p, q, draft_d, ua, ur).cpu()
+        # the draft rides in the verdict's one copy to the host
+        out = torch.cat([ops.accept_reject(p, q, draft_d, ua, ur), draft_d.t()]).cpu()
         ops.check_accept_flags(out[2], p.device)
         if bool(out[2].any()):
             raise ValueError(_BAD_DRAFT)
-        return Verdict(out[0].clone(), out[1].clone())
+        return Verdict(out[0].clone(), out[1].clone(), out[3:].t())
     stage = ops.accept_count(p, q, draft_d, ua)
     n_host = stage.cpu()
     if bool(n_host[1].any()):

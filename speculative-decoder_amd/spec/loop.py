@@ -18,7 +18,7 @@ What a caller of the reference's `generate` relies on, and what this driver keep
 
 How it is organised: every prompt becomes a `_Request` holding its context
 and output.  A round proposes, verifies and decides for all live requests,
-brings the verdict and the draft to the host in one copy each, then settles
+brings the verdict and the draft to the host in one copy, then settles
 in two phases: `_plan` works out each request's kept tokens, statistics and
 cache action on the host alone; `_apply` carries the actions out in request
 order (the cache's rollbacks are queued and reach the device with the next
@@ -180,7 +180,8 @@ def generate(target, cache: KVCache, drafter: Drafter, prompts: list[list[int]],
         p = verify(target, cache, ids, contexts, draft, temperature)
         verdict = accept_reject(p, q, draft, generator=gen)
         stats.rounds += 1
-        live, actions = _plan(live, verdict.n_accepted.tolist(), draft.tolist(), verdict.next_token.tolist(), stats,
+        drafted = verdict.draft if getattr(verdict, "draft", None) is not None else draft
+        live, actions = _plan(live, verdict.n_accepted.tolist(), drafted.tolist(), verdict.next_token.tolist(), stats,
                               max_new_tokens, eos_id)
         _apply(actions, cache, drafter)
         if stats.rounds == 1:
