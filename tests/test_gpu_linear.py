@@ -66,7 +66,8 @@ def test_accumulate_adds_before_the_rounding(rows, k, n):
     check(out.cpu(), x, w, base)
 
 
-@pytest.mark.parametrize("rows,k,n", [(5, 2048, 6144), (40, 576, 1000), (64, 8192, 48), (48, 64, 40)])
+@pytest.mark.parametrize("rows,k,n", [(5, 2048, 6144), (40, 576, 1000), (64, 8192, 48), (48, 64, 40),
+                                      (16, 8192, 2048)])
 def test_rows_do_not_depend_on_the_other_rows(rows, k, n):
     """Calls of 1 to 64 rows (one to four 16-row column tiles per wave; one
     wave for K = 64, up to eight otherwise): each row has the bits of the
@@ -76,7 +77,7 @@ def test_rows_do_not_depend_on_the_other_rows(rows, k, n):
     together = ops.linear(xd, wd)
     for r in range(rows):
         assert torch.equal(ops.linear(xd[r:r + 1], wd), together[r:r + 1]), r
-    for m in (1, 5, 16, 17, 33):
+    for m in (1, 5, 8, 9, 16, 17, 33):
         if m <= rows:
             assert torch.equal(ops.linear(xd[:m], wd), together[:m]), m
 
