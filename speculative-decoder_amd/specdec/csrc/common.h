@@ -177,11 +177,17 @@ __device__ __forceinline__ float row_rms_scale_bf16(const u32x4 *h, int nvec, in
 // SiLU(bf16(s g)) * bf16(s u), rounded to bf16 (raw bits): the gate and up
 // values scaled by the row's norm scale and rounded as a projection's output
 // is, then transformers' act_fn(gate) * up with each step rounded to bf16.
+// SiLU(x) = x / (1 + e^-x) is taken as x * rcp(1 + 2^(-x log2 e)) on the
+// hardware exp2 and reciprocal (about 1 ulp each, so the fp32 value is within
+// a few ulp of the quotient and rounds to the same bf16 but for ties): a
+// short dependent chain at the end of the MLP kernels, where an IEEE divide
+// and a library exp made a chain of tens of instructions on few live lanes.
 __device__ __forceinline__ unsigned short silu_mul_scaled_bf16(float g, float u, float s) {
 #pragma clang fp contract(off)
   const float x = to_f32(from_f32<__hip_bfloat16>(s * g));
   const float up = to_f32(from_f32<__hip_bfloat16>(s * u));
-  const __hip_bfloat16 a = from_f32<__hip_bfloat16>(x / (1.0f + expf(-x)));
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  const __hip_bfloat16 a = from_f32<__hip_bfloat16>(x * __builtin_amdgcn_rcpf(1.0f + e));
   return __builtin_bit_cast(unsigned short, from_f32<__hip_bfloat16>(to_f32(a) * up));
 }
 

@@ -365,10 +365,13 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_silu_kernel(LinArgs 
   const unsigned xtile = (unsigned)(16 * a.x_stride * 2);
   // the first pass over this wave's first residual row (row `wave`), loaded
   // now so its round trip overlaps the weight's (rows past M: not used)
+  // (and of its second row, wave + nw, when the call has more rows than waves)
   const int nvh = hdim / 8;
   const u32x4 *h0 = reinterpret_cast<const u32x4 *>(hid + (int64_t)min(wave, a.M - 1) * hid_stride);
-  u32x4 hv0[NVH];
+  const u32x4 *h1 = reinterpret_cast<const u32x4 *>(hid + (int64_t)min(wave + nw, a.M - 1) * hid_stride);
+  u32x4 hv0[NVH], hv1[NVH];
   row_pass_loads<NVH>(h0, 0, nvh, lane, hv0);
+  row_pass_loads<NVH>(h1, 0, nvh, lane, hv1);
   f32x4 accg[NCT], accu[NCT];
 #pragma unroll
   for (int ct = 0; ct < NCT; ++ct) accg[ct] = accu[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -430,8 +433,9 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_silu_kernel(LinArgs 
   // the rows' norm scales, wave w taking rows w, w + nw, ...
   for (int r = wave; r < a.M; r += nw) {
     const u32x4 *hr = reinterpret_cast<const u32x4 *>(hid + (int64_t)r * hid_stride);
-    const float sc = r == wave ? row_rms_scale_bf16_from<NVH>(hr, hv0, nvh, hdim, eps, lane)
-                               : row_rms_scale_bf16<NVH>(hr, nvh, hdim, eps, lane);
+    const float sc = r == wave        ? row_rms_scale_bf16_from<NVH>(hr, hv0, nvh, hdim, eps, lane)
+                     : r == wave + nw ? row_rms_scale_bf16_from<NVH>(hr, hv1, nvh, hdim, eps, lane)
+                                      : row_rms_scale_bf16<NVH>(hr, nvh, hdim, eps, lane);
     if (lane == 0) s_scale[r] = sc;
   }
   __syncthreads();
