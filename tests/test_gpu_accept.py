@@ -95,6 +95,8 @@ def test_scripted_uniforms():
 
     accepted = run(0.6, 0.5)
     assert accepted.n_accepted.item() == 1 and accepted.next_token.item() == 1
+    # the draft comes back with the verdict, as host int64 [B, k]
+    assert accepted.draft.device.type == "cpu" and torch.equal(accepted.draft, draft)
     rejected = run(0.7, 0.8)
     assert rejected.n_accepted.item() == 0 and rejected.next_token.item() == 1
     assert run(0.7, 0.5).next_token.item() == 0
