@@ -236,16 +236,22 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void linear_parts_kernel(LinArgs
   };
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   const int xrow = c * a.K;  // this lane's row of x in LDS (rows past M are zero)
+  // the batch's x operands are read from LDS first, then its MFMAs run back
+  // to back (reading each operand just before its MFMA waited out one LDS
+  // round trip per k-step)
   auto consume = [&](const u32x4 (&A)[KB], int b) {
+    u32x4 bv[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      bv[j] = u32x4{0u, 0u, 0u, 0u};
+      if (c < a.M && b * KB + j < cnt)
+        bv[j] = *reinterpret_cast<const u32x4 *>(&s_x[xrow + 32 * (s_lo + b * KB + j) + 8 * g]);
+    }
 #pragma unroll
     for (int j = 0; j < KB; ++j)
-      if (b * KB + j < cnt) {
-        const int s = s_lo + b * KB + j;
-        u32x4 bv = u32x4{0u, 0u, 0u, 0u};
-        if (c < a.M) bv = *reinterpret_cast<const u32x4 *>(&s_x[xrow + 32 * s + 8 * g]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[j]), __builtin_bit_cast(bf16x8, bv),
-                                                      acc, 0, 0, 0);
-      }
+      if (b * KB + j < cnt)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[j]),
+                                                      __builtin_bit_cast(bf16x8, bv[j]), acc, 0, 0, 0);
   };
   if (cnt > 0) issue(A0, 0);
   // ---- the fold: item (row r, head hq, dims d0 .. d0+3)
