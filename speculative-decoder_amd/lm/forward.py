@@ -163,7 +163,8 @@ def forward_core(llama: Llama, cache: KVCache, meta: torch.Tensor, ids: torch.Te
         else:
             ops.add_rmsnorm(hidden, _project(act, layer.wd, gemv, layer.wd_t), llama.unit_norm, x, eps)
     if last is not None:
-        x = x[torch.arange(b, device=x.device), last]
+        # last is in [0, t): with one token per row it selects that token, a view
+        x = x[:, 0] if t == 1 else x[torch.arange(b, device=x.device), last]
     if temperature is None:
         return logits(llama, x)
     return probabilities(llama, x, temperature, out, index_out)

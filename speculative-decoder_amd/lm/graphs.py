@@ -143,6 +143,9 @@ class DraftStepGraph(_Captured):
         self.meta = torch.zeros(3, batch, dtype=torch.int32, device=dev)
         self.u = torch.zeros(batch, dtype=torch.float32, device=dev)
         self.token = torch.zeros(batch, dtype=torch.int64, device=dev)
+        # one token per row (the usual first step): each row's last token is
+        # position 0, so no launch computes it
+        self.last0 = torch.zeros(batch, dtype=torch.int64, device=dev) if width == 1 else None
 
     def run(self, ids, meta, u):
         def prepare():
@@ -151,7 +154,7 @@ class DraftStepGraph(_Captured):
             self.u.copy_(u, non_blocking=True)
 
         def work():
-            last = self.meta[2].long() - 1
+            last = self.last0 if self.last0 is not None else self.meta[2].long() - 1
             if self.temperature == 0.0:  # the one-hot row's inverse-CDF draw is its argmax
                 q = forward_core(self.llama, self.cache, self.meta, self.ids, self.bucket, last, self.ws, self.split,
                                  temperature=0.0, index_out=self.token)
