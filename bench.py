@@ -47,6 +47,7 @@ sys.path.insert(0, str(ROOT / "speculative-decoder_amd"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+HOST_WAIT = "default"  # how the host waits for the GPU (main() may switch HIP to spinning)
 # HBM bytes per launch of the B=8, context-4096 verify attention (one tiled
 # launch): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention`,
 # each scaled by what the counter reads for a copy of known size.
@@ -1050,6 +1051,13 @@ def main():
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (the path is built and "
               "measured on a single GPU; sharding across GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
+    # the host spins while it waits for each round's verdict (before anything
+    # touches the GPU); SPECDEC_SPIN_WAIT=0 keeps HIP's default wait
+    global HOST_WAIT
+    if os.environ.get("SPECDEC_SPIN_WAIT", "1") != "0":
+        from specdec import spin_wait
+
+        HOST_WAIT = "spin" if spin_wait() else "default (spin refused)"
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
@@ -1135,7 +1143,8 @@ def main():
         "data": "synthetic (random-init weights N(0, 0.02), seeded uniform prompt ids)",
         "config": {"workload": "greedy speculative decode, target SmolLM2-1.7B shapes / draft SmolLM2-135M shapes, "
                                "batch 1, k=4, paged KV block 16, prompt 256, 128 new tokens",
-                   "batch": 1, "k": K, "prompt": PROMPT, "new_tokens": NEW_TOKENS, "block_size": BLOCK},
+                   "batch": 1, "k": K, "prompt": PROMPT, "new_tokens": NEW_TOKENS, "block_size": BLOCK,
+                   "host_wait": HOST_WAIT},
         "roofline": {"bound": "hbm", "achieved": attn["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": ATTN_B8_TRAFFIC,
                      "kernel": "verify paged attention (attention_bf16_kernel<1, 16, true>: one 16-wave workgroup "

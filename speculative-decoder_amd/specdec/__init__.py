@@ -4,4 +4,4 @@
 The library is loaded on first use; a missing library is an error, never a
 silent fallback.
 """
-from specdec._lib import LIB_PATH, available, lib  # noqa: F401
+from specdec._lib import LIB_PATH, available, lib, spin_wait  # noqa: F401

@@ -61,6 +61,29 @@ def available() -> bool:
     return LIB_PATH.exists()
 
 
+HIP_DEVICE_SCHEDULE_SPIN = 1  # hipDeviceScheduleSpin
+
+
+def spin_wait() -> bool:
+    """Have HIP spin, not sleep, while the host waits for the GPU (a
+    synchronising copy, an event or a stream wait), so the host resumes as
+    soon as the GPU is done -- a round loop reads each verdict back this
+    way -- at the cost of a busy core while it waits.  It must run before the
+    process first uses the GPU (torch.cuda.is_available() already does);
+    returns whether HIP accepted it.  Off unless called."""
+    for name in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+        try:
+            hip = ctypes.CDLL(name)
+            break
+        except OSError:
+            continue
+    else:
+        return False
+    hip.hipSetDeviceFlags.argtypes = [ctypes.c_uint]
+    hip.hipSetDeviceFlags.restype = c_int
+    return hip.hipSetDeviceFlags(HIP_DEVICE_SCHEDULE_SPIN) == 0
+
+
 def load(path: Path = LIB_PATH) -> ctypes.CDLL:
     """Load the library and declare every entry point (no GPU needed)."""
     handle = ctypes.CDLL(str(path))

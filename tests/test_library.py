@@ -56,3 +56,18 @@ def test_head_entry_points_check_shapes_before_launch():
     # more than 16 rows in one fused call
     assert lib.specdec_head_probabilities(16, 64, 16, 64, 17, 64, 100, 1.0, 16, 100, None, 0, None, 0, 16,
                                           nbytes.value, 0, None) == 3
+
+
+def test_spin_wait_is_a_plain_request():
+    """specdec.spin_wait() asks HIP to spin while waiting and reports whether
+    HIP took it (in a fresh process: it must come before any GPU use; with
+    no GPU HIP refuses it)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    pkg = Path(__file__).resolve().parents[1] / "speculative-decoder_amd"
+    out = subprocess.run([sys.executable, "-c", "import specdec; print(specdec.spin_wait())"], cwd=pkg,
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() in ("True", "False")
