@@ -509,7 +509,7 @@ def bench_prefill_attention():
 
 def bench_kernels(attention_grid=True):
     from specdec import ops
-    from specdec.workloads import planted_rows
+    from workloads import planted_rows
 
     res = {}
     # config 1: accept-reject, B=1, k=4, V=49152, fp32, T=1
@@ -737,7 +737,7 @@ def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 
     from spec.draft import ModelDraft
     from spec.loop import generate
     from spec.ngram import NGramDraft
-    from specdec.workloads import planted_rows
+    from workloads import planted_rows
 
     results = {}
     new_tokens = context - prompt_len
@@ -938,7 +938,7 @@ def cpu_kernel_baselines(seconds=1.0):
     import oracle.kv as okv
     import oracle.ngram as on
     import oracle.sampling as osamp
-    from specdec.workloads import planted_rows
+    from workloads import planted_rows
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -997,7 +997,7 @@ def cpu_batched_baseline(tm, dm, batch=8, prompt_len=128, new_tokens=8, k=4, tem
     import oracle.kv as okv
     import oracle.loop as ol
     from oracle.draft import ModelDraft as OModelDraft
-    from specdec.workloads import planted_rows
+    from workloads import planted_rows
 
     prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
     blocks = batch * ((prompt_len + new_tokens + 2 * k + 2 * BLOCK) // BLOCK + 2)

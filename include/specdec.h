@@ -67,7 +67,7 @@ extern "C" {
 #define SPECDEC_W_TILED 1
 
 /* ABI version; bumped whenever a signature or the meaning of an argument
- * below changes (currently 14). */
+ * below changes (currently 15). */
 int specdec_abi_version(void);
 
 /* ---------------------------------------------------------------- accept --- */
@@ -83,10 +83,11 @@ int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t v
                           int64_t out_stride, int64_t *index_out, int64_t index_stride,
                           void *stream);
 
-/* Bytes of the workspace specdec_accept_reject uses for `batch` rows
- * (chunk sums and barrier counters).  It must be zeroed once before its
- * first use (and again after a call reports flag 2, below); calls leave it
- * zeroed for the next. */
+/* Bytes of the workspace specdec_accept_reject and
+ * specdec_accept_reject_logits use for `batch` rows (arrival counters, the
+ * call epoch, and each row's meeting words).  It must be zeroed once, when
+ * it is allocated; calls never need it cleared again.  Calls sharing a
+ * workspace must be ordered (one stream). */
 int specdec_accept_workspace(int64_t batch, int64_t *bytes);
 
 /* Fused accept-reject for a batch: gather p(x), q(x) of the drafted tokens,
@@ -100,9 +101,11 @@ int specdec_accept_workspace(int64_t batch, int64_t *bytes);
  * [0, vocab).
  * With a workspace (fp32, and batch * chunks within one workgroup per
  * compute unit) each row is spread over many workgroups of one launch that
- * meet at two barriers; the flag is 2 if a barrier timed out (the workspace
- * must then be zeroed again; next_token is not valid).  Calls sharing a
- * workspace must be ordered.  Without one, one workgroup runs each row.
+ * exchange chunk values twice.  A workgroup reads the values it waits for
+ * at most `spin` more times after its first read (not at all for spin < 0)
+ * and then computes the missing chunks' values itself, with the same bits,
+ * so every call completes whether or not a row's workgroups are resident
+ * together.  Without a workspace one workgroup runs each row.
  * Replaces spec/accept.py:44-79 `accept_reject` with the default residual
  * (spec/accept.py:18-26) and spec/accept.py:29-35 `sample_inverse_cdf`. */
 int specdec_accept_reject(const void *p, const void *q, int dtype,
@@ -111,7 +114,29 @@ int specdec_accept_reject(const void *p, const void *q, int dtype,
                           const int64_t *draft, const void *u_accept,
                           const void *u_residual, int64_t batch, int64_t k,
                           int64_t vocab, int64_t *out, void *workspace,
-                          int64_t workspace_bytes, void *stream);
+                          int64_t workspace_bytes, int32_t spin, void *stream);
+
+/* Accept-reject from logits in one launch: p = probabilities(target_logits,
+ * temperature) and q = probabilities(draft_logits, temperature) -- the
+ * softmax of logits / T, or the one-hot of the lowest-index argmax at
+ * T = 0 -- are formed inside the launch from row statistics the row's
+ * workgroups exchange, and the accept test, residual and inverse-CDF sample
+ * follow as in specdec_accept_reject.  Every logit is read from memory once
+ * (the residual row's chunk a second time); no probability row is written.
+ * target_logits [batch, k+1, vocab] and draft_logits [batch, k, vocab] fp32
+ * (16-byte aligned rows: vocab and the strides multiples of 4), k <= 16;
+ * draft, u_accept, u_residual, out, workspace and spin as above (the
+ * workspace is required).  SPECDEC_EUNSUPPORTED when the shapes do not fit
+ * (then probabilities + accept_reject give the same decisions).
+ * Replaces lm/sampling.py:13-18 `probabilities` of the target and draft
+ * rows followed by spec/accept.py:44-79 `accept_reject`. */
+int specdec_accept_reject_logits(const void *target_logits, const void *draft_logits, int dtype,
+                                 int64_t t_batch_stride, int64_t t_row_stride,
+                                 int64_t d_batch_stride, int64_t d_row_stride, float temperature,
+                                 const int64_t *draft, const void *u_accept,
+                                 const void *u_residual, int64_t batch, int64_t k, int64_t vocab,
+                                 int64_t *out, void *workspace, int64_t workspace_bytes,
+                                 int32_t spin, void *stream);
 
 /* First stage of accept-reject alone (for a caller-supplied residual):
  * out int64 [2, batch]: n_accepted and a flag that is 1 when a drafted token

@@ -57,11 +57,29 @@ def sample_inverse_cdf(probs: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 class Verdict:
     n_accepted: torch.Tensor  # [B] leading draft tokens kept, 0..k
     next_token: torch.Tensor  # [B] residual sample at the first rejection, or the bonus token
-    draft: torch.Tensor | None = None  # [B, k] host copy of the draft, brought back with the verdict
+
+
+def host_draft(verdict: Verdict) -> torch.Tensor | None:
+    """The [B, k] host copy of the draft that came back in the verdict's
+    device-to-host copy, or None.  It is an attribute outside the dataclass's
+    fields, so `fields`, `astuple`, `==` and `repr` of a Verdict are those of
+    the reference's two-field type (spec/accept.py:38-41)."""
+    return getattr(verdict, "_host_draft", None)
 
 
 _BAD_DRAFT = ("a drafted token has zero draft probability or lies outside the vocabulary; q is not what it "
               "was sampled from")
+
+
+def _settle(out: torch.Tensor, draft_d: torch.Tensor) -> Verdict:
+    """The kernel's [3, B] output and the draft brought to the host in one
+    copy; the reference's ValueError for a bad draft."""
+    host = torch.cat([out, draft_d.t()]).cpu()
+    if bool(host[2].any()):
+        raise ValueError(_BAD_DRAFT)
+    verdict = Verdict(host[0].clone(), host[1].clone())
+    object.__setattr__(verdict, "_host_draft", host[3:].t())
+    return verdict
 
 
 def _uniforms(shape: tuple[int, ...], generator: torch.Generator | None, dtype: torch.dtype) -> torch.Tensor:
@@ -97,11 +115,7 @@ def accept_reject(
     ur = _cuda(u_residual.to(p.dtype)).contiguous()
     if residual is residual_distribution:
         # the draft rides in the verdict's one copy to the host
-        out = torch.cat([ops.accept_reject(p, q, draft_d, ua, ur), draft_d.t()]).cpu()
-        ops.check_accept_flags(out[2], p.device)
-        if bool(out[2].any()):
-            raise ValueError(_BAD_DRAFT)
-        return Verdict(out[0].clone(), out[1].clone(), out[3:].t())
+        return _settle(ops.accept_reject(p, q, draft_d, ua, ur), draft_d)
     stage = ops.accept_count(p, q, draft_d, ua)
     n_host = stage.cpu()
     if bool(n_host[1].any()):
@@ -112,3 +126,39 @@ def accept_reject(
     r = residual(p[rows, n], q_padded[rows, n])
     tokens = ops.sample_inverse_cdf(_cuda(r).to(p.dtype).contiguous(), ur)
     return Verdict(n_host[0].clone(), tokens.cpu())
+
+
+def accept_reject_logits(
+    target_logits: torch.Tensor,
+    draft_logits: torch.Tensor,
+    draft: torch.Tensor,
+    temperature: float,
+    generator: torch.Generator | None = None,
+    u_accept: torch.Tensor | None = None,
+    u_residual: torch.Tensor | None = None,
+) -> Verdict:
+    """accept_reject(probabilities(target_logits, T), probabilities(draft_logits, T), draft, ...)
+    with p and q never materialised: target_logits [B, k+1, V] and
+    draft_logits [B, k, V] (lm/sampling.py:13-18 then spec/accept.py:44-79).
+    One launch reads each logit once and returns the same verdict the two
+    steps give (up to the last bits of the softmax, as two softmax kernels
+    differ).  Uniforms are drawn as accept_reject draws them (fp32, u_accept
+    then u_residual).  Shapes the fused kernel does not take run the two
+    steps."""
+    b, k = draft.shape
+    if u_accept is None:
+        u_accept = _uniforms((b, k), generator, torch.float32)
+    if u_residual is None:
+        u_residual = _uniforms((b,), generator, torch.float32)
+    tl = _cuda(target_logits).float()
+    dl = _cuda(draft_logits).float()
+    draft_d = _cuda(draft.to(torch.int64)).contiguous()
+    ua = _cuda(u_accept.float()).contiguous()
+    ur = _cuda(u_residual.float()).contiguous()
+    out = ops.accept_reject_logits(tl, dl, temperature, draft_d, ua, ur)
+    if out is None:
+        from lm.sampling import probabilities
+
+        return accept_reject(probabilities(tl, temperature), probabilities(dl, temperature), draft, u_accept=ua,
+                             u_residual=ur)
+    return _settle(out, draft_d)

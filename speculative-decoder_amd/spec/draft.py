@@ -64,9 +64,9 @@ class ModelDraft:
 
     def propose(self, seq_ids: list[int], contexts: list[list[int]], k: int, temperature: float,
                 generator: torch.Generator) -> tuple[torch.Tensor, torch.Tensor]:
-        # The draft cache lags the context by one token normally and by two
-        # after a round that accepted every draft (d_k was sampled but never
-        # fed); feeding every uncached token in the first step closes either gap.
+        # whatever part of the context the draft has not cached (its last
+        # token, plus the final draft of a fully accepted round, whose KV was
+        # never computed) goes into the first step as one right-padded chunk
         pending: list[list[int]] | torch.Tensor = [ctx[self.cache.length(s):] for s, ctx in zip(seq_ids, contexts)]
         if graphs.enabled() and k > 0:
             return self._propose_graphs(seq_ids, pending, k, temperature, generator)
@@ -114,7 +114,9 @@ class ModelDraft:
 
 
 class UniformDraft:
-    """The worst useful draft: acceptance near 1/V, output must still be exact."""
+    """Drafts ids uniformly at random with q = 1/V everywhere.  Almost every
+    draft is rejected, so this exercises the residual-sampling path; the loop's
+    output distribution must still be the target's."""
 
     def __init__(self, vocab_size: int) -> None:
         self.vocab_size = vocab_size

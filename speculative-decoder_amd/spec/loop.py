@@ -33,7 +33,7 @@ import torch
 
 from cache.kv import KVCache
 from lm.sampling import probabilities
-from spec.accept import accept_reject
+from spec.accept import accept_reject, host_draft
 from spec.draft import Drafter, run, sample
 from spec.verify import verify
 
@@ -180,7 +180,9 @@ def generate(target, cache: KVCache, drafter: Drafter, prompts: list[list[int]],
         p = verify(target, cache, ids, contexts, draft, temperature)
         verdict = accept_reject(p, q, draft, generator=gen)
         stats.rounds += 1
-        drafted = verdict.draft if getattr(verdict, "draft", None) is not None else draft
+        drafted = host_draft(verdict)
+        if drafted is None:
+            drafted = draft
         live, actions = _plan(live, verdict.n_accepted.tolist(), drafted.tolist(), verdict.next_token.tolist(), stats,
                               max_new_tokens, eos_id)
         _apply(actions, cache, drafter)

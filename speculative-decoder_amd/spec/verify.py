@@ -11,13 +11,15 @@ from lm.model import as_llama
 
 def verify(target, cache: KVCache, seq_ids: list[int], contexts: list[list[int]], draft: torch.Tensor,
            temperature: float) -> torch.Tensor:
-    """One target forward over [context[-1], d_1, ..., d_k] per row.  Output row
-    i is the target's distribution for the token after d_i (row 0: for d_1
-    itself) and row k is the bonus position.  Returns p [B, k+1, V] float32.
+    """p [B, k+1, V] float32, in GPU memory, for accept_reject.
 
-    p stays in GPU memory: its only consumer is accept_reject, which runs
-    there.  Positions run from len(context) - 1 to len(context) + k - 1, set
-    by the cache's per-row past length."""
+    Each row feeds k+1 tokens at once: the last context token, whose KV the
+    target has not cached yet, followed by the k drafted ids.  The softmax
+    (or one-hot, at temperature 0) after input position j is what the
+    target would emit there: positions 0..k-1 judge drafts 1..k, position k
+    gives the extra token emitted when every draft is kept.  The new tokens
+    occupy cache positions len(context) - 1 .. len(context) + k - 1, so the
+    cache must hold exactly len(context) - 1 positions on entry."""
     for seq_id, ctx in zip(seq_ids, contexts):
         if cache.length(seq_id) != len(ctx) - 1:
             raise RuntimeError(f"seq {seq_id}: target cache holds {cache.length(seq_id)}, expected {len(ctx) - 1}")

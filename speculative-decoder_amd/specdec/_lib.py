@@ -17,7 +17,9 @@ SIGNATURES: dict[str, list] = {
     "specdec_abi_version": [],
     "specdec_probabilities": [P, c_int, I64, I64, I64, c_float, P, I64, P, I64, P],
     "specdec_accept_workspace": [I64, P],
-    "specdec_accept_reject": [P, P, c_int, I64, I64, I64, I64, P, P, P, I64, I64, I64, P, P, I64, P],
+    "specdec_accept_reject": [P, P, c_int, I64, I64, I64, I64, P, P, P, I64, I64, I64, P, P, I64, I32, P],
+    "specdec_accept_reject_logits": [P, P, c_int, I64, I64, I64, I64, c_float, P, P, P, I64, I64, I64, P, P, I64,
+                                     I32, P],
     "specdec_accept_count": [P, P, c_int, I64, I64, I64, I64, P, P, I64, I64, I64, P, P],
     "specdec_sample_inverse_cdf": [P, c_int, I64, I64, I64, P, P, P],
     "specdec_one_hot": [P, I64, I64, P, P],
@@ -53,7 +55,7 @@ SIGNATURES: dict[str, list] = {
 # fp32 split partials the library holds per GPU for specdec_paged_attention_static
 STATIC_PARTIAL_FLOATS = 2 * 1024 * 1024
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 _lib: ctypes.CDLL | None = None
 
 

@@ -17,6 +17,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <initializer_list>
+
 namespace specdec {
 
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
@@ -602,46 +604,69 @@ __global__ __launch_bounds__(kAcceptThreads) void sample_inverse_cdf_kernel(
 // ----------------------------------------- accept-reject over many CUs ----
 // fp32 accept-reject with each batch row spread over G workgroups of 256
 // threads -- chunk g of the row, E consecutive elements per thread -- in
-// one launch whose workgroups meet twice per row:
-//   0. each workgroup finds the accept count n itself with scalar loads (the
-//      drafted ids, then p(x) and q(x)) and loads its chunk of p[n] and q[n]
-//      (q[k] is the zero row: the bonus samples p[k]);
-//   1. it publishes the fp64 sum of its chunk of the residual
-//      r = max(0, p[n] - q[n]);
-//   2. once every chunk sum of its row is published, each adds them in chunk
-//      order (the residual total, rounded to fp32), divides its elements by
-//      it (or takes p's row when the total is 0) and publishes L_g, the fp64
-//      inclusive prefix sum of its chunk at the chunk's last element;
-//   3. once every L_g is published, each forms C_j = L_0 + ... + L_{j-1} in
-//      chunk order and the target u * fp32(C_G); the one workgroup whose
-//      chunk holds the first prefix above the target -- fp32(C_g) <= target
-//      < fp32(C_{g+1}) -- counts its prefixes that do not exceed it.
-// An element's prefix is C_g + its chunk-local inclusive prefix (fp64, the
-// thread's run after a fixed-order workgroup scan), so a chunk's last
-// prefix is C_{g+1} exactly and the chunk test agrees with the count.
+// one launch, in two forms:
+//   probabilities: p [B, k+1, V] and q [B, k, V] as given;
+//   logits: the target and draft logits of those shapes and a temperature
+//     T.  p = softmax(l / T) (the one-hot of the lowest-index argmax at
+//     T = 0) is formed on the fly from row statistics; no probability row
+//     is written or read back.
+// The workgroups of a row meet up to three times, each meeting exchanging
+// one value set per chunk:
+//   A (logits form): for every logit row, the chunk's max m of y = l / T
+//     and its sum of 2^((y - m) log2 e) (at T = 0 the max of l and the
+//     lowest index holding it).  Every workgroup folds them in chunk order
+//     into the row's (M, S), so it knows p(x) and q(x) of every drafted
+//     token and the accept count n;
+//   B: the fp64 sum of the chunk's residual r = max(0, p[n] - q[n]) (q[k]
+//     is the zero row: the bonus samples p[k]);
+//   C: once the chunk sums are added in chunk order (the residual total,
+//     rounded to fp32) and the chunk's elements divided by it (or p's row
+//     taken when it is 0), L_g, the fp64 inclusive prefix at the chunk's
+//     last element.
+// Then C_j = L_0 + ... + L_{j-1} in chunk order and the target u * fp32(C_G);
+// the one workgroup whose chunk holds the first prefix above the target --
+// fp32(C_g) <= target < fp32(C_{g+1}) -- counts its prefixes that do not
+// exceed it.  An element's prefix is C_g + its chunk-local inclusive prefix
+// (fp64, the thread's run after a fixed-order workgroup scan), so a chunk's
+// last prefix is C_{g+1} exactly and the chunk test agrees with the count.
 // Accumulation in fp64 with a rounding per prefix is the CPU cumsum's rule;
 // only the order of the fp64 additions differs from a sequential sum.
 //
-// Meetings: a value is published with a device-scope atomic store, encoded
-// as the complement of the fp64 bits, so that it is never 0; a reader polls
-// the slots it needs until none reads 0 (bounded: a timeout flags the row
-// with 2 in out[2B + b]).  Slots go back to 0 without a counter: a
-// workgroup clears its L slot first thing (the clear is acknowledged before
-// its first publish, so no reader can pass the first meeting and still see
-// the last call's L), and clears its chunk-sum slot once every L is
-// published (every reader of the chunk sums has then finished with them).
-// The workspace needs zeroing once, not per call.  The grid never exceeds
-// one workgroup per compute unit, so every workgroup of a row is resident
-// together.  At B = 1 and 8 twelve chunks of 16 elements per thread
-// measured fastest (8.7 us against 9.7 with 24 chunks, 10.9 with 48, and
-// 13.1 for a variant loading every candidate row before n was known).
+// Meeting words carry the call's tag: word = (tag << 32) | 32-bit payload
+// (an fp64 value takes two words).  The tag is the workspace's epoch plus
+// one, read by every workgroup when it starts; the last workgroup to arrive
+// at the end advances the epoch, so words left by earlier calls never carry
+// the current tag, and nothing is ever cleared (the workspace is zeroed
+// once, when it is allocated).  A reader reads the words it needs, then
+// again at most `spin` times while some are missing (never, for spin < 0).
+// A chunk whose words are still missing then is computed by the reader
+// itself, with the code its own workgroup runs -- the same loads, the same
+// operations in the same order, so the same bits -- and the call finishes
+// whether or not the workgroups of a row are resident together.
 constexpr int kMwThreads = 256;
-constexpr int kMwMaxG = 64;     // chunks per row
-constexpr int kMwSpin = 1 << 20;
-// per-row workspace, in uint64 words: chunk sums [G], then L [G]
-constexpr int64_t kMwL = kMwMaxG;
-constexpr int64_t kMwRowWords = 2 * kMwMaxG;
+constexpr int kMwMaxG = 64;                 // chunks per row
+constexpr int kMwMaxK = 16;                 // draft positions (logits form)
+constexpr int kMwMaxR = 2 * kMwMaxK + 1;    // logit rows per batch entry
+constexpr int64_t kMwHead = 16;             // words before the rows: arrival counters [2], the epoch
+// a row's words: B (2 per chunk), C (2 per chunk), A (2 per logit row and chunk)
+constexpr int64_t kMwB = 0, kMwC = 2 * kMwMaxG, kMwA = 4 * kMwMaxG;
+constexpr int64_t kMwRowWords = kMwA + 2 * (int64_t)kMwMaxR * kMwMaxG;
+constexpr int kMwPollMax = (int)((2 * kMwMaxR * kMwMaxG + kMwThreads - 1) / kMwThreads);
 constexpr int kMwUnroll = 8;  // drafted positions whose scalar loads go out together
+constexpr float kMwLog2e = 1.4426950408889634f;
+
+struct MwArgs {
+  const float *p, *q;  // probabilities, or the target and draft logits
+  int64_t p_bs, p_rs, q_bs, q_rs;
+  const int64_t *draft;
+  const float *u_accept, *u_residual;
+  int64_t batch, k, vocab;
+  int G;
+  float temperature;  // logits form
+  int spin;
+  int64_t *out;
+  uint64_t *ws;
+};
 
 // the E elements of one thread from a row buffer (zeros past the row)
 template <int E, bool VEC4>
@@ -660,45 +685,246 @@ __device__ __forceinline__ void load_elems(__amdgpu_buffer_rsrc_t rb, unsigned f
   }
 }
 
-__device__ __forceinline__ void publish(uint64_t *slot, uint64_t encoded) {
-  __hip_atomic_store(slot, encoded, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void put_word(uint64_t *slot, uint64_t w) {
+  __hip_atomic_store(slot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint64_t enc64(double v) { return ~__builtin_bit_cast(uint64_t, v); }
-__device__ __forceinline__ double dec64(uint64_t w) { return __builtin_bit_cast(double, ~w); }
+__device__ __forceinline__ uint64_t get_word(const uint64_t *slot) {
+  return __hip_atomic_load(const_cast<uint64_t *>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t payload) {
+  return ((uint64_t)tag << 32) | payload;
+}
+__device__ __forceinline__ uint32_t hi32(double v) { return (uint32_t)(__builtin_bit_cast(uint64_t, v) >> 32); }
+__device__ __forceinline__ uint32_t lo32(double v) { return (uint32_t)__builtin_bit_cast(uint64_t, v); }
+__device__ __forceinline__ double from_words(uint32_t hi, uint32_t lo) {
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 
-// Poll slots[0..n) (this workgroup's threads share them) until each is
-// published; their raw words land in dst.  False on timeout.
-__device__ bool await_slots(uint64_t *slots, int n, uint64_t *dst) {
-  __shared__ int s_late;
-  if (threadIdx.x == 0) s_late = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    uint64_t w = 0;
-    for (int spin = 0; spin < kMwSpin; ++spin) {
-      w = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (w != 0) break;
+// One meeting: chunk c's `per` words lie at slots[c * per ..]; this
+// workgroup's own chunk `own` is not read (its payloads are set by the
+// caller).  Payloads of the words seen with the call's tag land in
+// pay[c * per + i]; miss[c] = 1 for a chunk with a word still missing after
+// the first read and `spin` more rounds (every word is missing for
+// spin < 0).  Each round issues all of a thread's reads before it checks
+// any.  Ends with a barrier.
+__device__ void gather_meeting(const uint64_t *slots, int G, int per, int own, uint32_t tag, int spin,
+                               uint32_t *pay, int *miss) {
+  const int tid = threadIdx.x, n = G * per;
+  for (int c = tid; c < G; c += kMwThreads) miss[c] = 0;
+  unsigned pending = 0;  // bit j: word tid + j * kMwThreads not seen yet
+#pragma unroll
+  for (int j = 0; j < kMwPollMax; ++j) {
+    const int i = tid + j * kMwThreads;
+    if (i < n && i / per != own) pending |= 1u << j;
+  }
+  if (spin >= 0) {
+    for (int round = 0;; ++round) {
+      uint64_t w[kMwPollMax];
+#pragma unroll
+      for (int j = 0; j < kMwPollMax; ++j) w[j] = (pending >> j & 1u) ? get_word(slots + tid + j * kMwThreads) : 0;
+#pragma unroll
+      for (int j = 0; j < kMwPollMax; ++j) {
+        if ((pending >> j & 1u) && (uint32_t)(w[j] >> 32) == tag) {
+          pay[tid + j * kMwThreads] = (uint32_t)w[j];
+          pending &= ~(1u << j);
+        }
+      }
+      if (!__syncthreads_or(pending != 0u) || round >= spin) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (w == 0) s_late = 1;
-    dst[i] = w;
   }
+  __syncthreads();  // the zeroed miss[] before any mark
+#pragma unroll
+  for (int j = 0; j < kMwPollMax; ++j)
+    if (pending >> j & 1u) miss[(tid + j * kMwThreads) / per] = 1;
   __syncthreads();
-  return s_late == 0;
 }
 
-// Sequential fp64 sum of the decoded words w[0..n) (n >= 1), in index
-// order, with the reads issued 16 at a time so their latencies overlap;
-// also the running sum before and after element j (when 0 <= j < n).
+// ---- statistics of the logits form (meeting A) ----
+// Two threads' (max, sum of 2^((y - max) log2 e)) merged.  Both products
+// are rounded before the add (no contraction), so the merge is commutative
+// bit for bit and every lane of a butterfly ends with the same pair.
+__device__ __forceinline__ void stat_merge(float &m, float &s, float m2, float s2) {
+#pragma clang fp contract(off)
+  const float mx = fmaxf(m, m2);
+  if (mx == -INFINITY) {
+    m = mx;
+    s = 0.0f;
+    return;
+  }
+  const float f1 = __builtin_amdgcn_exp2f((m - mx) * kMwLog2e);
+  const float f2 = __builtin_amdgcn_exp2f((m2 - mx) * kMwLog2e);
+  s = s * f1 + s2 * f2;
+  m = mx;
+}
+
+// Row r of the logits form: the target's rows 0..k, then the draft's 0..k-1.
+__device__ __forceinline__ const float *logit_row(const MwArgs &a, int64_t b, int r) {
+  return r <= a.k ? a.p + b * a.p_bs + (int64_t)r * a.p_rs : a.q + b * a.q_bs + (int64_t)(r - a.k - 1) * a.q_rs;
+}
+
+// Meeting A payloads of chunk gc, every logit row: pay[2r] = the max bits,
+// pay[2r + 1] = the sum bits (T > 0) or the index (T = 0).  RB rows are
+// loaded together.  Uses s_red; ends with a barrier.
+template <int E, bool VEC4>
+__device__ void chunk_stats(const MwArgs &a, int64_t b, int gc, int R, uint32_t *pay, float (*s_red)[4][2]) {
+#pragma clang fp contract(off)
+  constexpr int RB = E >= 32 ? 1 : 32 / E;  // rows per batch of loads
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const unsigned first = (unsigned)gc * (kMwThreads * E) + (unsigned)tid * E;
+  const float T = a.temperature;
+  for (int r0 = 0; r0 < R; r0 += RB) {
+    float v[RB][E];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (r0 + rb < R) {
+        load_elems<E, VEC4>(row_buffer(logit_row(a, b, r0 + rb), (unsigned)a.vocab), first, v[rb]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[rb][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float m = -INFINITY, s = 0.0f;
+      int idx = INT32_MAX;
+      if (T == 0.0f) {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          if (first + e < (unsigned)a.vocab) argmax_merge(m, idx, v[rb][e], (int)(first + e));
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) argmax_merge(m, idx, __shfl_xor(m, o, kWave), __shfl_xor(idx, o, kWave));
+      } else {
+        float y[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          y[e] = first + e < (unsigned)a.vocab ? (T == 1.0f ? v[rb][e] : v[rb][e] / T) : -INFINITY;
+          m = fmaxf(m, y[e]);
+        }
+        if (m != -INFINITY) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((y[e] - m) * kMwLog2e);
+        }
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) stat_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
+      }
+      if (lane == 0) {
+        s_red[rb][wave][0] = m;
+        s_red[rb][wave][1] = T == 0.0f ? __int_as_float(idx) : s;
+      }
+    }
+    __syncthreads();
+    if (tid < RB && r0 + tid < R) {
+      float m = s_red[tid][0][0], s = s_red[tid][0][1];
+      int idx = __float_as_int(s);
+      for (int w = 1; w < kMwThreads / kWave; ++w) {
+        if (T == 0.0f) argmax_merge(m, idx, s_red[tid][w][0], __float_as_int(s_red[tid][w][1]));
+        else stat_merge(m, s, s_red[tid][w][0], s_red[tid][w][1]);
+      }
+      pay[2 * (r0 + tid)] = __float_as_uint(m);
+      pay[2 * (r0 + tid) + 1] = T == 0.0f ? (uint32_t)idx : __float_as_uint(s);
+    }
+    __syncthreads();
+  }
+}
+
+// p (or q) of one element from its logit and its row's statistics: the
+// softmax 2^((y - M) log2 e) / S, rounded as exp2 times the rounded 1 / S;
+// at T = 0 the one-hot of the row's argmax index.
+__device__ __forceinline__ float prob_of(float l, int64_t i, float T, float M, float inv_or_idx) {
+#pragma clang fp contract(off)
+  if (T == 0.0f) return i == (int64_t)__float_as_int(inv_or_idx) ? 1.0f : 0.0f;
+  const float y = T == 1.0f ? l : l / T;
+  return __builtin_amdgcn_exp2f((y - M) * kMwLog2e) * inv_or_idx;
+}
+
+// This thread's elements of chunk gc of the residual row: x = max(0, p - q)
+// and p itself (both 0 past the row).  s_fin[r] holds logit row r's
+// (M, 1 / S) -- or (max, index) -- in the logits form.
+template <int E, bool VEC4, bool LOGITS>
+__device__ __forceinline__ void residual_elems(const MwArgs &a, int64_t b, int64_t n, int gc,
+                                               const float (*s_fin)[2], float (&x)[E], float (&pv)[E]) {
+#pragma clang fp contract(off)
+  const unsigned first = (unsigned)gc * (kMwThreads * E) + (unsigned)threadIdx.x * E;
+  float pr[E], qr[E];
+  if constexpr (LOGITS) {
+    load_elems<E, VEC4>(row_buffer(logit_row(a, b, (int)n), (unsigned)a.vocab), first, pr);
+    if (n < a.k) load_elems<E, VEC4>(row_buffer(logit_row(a, b, (int)(a.k + 1 + n)), (unsigned)a.vocab), first, qr);
+    const float Mp = s_fin[n][0], Ip = s_fin[n][1];
+    const float Mq = n < a.k ? s_fin[a.k + 1 + n][0] : 0.0f, Iq = n < a.k ? s_fin[a.k + 1 + n][1] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const bool in = first + e < (unsigned)a.vocab;
+      pr[e] = in ? prob_of(pr[e], first + e, a.temperature, Mp, Ip) : 0.0f;
+      qr[e] = in && n < a.k ? prob_of(qr[e], first + e, a.temperature, Mq, Iq) : 0.0f;
+    }
+  } else {
+    load_elems<E, VEC4>(row_buffer(a.p + b * a.p_bs + n * a.p_rs, (unsigned)a.vocab), first, pr);
+    if (n < a.k) load_elems<E, VEC4>(row_buffer(a.q + b * a.q_bs + n * a.q_rs, (unsigned)a.vocab), first, qr);
+    else
+#pragma unroll
+      for (int e = 0; e < E; ++e) qr[e] = 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float r = pr[e] - qr[e];
+    x[e] = r > 0.0f ? r : 0.0f;
+    pv[e] = pr[e];
+  }
+}
+
+// The chunk's residual sum (meeting B's value).
+template <int E>
+__device__ __forceinline__ double chunk_residual_sum(const float (&x)[E], double *scratch) {
+  double run = 0.0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) run += (double)x[e];
+  return block_sum(run, scratch);
+}
+
+// The chunk's elements divided by the residual total (p where it is 0) in
+// place, and L_g (meeting C's value); *excl receives the thread's exclusive
+// prefix within the chunk.
+template <int E>
+__device__ __forceinline__ double chunk_prefix(float (&x)[E], const float (&pv)[E], bool use_residual, float denom,
+                                               double *scratch, double *s_last, double *excl) {
+#pragma clang fp contract(off)
+  double run = 0.0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x[e] = use_residual ? x[e] / denom : pv[e];
+    run += (double)x[e];
+  }
+  double unused;
+  *excl = block_exclusive_scan(run, scratch, &unused);
+  if (threadIdx.x == kMwThreads - 1) {
+    double acc = *excl;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc += (double)x[e];
+    *s_last = acc;
+  }
+  __syncthreads();
+  const double last = *s_last;
+  __syncthreads();
+  return last;
+}
+
+// Sequential fp64 sum, in chunk order, of the values held as (hi, lo)
+// payload pairs pay[2i], pay[2i + 1]; also the running sum before and after
+// chunk j.
 struct Chain {
   double total, before, after;
 };
-__device__ __forceinline__ Chain chain_sum(const uint64_t *w, int n, int j) {
+__device__ __forceinline__ Chain chain_sum(const uint32_t *pay, int n, int j) {
   Chain r{0.0, 0.0, 0.0};
   double acc = 0.0;
   for (int i0 = 0; i0 < n; i0 += 16) {
     double v[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = dec64(w[min(i0 + i, n - 1)]);
+    for (int i = 0; i < 16; ++i) {
+      const int c = min(i0 + i, n - 1);
+      v[i] = from_words(pay[2 * c], pay[2 * c + 1]);
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const double next = i0 + i < n ? acc + v[i] : acc;
@@ -710,126 +936,184 @@ __device__ __forceinline__ Chain chain_sum(const uint64_t *w, int n, int j) {
   return r;
 }
 
-template <int E, bool VEC4>
-__global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(
-    const float *__restrict__ p, const float *__restrict__ q, int64_t p_bs, int64_t p_rs, int64_t q_bs,
-    int64_t q_rs, const int64_t *__restrict__ draft, const float *__restrict__ u_accept,
-    const float *__restrict__ u_residual, int64_t batch, int64_t k, int64_t vocab, int G,
-    int64_t *__restrict__ out, uint64_t *__restrict__ ws) {
+template <int E, bool VEC4, bool LOGITS>
+__global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) {
   __shared__ double scratch[kMwThreads / kWave + 1];
-  __shared__ uint64_t s_words[kMwMaxG];
+  __shared__ uint32_t s_pay[2 * kMwMaxR * kMwMaxG];  // one meeting's payloads
+  __shared__ int s_miss[kMwMaxG];
+  __shared__ float s_fin[LOGITS ? kMwMaxR : 1][2];   // per logit row: (M, 1 / S) or (max, index)
+  __shared__ float s_red[LOGITS ? (E >= 32 ? 1 : 32 / E) : 1][4][2];
+  __shared__ float s_px[LOGITS ? kMwMaxK : 1][2];     // p(x_t), q(x_t)
+  __shared__ int s_flag[LOGITS ? kMwMaxK : 1];        // bit 0: rejected, bit 1: bad draft
   __shared__ double s_last;
-  const int64_t b = blockIdx.x / G;
+  const int G = a.G;
+  const int64_t b = blockIdx.x / G, k = a.k, vocab = a.vocab;
   const int g = (int)(blockIdx.x % G);
   const int tid = threadIdx.x;
   constexpr int kChunk = kMwThreads * E;
-  const unsigned first = (unsigned)g * kChunk + (unsigned)tid * E;  // this thread's first element
-  uint64_t *row_ws = ws + b * kMwRowWords;
-  const float *p_b = p + b * p_bs;
-  const float *q_b = q + b * q_bs;
-  auto flag_late = [&]() {
-    if (tid == 0) __hip_atomic_store(reinterpret_cast<uint64_t *>(out + 2 * batch + b), 2ull, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-  };
-  // the last call's L of this chunk goes back to 0 before anything is published
-  if (tid == 0) publish(row_ws + kMwL + g, 0);
-  const float ur = u_residual[b];
+  uint64_t *row_ws = a.ws + kMwHead + b * kMwRowWords;
+  // the call's tag: the epoch before anyone arrives, plus one (never 0)
+  const uint64_t epoch = get_word(a.ws + 2);
+  const uint32_t tag = (uint32_t)(epoch % 0xFFFFFFFFull) + 1u;
+  const float ur = a.u_residual[b];
   __asm__ volatile("" ::"s"(ur));  // loaded now, not after a meeting
 
-  // 0. the accept count n and the bad-draft flag, the same in every thread
-  // (accept_stage's test, u * q(x) < p(x) as a product; an id outside the
-  // vocabulary is never read through)
   int64_t n = k, bad = 0;
-  for (int64_t t0 = 0; t0 < k; t0 += kMwUnroll) {
-    int64_t xs[kMwUnroll];
-    float pxs[kMwUnroll], qxs[kMwUnroll], us[kMwUnroll];
-#pragma unroll
-    for (int j = 0; j < kMwUnroll; ++j) {
-      xs[j] = -1;
-      if (t0 + j < k) xs[j] = draft[b * k + t0 + j];
-    }
-#pragma unroll
-    for (int j = 0; j < kMwUnroll; ++j) {
-      const int64_t t = t0 + j, x = xs[j];
-      pxs[j] = qxs[j] = us[j] = 0.0f;
-      if (t < k) us[j] = u_accept[b * k + t];
-      if (t < k && x >= 0 && x < vocab) {
-        pxs[j] = p_b[t * p_rs + x];
-        qxs[j] = q_b[t * q_rs + x];
+  if constexpr (LOGITS) {
+    // the drafted ids and their two logits, one thread per position, in
+    // flight during meeting A
+    const int R = (int)(2 * k + 1);
+    float lt = 0.0f, ld = 0.0f, uacc = 0.0f;
+    int64_t x = -1;
+    if (tid < k) {
+      x = a.draft[b * k + tid];
+      uacc = a.u_accept[b * k + tid];
+      if (x >= 0 && x < vocab) {
+        lt = logit_row(a, b, tid)[x];
+        ld = logit_row(a, b, (int)(k + 1 + tid))[x];
       }
     }
-#pragma unroll
-    for (int j = 0; j < kMwUnroll; ++j) {
-      const int64_t t = t0 + j, x = xs[j];
-      if (t >= k) break;
+    // A: this chunk's statistics, published; the other chunks', gathered
+    uint32_t *pay = s_pay;
+    chunk_stats<E, VEC4>(a, b, g, R, pay + 2 * R * g, s_red);
+    uint64_t *slots = row_ws + kMwA;
+    for (int i = tid; i < 2 * R; i += kMwThreads) put_word(slots + 2 * R * g + i, tagged(tag, pay[2 * R * g + i]));
+    gather_meeting(slots, G, 2 * R, g, tag, a.spin, pay, s_miss);
+    for (int c = 0; c < G; ++c)
+      if (s_miss[c]) chunk_stats<E, VEC4>(a, b, c, R, pay + 2 * R * c, s_red);
+    // every row's (M, 1 / S) -- or (max, index) -- folded in chunk order
+    if (tid < R) {
+#pragma clang fp contract(off)
+      float m = __uint_as_float(pay[2 * tid]), s = __uint_as_float(pay[2 * tid + 1]);
+      int idx = (int)pay[2 * tid + 1];
+      for (int c = 1; c < G; ++c) {
+        const float mc = __uint_as_float(pay[2 * R * c + 2 * tid]);
+        const uint32_t sc = pay[2 * R * c + 2 * tid + 1];
+        if (a.temperature == 0.0f) argmax_merge(m, idx, mc, (int)sc);
+        else stat_merge(m, s, mc, __uint_as_float(sc));
+      }
+      s_fin[tid][0] = m;
+      s_fin[tid][1] = a.temperature == 0.0f ? __int_as_float(idx) : 1.0f / s;
+    }
+    __syncthreads();
+    // the accept test of every position: u * q(x) < p(x)
+    if (tid < k) {
+      int f = 0;
       if (x < 0 || x >= vocab) {
-        bad = 1;
-        if (n == k) n = t;
-        continue;
+        f = 3;
+      } else {
+        const float px = prob_of(lt, x, a.temperature, s_fin[tid][0], s_fin[tid][1]);
+        const float qx = prob_of(ld, x, a.temperature, s_fin[k + 1 + tid][0], s_fin[k + 1 + tid][1]);
+        s_px[tid][0] = px;
+        s_px[tid][1] = qx;
+        f = (uacc * qx < px ? 0 : 1) | (qx > 0.0f ? 0 : 2);
       }
-      if (!(qxs[j] > 0.0f)) bad = 1;
-      if (n == k && !(us[j] * qxs[j] < pxs[j])) n = t;
+      s_flag[tid] = f;
+    }
+    __syncthreads();
+    for (int64_t t = 0; t < k; ++t) {
+      const int f = s_flag[t];
+      if (f & 2) bad = 1;
+      if (n == k && (f & 1)) n = t;
+    }
+  } else {
+    // the accept count n and the bad-draft flag, the same in every thread
+    // (accept_stage's test, u * q(x) < p(x) as a product; an id outside the
+    // vocabulary is never read through)
+    const float *p_b = a.p + b * a.p_bs, *q_b = a.q + b * a.q_bs;
+    for (int64_t t0 = 0; t0 < k; t0 += kMwUnroll) {
+      int64_t xs[kMwUnroll];
+      float pxs[kMwUnroll], qxs[kMwUnroll], us[kMwUnroll];
+#pragma unroll
+      for (int j = 0; j < kMwUnroll; ++j) {
+        xs[j] = -1;
+        if (t0 + j < k) xs[j] = a.draft[b * k + t0 + j];
+      }
+#pragma unroll
+      for (int j = 0; j < kMwUnroll; ++j) {
+        const int64_t t = t0 + j, x = xs[j];
+        pxs[j] = qxs[j] = us[j] = 0.0f;
+        if (t < k) us[j] = a.u_accept[b * k + t];
+        if (t < k && x >= 0 && x < vocab) {
+          pxs[j] = p_b[t * a.p_rs + x];
+          qxs[j] = q_b[t * a.q_rs + x];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kMwUnroll; ++j) {
+        const int64_t t = t0 + j, x = xs[j];
+        if (t >= k) break;
+        if (x < 0 || x >= vocab) {
+          bad = 1;
+          if (n == k) n = t;
+          continue;
+        }
+        if (!(qxs[j] > 0.0f)) bad = 1;
+        if (n == k && !(us[j] * qxs[j] < pxs[j])) n = t;
+      }
     }
   }
   if (g == 0 && tid == 0) {
-    out[b] = n;
-    out[2 * batch + b] = bad;
-  }
-  float pr[E], qr[E];  // this thread's elements of p[n] and q[n]
-  load_elems<E, VEC4>(row_buffer(p_b + n * p_rs, (unsigned)vocab), first, pr);
-  if (n < k) load_elems<E, VEC4>(row_buffer(q_b + n * q_rs, (unsigned)vocab), first, qr);
-  else
-#pragma unroll
-    for (int e = 0; e < E; ++e) qr[e] = 0.0f;
-
-  // 1. the chunk's residual sum
-  float x[E];
-  double run = 0.0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float r = pr[e] - qr[e];
-    x[e] = r > 0.0f ? r : 0.0f;
-    run += (double)x[e];
-  }
-  const double chunk_sum = block_sum(run, scratch);
-  if (tid == 0) {
-    __builtin_amdgcn_s_waitcnt(0);  // the L clear is acknowledged before any publish
-    publish(row_ws + g, enc64(chunk_sum));
-  }
-  if (!await_slots(row_ws, G, s_words)) {
-    flag_late();
-    return;
+    a.out[b] = n;
+    a.out[2 * a.batch + b] = bad;
   }
 
-  // 2. the total in chunk order, the quotients, L_g
-  const float total = (float)chain_sum(s_words, G, -1).total;
+  // B: the chunk's residual sum
+  float x[E], pv[E];  // this thread's residual elements and p, then the quotients
+  residual_elems<E, VEC4, LOGITS>(a, b, n, g, s_fin, x, pv);
+  {
+    const double sum = chunk_residual_sum(x, scratch);
+    if (tid == 0) {
+      s_pay[2 * g] = hi32(sum);
+      s_pay[2 * g + 1] = lo32(sum);
+      put_word(row_ws + kMwB + 2 * g, tagged(tag, hi32(sum)));
+      put_word(row_ws + kMwB + 2 * g + 1, tagged(tag, lo32(sum)));
+    }
+  }
+  gather_meeting(row_ws + kMwB, G, 2, g, tag, a.spin, s_pay, s_miss);
+  for (int c = 0; c < G; ++c) {
+    if (!s_miss[c]) continue;
+    float xc[E], pc[E];
+    residual_elems<E, VEC4, LOGITS>(a, b, n, c, s_fin, xc, pc);
+    const double sum = chunk_residual_sum(xc, scratch);
+    if (tid == 0) {
+      s_pay[2 * c] = hi32(sum);
+      s_pay[2 * c + 1] = lo32(sum);
+    }
+    __syncthreads();
+  }
+
+  // C: the total in chunk order, the quotients, L_g
+  const float total = (float)chain_sum(s_pay, G, -1).total;
   const float denom = total > FLT_MIN ? total : FLT_MIN;
   const bool use_residual = total > 0.0f;
-  run = 0.0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    x[e] = use_residual ? x[e] / denom : pr[e];  // p == q: p itself
-    run += (double)x[e];
+  __syncthreads();  // every thread has read meeting B's payloads
+  double excl;
+  {
+    const double L = chunk_prefix(x, pv, use_residual, denom, scratch, &s_last, &excl);
+    if (tid == 0) {
+      s_pay[2 * g] = hi32(L);
+      s_pay[2 * g + 1] = lo32(L);
+      put_word(row_ws + kMwC + 2 * g, tagged(tag, hi32(L)));
+      put_word(row_ws + kMwC + 2 * g + 1, tagged(tag, lo32(L)));
+    }
   }
-  double unused;
-  const double excl = block_exclusive_scan(run, scratch, &unused);
-  if (tid == kMwThreads - 1) {
-    double acc = excl;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc += (double)x[e];
-    s_last = acc;
+  gather_meeting(row_ws + kMwC, G, 2, g, tag, a.spin, s_pay, s_miss);
+  for (int c = 0; c < G; ++c) {
+    if (!s_miss[c]) continue;
+    float xc[E], pc[E];
+    residual_elems<E, VEC4, LOGITS>(a, b, n, c, s_fin, xc, pc);
+    double unused;
+    const double L = chunk_prefix(xc, pc, use_residual, denom, scratch, &s_last, &unused);
+    if (tid == 0) {
+      s_pay[2 * c] = hi32(L);
+      s_pay[2 * c + 1] = lo32(L);
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (tid == 0) publish(row_ws + kMwL + g, enc64(s_last));
-  if (!await_slots(row_ws + kMwL, G, s_words)) {
-    flag_late();
-    return;
-  }
-  // every reader of the chunk sums is past them: clear this chunk's
-  if (tid == 0) publish(row_ws + g, 0);
 
-  // 3. chunk bases, the target, the count in the chunk that holds it
-  const Chain chain = chain_sum(s_words, G, g);
+  // D: chunk bases, the target, the count in the chunk that holds it
+  const Chain chain = chain_sum(s_pay, G, g);
   const double c_lo = chain.before, c_hi = chain.after, c = chain.total;
   const float target = ur * (float)c;
   if ((float)c_lo <= target && target < (float)c_hi) {
@@ -841,9 +1125,19 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(
       if ((float)(c_lo + acc) <= target) ++cnt_le;
     }
     const int64_t idx = (int64_t)g * kChunk + (int64_t)block_sum((double)cnt_le, scratch);
-    if (tid == 0) out[batch + b] = idx < vocab - 1 ? idx : vocab - 1;
+    if (tid == 0) a.out[a.batch + b] = idx < vocab - 1 ? idx : vocab - 1;
   } else if (g == G - 1 && !(target < (float)c)) {
-    if (tid == 0) out[batch + b] = vocab - 1;  // no prefix exceeds the target
+    if (tid == 0) a.out[a.batch + b] = vocab - 1;  // no prefix exceeds the target
+  }
+  // arrive: the count only decides who advances the epoch -- the last to
+  // arrive, once every workgroup has read it
+  if (tid == 0) {
+    const uint64_t before = __hip_atomic_fetch_add(a.ws + (epoch & 1), 1ull, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    if (before == (uint64_t)gridDim.x - 1) {  // ready the next call's counter and tag
+      put_word(a.ws + ((epoch + 1) & 1), 0ull);
+      put_word(a.ws + 2, epoch + 1);
+    }
   }
 }
 
@@ -861,7 +1155,7 @@ __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64
 
 using namespace specdec;
 
-SPECDEC_API int specdec_abi_version(void) { return 14; }
+SPECDEC_API int specdec_abi_version(void) { return 15; }
 
 SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t rows, int64_t vocab,
                                       int64_t row_stride, float temperature, float *out,
@@ -906,18 +1200,20 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
   return launch_status();
 }
 
-// Grid of the many-CU accept-reject: E elements per thread, preferring 16
-// (12 chunks of a 49152 vocabulary, the fastest measured), then the next E
-// whose G chunks per row keep the grid within one workgroup per compute
-// unit; false when none fits (then one workgroup runs each row).
+// Grid of the many-CU accept-reject: E elements per thread, taken from
+// `choices` in order, the first whose G chunks per row keep the grid within
+// one workgroup per compute unit; false when none fits.  The probabilities
+// form prefers 16 (12 chunks of a 49152 vocabulary, the fastest measured at
+// batch 1 and 8); the logits form reads 2k+1 rows per chunk and prefers the
+// smallest chunks that fill the GPU.
 struct MwPlan {
   int E = 0, G = 0;
 };
 
-static bool plan_mw(int64_t batch, int64_t vocab, MwPlan &pl) {
+static bool plan_mw(int64_t batch, int64_t vocab, std::initializer_list<int> choices, MwPlan &pl) {
   const int cus = cu_count();
   if (cus <= 0) return false;
-  for (int E : {16, 24, 32, 48}) {
+  for (int E : choices) {
     const int64_t G = (vocab + (int64_t)kMwThreads * E - 1) / ((int64_t)kMwThreads * E);
     if (G > kMwMaxG || batch * G > cus) continue;
     pl.E = E;
@@ -927,22 +1223,25 @@ static bool plan_mw(int64_t batch, int64_t vocab, MwPlan &pl) {
   return false;
 }
 
-template <int E>
-static void launch_mw_e(bool vec4, int64_t batch, int G, hipStream_t s, const float *p, const float *q, int64_t p_bs,
-                        int64_t p_rs, int64_t q_bs, int64_t q_rs, const int64_t *draft, const float *ua,
-                        const float *ur, int64_t k, int64_t vocab, int64_t *out, uint64_t *ws) {
-  dim3 grid((unsigned)(batch * G)), block(kMwThreads);
-  if (vec4)
-    accept_reject_mw_kernel<E, true><<<grid, block, 0, s>>>(p, q, p_bs, p_rs, q_bs, q_rs, draft, ua, ur, batch, k,
-                                                             vocab, G, out, ws);
-  else
-    accept_reject_mw_kernel<E, false><<<grid, block, 0, s>>>(p, q, p_bs, p_rs, q_bs, q_rs, draft, ua, ur, batch, k,
-                                                              vocab, G, out, ws);
+template <int E, bool LOGITS>
+static void launch_mw_e(bool vec4, const MwArgs &a, hipStream_t s) {
+  dim3 grid((unsigned)(a.batch * a.G)), block(kMwThreads);
+  if (vec4) accept_reject_mw_kernel<E, true, LOGITS><<<grid, block, 0, s>>>(a);
+  else accept_reject_mw_kernel<E, false, LOGITS><<<grid, block, 0, s>>>(a);
+}
+
+static int64_t mw_workspace_bytes(int64_t batch) { return (kMwHead + batch * kMwRowWords) * (int64_t)sizeof(uint64_t); }
+
+// 16-byte vectors when every row of p (and q) starts 16-byte aligned
+static bool mw_vec4(const void *p, const void *q, int64_t pb, int64_t pr, int64_t qb, int64_t qr, int64_t k,
+                    int64_t vocab) {
+  return vocab % 4 == 0 && pb % 4 == 0 && pr % 4 == 0 &&
+         (k == 0 || (qb % 4 == 0 && qr % 4 == 0 && ((uintptr_t)q & 15) == 0)) && ((uintptr_t)p & 15) == 0;
 }
 
 SPECDEC_API int specdec_accept_workspace(int64_t batch, int64_t *bytes) {
   if (batch < 0 || !bytes) return SPECDEC_EINVAL;
-  *bytes = batch * kMwRowWords * (int64_t)sizeof(uint64_t);
+  *bytes = mw_workspace_bytes(batch);
   return SPECDEC_OK;
 }
 
@@ -952,7 +1251,7 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
                                       const int64_t *draft, const void *u_accept,
                                       const void *u_residual, int64_t batch, int64_t k,
                                       int64_t vocab, int64_t *out, void *workspace,
-                                      int64_t workspace_bytes, void *stream) {
+                                      int64_t workspace_bytes, int32_t spin, void *stream) {
   if (batch < 0 || k < 0 || vocab <= 0) return SPECDEC_EINVAL;
   if (vocab > (int64_t)kMaxTiles * kCdfPerThread * kAcceptThreads) return SPECDEC_EUNSUPPORTED;
   if (batch == 0) return SPECDEC_OK;
@@ -960,21 +1259,26 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
   dim3 grid((unsigned)batch), block(kAcceptThreads);
   hipStream_t s = as_stream(stream);
   MwPlan pl;
-  if (workspace && dtype == SPECDEC_F32 && plan_mw(batch, vocab, pl)) {
-    if (workspace_bytes < batch * kMwRowWords * (int64_t)sizeof(uint64_t) || ((uintptr_t)workspace & 7) != 0)
-      return SPECDEC_EINVAL;
-    const bool vec4 = vocab % 4 == 0 && p_batch_stride % 4 == 0 && p_row_stride % 4 == 0 &&
-                      (k == 0 || (q_batch_stride % 4 == 0 && q_row_stride % 4 == 0 && ((uintptr_t)q & 15) == 0)) &&
-                      ((uintptr_t)p & 15) == 0;
-    const float *fp = (const float *)p, *fq = (const float *)q;
-    const float *ua = (const float *)u_accept, *ur = (const float *)u_residual;
-    uint64_t *ws = (uint64_t *)workspace;
-    const int64_t pb = p_batch_stride, pr = p_row_stride, qb = q_batch_stride, qr = q_row_stride;
+  if (workspace && dtype == SPECDEC_F32 && plan_mw(batch, vocab, {16, 24, 32, 48}, pl)) {
+    if (workspace_bytes < mw_workspace_bytes(batch) || ((uintptr_t)workspace & 7) != 0) return SPECDEC_EINVAL;
+    MwArgs a{};
+    a.p = (const float *)p;
+    a.q = (const float *)q;
+    a.p_bs = p_batch_stride, a.p_rs = p_row_stride, a.q_bs = q_batch_stride, a.q_rs = q_row_stride;
+    a.draft = draft;
+    a.u_accept = (const float *)u_accept;
+    a.u_residual = (const float *)u_residual;
+    a.batch = batch, a.k = k, a.vocab = vocab, a.G = pl.G;
+    a.temperature = 1.0f;
+    a.spin = spin;
+    a.out = out;
+    a.ws = (uint64_t *)workspace;
+    const bool vec4 = mw_vec4(p, q, p_batch_stride, p_row_stride, q_batch_stride, q_row_stride, k, vocab);
     switch (pl.E) {
-      case 16: launch_mw_e<16>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
-      case 24: launch_mw_e<24>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
-      case 32: launch_mw_e<32>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
-      default: launch_mw_e<48>(vec4, batch, pl.G, s, fp, fq, pb, pr, qb, qr, draft, ua, ur, k, vocab, out, ws); break;
+      case 16: launch_mw_e<16, false>(vec4, a, s); break;
+      case 24: launch_mw_e<24, false>(vec4, a, s); break;
+      case 32: launch_mw_e<32, false>(vec4, a, s); break;
+      default: launch_mw_e<48, false>(vec4, a, s); break;
     }
     return launch_status();
   }
@@ -1001,6 +1305,49 @@ SPECDEC_API int specdec_accept_reject(const void *p, const void *q, int dtype,
         vocab, out);
   } else {
     return SPECDEC_EINVAL;
+  }
+  return launch_status();
+}
+
+SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const void *draft_logits, int dtype,
+                                             int64_t t_batch_stride, int64_t t_row_stride,
+                                             int64_t d_batch_stride, int64_t d_row_stride, float temperature,
+                                             const int64_t *draft, const void *u_accept,
+                                             const void *u_residual, int64_t batch, int64_t k, int64_t vocab,
+                                             int64_t *out, void *workspace, int64_t workspace_bytes,
+                                             int32_t spin, void *stream) {
+  if (batch < 0 || k < 0 || vocab <= 0 || !(temperature >= 0.0f)) return SPECDEC_EINVAL;
+  if (batch == 0) return SPECDEC_OK;
+  if (!target_logits || !out || !u_residual || !workspace ||
+      (k > 0 && (!draft_logits || !draft || !u_accept)))
+    return SPECDEC_EINVAL;
+  if (dtype != SPECDEC_F32) return SPECDEC_EUNSUPPORTED;
+  if (workspace_bytes < mw_workspace_bytes(batch) || ((uintptr_t)workspace & 7) != 0) return SPECDEC_EINVAL;
+  if (k > kMwMaxK || vocab > INT32_MAX / 2 ||
+      !mw_vec4(target_logits, draft_logits, t_batch_stride, t_row_stride, d_batch_stride, d_row_stride, k, vocab))
+    return SPECDEC_EUNSUPPORTED;
+  MwPlan pl;
+  if (!plan_mw(batch, vocab, {4, 8, 16, 24, 32, 48}, pl)) return SPECDEC_EUNSUPPORTED;
+  MwArgs a{};
+  a.p = (const float *)target_logits;
+  a.q = (const float *)draft_logits;
+  a.p_bs = t_batch_stride, a.p_rs = t_row_stride, a.q_bs = d_batch_stride, a.q_rs = d_row_stride;
+  a.draft = draft;
+  a.u_accept = (const float *)u_accept;
+  a.u_residual = (const float *)u_residual;
+  a.batch = batch, a.k = k, a.vocab = vocab, a.G = pl.G;
+  a.temperature = temperature;
+  a.spin = spin;
+  a.out = out;
+  a.ws = (uint64_t *)workspace;
+  hipStream_t s = as_stream(stream);
+  switch (pl.E) {
+    case 4: launch_mw_e<4, true>(true, a, s); break;
+    case 8: launch_mw_e<8, true>(true, a, s); break;
+    case 16: launch_mw_e<16, true>(true, a, s); break;
+    case 24: launch_mw_e<24, true>(true, a, s); break;
+    case 32: launch_mw_e<32, true>(true, a, s); break;
+    default: launch_mw_e<48, true>(true, a, s); break;
   }
   return launch_status();
 }

@@ -643,11 +643,13 @@ attention_bf16_kernel(
         sk2[u] = kx[i + kD / 2];
       }
     }
+    // v token-fastest (task -> token task % width, dim task / width), the
+    // order its dim-major pool tile is stored in below
 #pragma unroll
     for (int u = 0; u < kVT; ++u) {
       const int task = tid0 + u * kThreads;
       if (task < a.width * kD) {
-        const int tk = task / kD, dd = task % kD;
+        const int tk = task % a.width, dd = task / a.width;
         svv[u] = qkv16[((int64_t)ti.b * a.width + tk) * a.q_stride + (int64_t)(a.H + a.Hkv + ti.h) * kD + dd];
       }
     }
@@ -693,6 +695,9 @@ attention_bf16_kernel(
   const int p0 = max(lo, ti.past), p1 = min(hi, ti.past + ti.nnew);
   const int n_in = max(p1 - p0, 0);
   const bool staged = MODE != 0 && a.rope && n_in <= kStage;
+  // tokens per dim in the staged v tasks' token-fastest order: the row's
+  // width when the values were loaded before the metadata (then p0 = past)
+  const int vw = pre_kv ? a.width : max(n_in, 1);
   __shared__ __align__(16) u16 s_nk[kStage][kD];
   __shared__ __align__(16) u16 s_nv[kStage][kD];
   // 16 waves: the LDS of finish_grouped, or of a tiled call's wave states
@@ -732,8 +737,9 @@ attention_bf16_kernel(
 #pragma unroll
     for (int u = 0; u < kVT; ++u) {
       const int task = tid + u * kThreads;
-      if (task < n_in * kD) {
-        const int pos = p0 + task / kD, dd = task % kD;
+      const int t = task % vw, dd = task / vw;  // token-fastest
+      if (task < vw * kD && t < n_in) {
+        const int pos = p0 + t;
         if (!pre_kv) svv[u] = new_row(pos)[(int64_t)(a.H + Hkv + ti.h) * kD + dd];
         svb[u] = trow[pos / bs];
       }
@@ -815,7 +821,6 @@ attention_bf16_kernel(
 
   if (staged) {
     u16 *kpw = const_cast<u16 *>(kp);
-    u16 *vpw = const_cast<u16 *>(vp);
 #pragma unroll
     for (int u = 0; u < kKT; ++u) {
       const int task = tid + u * kThreads;
@@ -838,13 +843,18 @@ attention_bf16_kernel(
         kd[i + kD / 2] = b2;
       }
     }
+    // V token-fastest: its pool tile is dim-major (a 32-byte row of 16
+    // slots per dim), so the lanes of one dim store consecutive slots of
+    // its row, not one token's dims 32 bytes apart in separate lanes
+    u16 *vpw = const_cast<u16 *>(vp);
 #pragma unroll
     for (int u = 0; u < kVT; ++u) {
       const int task = tid + u * kThreads;
-      if (task < n_in * kD) {
-        const int pos = p0 + task / kD, dd = task % kD;
+      const int t = task % vw, dd = task / vw;
+      if (task < vw * kD && t < n_in) {
+        const int pos = p0 + t;
         if (norm_in) svv[u] = scaled_bits(svv[u], s_tok[pos - ti.past]);
-        s_nv[pos - p0][dd] = svv[u];
+        s_nv[t][dd] = svv[u];
         vpw[((int64_t)svb[u] * Hkv + ti.h) * tile_elems + (int64_t)dd * bs + pos % bs] = svv[u];
       }
     }

@@ -95,9 +95,14 @@ __global__ void slot_map_kernel(const int32_t *__restrict__ tables, int64_t tabl
   }
 }
 
-// One thread per (token, head, rotation pair).  Heads [0, H) are queries,
-// [H, H+Hkv) keys, [H+Hkv, H+2Hkv) values (copied, not rotated).  Heads
-// below head0 are skipped (head0 = H: k and v only, q left as it is).
+// One thread per (token, q or k head, rotation pair), then one thread per
+// (row, v head, dim, token).  Heads [0, H) are queries, [H, H+Hkv) keys,
+// [H+Hkv, H+2Hkv) values (copied, not rotated).  Heads below head0 are
+// skipped (head0 = H: k and v only, q left as it is).  V's pool tile is
+// dim-major ([dim][slot], one 32-byte row of 16 slots per dim at block size
+// 16), so the value threads run token-fastest: the lanes of one dim write
+// consecutive slots of its row -- one run per (dim, block) -- instead of a
+// token's 64 dims landing 32 bytes apart in 64 separate lanes.
 template <typename T>
 __global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, int32_t H,
                                    int32_t Hkv, int32_t d, const float *__restrict__ cos_t,
@@ -106,10 +111,25 @@ __global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, in
                                    int64_t table_stride, int32_t bs, T *__restrict__ kpool,
                                    T *__restrict__ vpool, int32_t head0) {
   const int half = d / 2;
-  const int heads = H + 2 * Hkv - head0;
-  const int64_t total = (int64_t)batch * width * heads * half;
+  const int heads = H + Hkv - head0;  // rotated heads
+  const int64_t n_qk = (int64_t)batch * width * heads * half;
+  const int64_t total = n_qk + (int64_t)batch * Hkv * d * width;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
+    if (idx >= n_qk) {  // a value element: (row, v head, dim, token), token fastest
+      const int64_t j = idx - n_qk;
+      const int t = (int)(j % width);
+      const int c = (int)((j / width) % d);
+      const int h = (int)((j / ((int64_t)width * d)) % Hkv);
+      const int b = (int)(j / ((int64_t)width * d * Hkv));
+      const int32_t row = meta[b], past = meta[batch + b], n = meta[2 * batch + b];
+      if (t >= n) continue;  // right padding
+      const int64_t pos = past + t;
+      const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
+      vpool[((blk * Hkv + h) * d + c) * bs + pos % bs] =
+          qkv[((int64_t)b * width + t) * token_stride + (int64_t)(H + Hkv + h) * d + c];
+      continue;
+    }
     const int i = (int)(idx % half);
     const int head = head0 + (int)((idx / half) % heads);
     const int64_t tok = idx / ((int64_t)half * heads);
@@ -118,35 +138,18 @@ __global__ void rope_append_kernel(T *__restrict__ qkv, int64_t token_stride, in
     if (t >= n) continue;  // right padding
     const int64_t pos = past + t;
     T *x = qkv + tok * token_stride + (int64_t)head * d;
-    float x1 = to_f32(x[i]), x2 = to_f32(x[i + half]);
-    if (head < H + Hkv) {
-      // q*cos + rotate_half(q)*sin, each product and the sum rounded
-      // separately (rope_pair), cos/sin in fp32
-      float y1, y2;
-      rope_pair(x1, x2, cos_t[pos * half + i], sin_t[pos * half + i], y1, y2);
-      x1 = y1;
-      x2 = y2;
-      if (head < H) {
-        x[i] = from_f32<T>(x1);
-        x[i + half] = from_f32<T>(x2);
-        continue;
-      }
-    }
-    const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
-    const int off = (int)(pos % bs);
-    if (head < H + Hkv) {
-      const int h = head - H;
-      T *dst = kpool + ((blk * Hkv + h) * bs + off) * d;
-      const T v1 = from_f32<T>(x1), v2 = from_f32<T>(x2);
+    // q*cos + rotate_half(q)*sin, each product and the sum rounded
+    // separately (rope_pair), cos/sin in fp32
+    float y1, y2;
+    rope_pair(to_f32(x[i]), to_f32(x[i + half]), cos_t[pos * half + i], sin_t[pos * half + i], y1, y2);
+    const T v1 = from_f32<T>(y1), v2 = from_f32<T>(y2);
+    x[i] = v1;  // q rotated in place; the rotated key is kept in qkv as well
+    x[i + half] = v2;
+    if (head >= H) {
+      const int64_t blk = tables[(int64_t)row * table_stride + pos / bs];
+      T *dst = kpool + ((blk * Hkv + (head - H)) * bs + pos % bs) * d;
       dst[i] = v1;
       dst[i + half] = v2;
-      x[i] = v1;  // keep the rotated key in qkv as well
-      x[i + half] = v2;
-    } else {
-      const int h = head - H - Hkv;
-      T *dst = vpool + (blk * Hkv + h) * (int64_t)d * bs + off;
-      dst[(int64_t)i * bs] = x[i];
-      dst[(int64_t)(i + half) * bs] = x[i + half];
     }
   }
 }
@@ -301,7 +304,7 @@ int launch_rope_append(void *qkv, int dtype, int64_t token_stride, int32_t H, in
                        const int32_t *tables, int64_t table_stride, int32_t bs, void *k_pool, void *v_pool,
                        bool kv_only, hipStream_t s) {
   const int32_t head0 = kv_only ? H : 0;
-  const int64_t n = (int64_t)batch * width * (H + 2 * Hkv - head0) * (d / 2);
+  const int64_t n = (int64_t)batch * width * ((H + Hkv - head0) * (d / 2) + Hkv * d);
   dim3 grid(grid_for(n, 256)), block(256);
   if (dtype == SPECDEC_BF16) {
     rope_append_kernel<__hip_bfloat16><<<grid, block, 0, s>>>((__hip_bfloat16 *)qkv, token_stride, H, Hkv, d, cos_t,

@@ -120,9 +120,10 @@ def _accept_inputs(p, q, draft, u_accept) -> tuple[int, int]:
 
 
 class AcceptWorkspace:
-    """Zero-initialised, grow-only workspace of the many-CU accept-reject
-    (chunk sums and barrier counters; every call leaves it zeroed).  Calls
-    sharing one must be ordered on one stream."""
+    """Grow-only workspace of the many-CU accept-reject (arrival counters,
+    the call epoch and the meeting words), zeroed when it is allocated and
+    never cleared again: every word a call reads carries that call's tag.
+    Calls sharing one must be ordered on one stream."""
 
     def __init__(self, device: torch.device) -> None:
         self.device = device
@@ -137,9 +138,6 @@ class AcceptWorkspace:
             self.buf = torch.zeros(max(nbytes.value, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
         return self.buf
 
-    def reset(self) -> None:
-        self.buf.zero_()
-
 
 _accept_workspaces: dict[torch.device, AcceptWorkspace] = {}
 
@@ -151,17 +149,19 @@ def accept_workspace_for(device: torch.device) -> AcceptWorkspace:
     return ws
 
 
-# out[2] flag bit: a barrier of the many-CU accept kernel timed out
-ACCEPT_TIMEOUT = 2
+# Reads of the values a many-CU accept workgroup waits for, after its first,
+# before it computes the missing chunks itself (about a microsecond each).
+ACCEPT_SPIN = 1 << 14
 
 
 def accept_reject(p, q, draft, u_accept, u_residual, workspace: AcceptWorkspace | None = None,
-                  single: bool = False) -> torch.Tensor:
+                  single: bool = False, spin: int = ACCEPT_SPIN) -> torch.Tensor:
     """Fused accept + residual + inverse CDF; returns int64 [3, B] on the GPU:
-    n_accepted, next_token, and a flag (1: a drafted token with zero q(x) or
-    outside the vocabulary; 2: a barrier of the many-CU kernel timed out --
-    see check_accept_flags).  `single` asks for the one-workgroup-per-row
-    kernel (no workspace)."""
+    n_accepted, next_token, and a flag that is 1 for a drafted token with
+    zero q(x) or outside the vocabulary.  `single` asks for the
+    one-workgroup-per-row kernel (no workspace); `spin` bounds the waits of
+    the many-CU kernel (negative: none; every workgroup then computes the
+    other chunks' values itself, with the same bits)."""
     p, q = _rows3(gpu(p, "p")), _rows3(gpu(q, "q"))
     b, k = _accept_inputs(p, q, draft, u_accept)
     _on(p.device, u_residual, "u_residual", p.dtype, True, b)
@@ -173,19 +173,35 @@ def accept_reject(p, q, draft, u_accept, u_residual, workspace: AcceptWorkspace 
     st = lib().specdec_accept_reject(p.data_ptr(), q.data_ptr(), dtype_code(p), p.stride(0), p.stride(1),
                                      q.stride(0), q.stride(1), draft.data_ptr(), u_accept.data_ptr(),
                                      u_residual.data_ptr(), b, k, p.shape[-1], out.data_ptr(), ws_ptr, ws_bytes,
-                                     stream())
+                                     int(spin), stream())
     _check(st, "accept_reject")
     return out
 
 
-def check_accept_flags(flags: torch.Tensor, device: torch.device, workspace: AcceptWorkspace | None = None) -> None:
-    """Raise for the flags of an accept_reject call read back to the host: a
-    timed-out barrier (the workspace is zeroed again first) is a
-    RuntimeError; a bad draft is the reference's ValueError."""
-    if bool((flags & ACCEPT_TIMEOUT).any()):
-        (workspace or accept_workspace_for(device)).reset()
-        raise KernelError("accept_reject: a barrier of the many-CU kernel timed out (the workgroups of a row were "
-                          "not resident together); the workspace was reset")
+def accept_reject_logits(target_logits, draft_logits, temperature: float, draft, u_accept, u_residual,
+                         workspace: AcceptWorkspace | None = None, spin: int = ACCEPT_SPIN) -> torch.Tensor | None:
+    """probabilities() of the target [B, k+1, V] and draft [B, k, V] fp32
+    logits followed by accept_reject, in one launch that reads the logits
+    once; int64 [3, B] as accept_reject returns, or None when the shapes do
+    not fit the kernel (more than 16 drafted positions, rows that are not
+    16-byte aligned, too many rows for the GPU)."""
+    tl, dl = _rows3(gpu(target_logits, "target_logits")), _rows3(gpu(draft_logits, "draft_logits"))
+    if tl.dtype != torch.float32:
+        return None
+    b, k = _accept_inputs(tl, dl, draft, u_accept)
+    _on(tl.device, u_residual, "u_residual", tl.dtype, True, b)
+    if temperature < 0:
+        raise ValueError(f"temperature must be >= 0 (got {temperature})")
+    out = torch.empty(3, b, dtype=torch.int64, device=tl.device)
+    buf = (workspace or accept_workspace_for(tl.device)).reserve(b)
+    st = lib().specdec_accept_reject_logits(tl.data_ptr(), dl.data_ptr(), dtype_code(tl), tl.stride(0), tl.stride(1),
+                                            dl.stride(0), dl.stride(1), float(temperature), draft.data_ptr(),
+                                            u_accept.data_ptr(), u_residual.data_ptr(), b, k, tl.shape[-1],
+                                            out.data_ptr(), buf.data_ptr(), buf.numel(), int(spin), stream())
+    if st == EUNSUPPORTED:
+        return None
+    _check(st, "accept_reject_logits")
+    return out
 
 
 def accept_count(p, q, draft, u_accept) -> torch.Tensor:

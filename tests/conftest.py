@@ -15,11 +15,6 @@ def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line("markers", "gpu: runs HIP kernels; needs an MI355X (gfx950) GPU")
 
 
-def pytest_collection_modifyitems(config, items):
-    # GPU tests print the case they run, so a crash names it
-    pass
-
-
 @pytest.fixture(autouse=True)
 def _name_gpu_case(request):
     if request.node.get_closest_marker("gpu") is not None:

@@ -23,8 +23,8 @@ from pathlib import Path
 
 import torch
 
-sys.path.insert(0, str(Path(__file__).resolve().parents[2] / "speculative-decoder_amd"))
-from specdec.workloads import accept_inputs, planted_rows  # noqa: E402
+sys.path.insert(0, str(Path(__file__).resolve().parents[2]))
+from workloads import accept_inputs, planted_rows  # noqa: E402
 
 REF = Path("/root/reference")
 OUT = Path(__file__).resolve().parent

@@ -1,4 +1,5 @@
 """Accept-reject kernels vs the oracle and the reference's known answers."""
+import dataclasses
 from fractions import Fraction
 
 import pytest
@@ -8,7 +9,7 @@ import oracle.accept as oa
 import oracle.sampling as osamp
 from helpers import golden
 from lm.sampling import probabilities
-from spec.accept import accept_reject, residual_distribution, sample_inverse_cdf
+from spec.accept import Verdict, accept_reject, host_draft, residual_distribution, sample_inverse_cdf
 
 pytestmark = pytest.mark.gpu
 V = 49152
@@ -96,7 +97,10 @@ def test_scripted_uniforms():
     accepted = run(0.6, 0.5)
     assert accepted.n_accepted.item() == 1 and accepted.next_token.item() == 1
     # the draft comes back with the verdict, as host int64 [B, k]
-    assert accepted.draft.device.type == "cpu" and torch.equal(accepted.draft, draft)
+    assert host_draft(accepted).device.type == "cpu" and torch.equal(host_draft(accepted), draft)
+    # the verdict itself is the reference's two-field frozen dataclass
+    assert [f.name for f in dataclasses.fields(Verdict)] == ["n_accepted", "next_token"]
+    assert len(dataclasses.astuple(accepted)) == 2
     rejected = run(0.7, 0.8)
     assert rejected.n_accepted.item() == 0 and rejected.next_token.item() == 1
     assert run(0.7, 0.5).next_token.item() == 0
@@ -170,7 +174,7 @@ def test_draft_id_outside_vocab_raises(custom, bad_id):
 
 
 def _golden_inputs(case):
-    from specdec.workloads import accept_inputs
+    from workloads import accept_inputs
 
     dtype = getattr(torch, case["dtype"])
     if case["p"] is not None:

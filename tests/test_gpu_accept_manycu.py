@@ -1,5 +1,5 @@
 """The many-CU accept-reject kernel (each row spread over many workgroups of
-one launch meeting at two barriers) against the one-workgroup-per-row
+one launch that exchange chunk values twice) against the one-workgroup-per-row
 kernel and the oracle (spec/accept.py:44-79).  The two kernels add the
 residual and the prefix sums in fp64 in different orders, so a row may
 differ only where the oracle's 1e-6 exclusion band says the decision sits
@@ -82,9 +82,11 @@ def test_bad_draft_flag_and_out_of_range_ids():
 
 def test_workspace_reused_across_shapes_stays_exact():
     """One workspace, calls of different batch and vocab back to back: the
-    meeting slots are cleared as the calls go, so every call equals a fresh
-    one."""
+    meeting words of earlier calls carry earlier tags and are never read as
+    the current call's, so every call equals one on a fresh workspace, and
+    the epoch counts the calls."""
     ws = ops.AcceptWorkspace(torch.device("cuda"))
+    ws.reserve(64)  # sized once: a larger buffer would start a fresh epoch
     cases = [inputs(b, k, v, seed=s) for s, (b, k, v) in enumerate([(8, 4, 49152), (1, 4, 49152), (32, 8, 4099),
                                                                      (2, 2, 17), (64, 4, 49152)])]
     for rep in range(3):
@@ -93,10 +95,31 @@ def test_workspace_reused_across_shapes_stays_exact():
             got = ops.accept_reject(*dev, workspace=ws).cpu()
             fresh = ops.accept_reject(*dev, workspace=ops.AcceptWorkspace(torch.device("cuda"))).cpu()
             assert torch.equal(got, fresh), (rep, i)
-    # each row's chunk-sum slots (its first 64 words) were cleared by the call
-    # that used them; the L slots are cleared at the start of the next call
-    rows = ws.buf.view(torch.int64).view(-1, 128)
-    assert int(rows[:, :64].count_nonzero()) == 0
+    words = ws.buf.view(torch.int64)
+    assert int(words[2]) == 3 * len(cases)  # the epoch
+    assert int(words[(3 * len(cases)) % 2]) == 0  # the next call's arrival counter
+
+
+@pytest.mark.parametrize("spin", [-1, 0])
+@pytest.mark.parametrize("b,k,v", [(1, 4, 49152), (8, 4, 49152), (32, 8, 49152), (5, 8, 4099), (16, 9, 65536),
+                                   (3, 2, 1000)])
+def test_workgroups_that_stop_waiting_compute_the_same_bits(spin, b, k, v):
+    """spin < 0: no workgroup waits for any other, each computes every other
+    chunk's sums and prefixes itself; spin 0: one read, then the same for
+    whatever is missing.  Every kernel exits normally and the output has the
+    bits of the default, waiting path."""
+    p, q, draft, ua, ur = inputs(b, k, v, seed=b * 31 + k + v)
+    dev = [t.cuda().contiguous() for t in (p, q, draft, ua, ur)]
+    want = ops.accept_reject(*dev).cpu()
+    for rep in range(2):
+        got = ops.accept_reject(*dev, spin=spin).cpu()
+        assert torch.equal(got, want), (rep, got, want)
+    # and the bad-draft flag survives the recomputing path
+    q_bad = dev[1].clone()
+    q_bad[0, 0, dev[2][0, 0]] = 0.0
+    bad = ops.accept_reject(dev[0], q_bad, *dev[2:], spin=spin).cpu()
+    assert int(bad[2, 0]) == 1
+    assert torch.equal(bad, ops.accept_reject(dev[0], q_bad, *dev[2:]).cpu())
 
 
 def test_graph_replays_match_eager():

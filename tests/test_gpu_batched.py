@@ -1,9 +1,11 @@
-"""Batched sampled speculative decoding (8 rows, T = 0.8, k = 4 and 8, the
-135M-shaped model drafter and the n-gram drafter, 1024-token prompts with
-~30% planted repetition) against the oracle's restatement of the
+"""Batched sampled speculative decoding (8 and 32 rows, T = 0.8, k = 4 and 8,
+the 135M-shaped model drafter and the n-gram drafter, 1024-token prompts
+with ~30% planted repetition) against the oracle's restatement of the
 reference loop on the same fp32 weights: SmolLM2-1.7B layer shapes for the
 target and SmolLM2-135M shapes for the draft, two layers each so the CPU
-oracle finishes in seconds, vocab 49152.
+oracle finishes in seconds, vocab 49152.  The graphs' context buckets are
+shrunk to 1040 keys so that the 32 new tokens cross a bucket (a recapture
+at 2080 keys, five 512-key splits) as well as 16-token block boundaries.
 
 Every sampled decision of both runs is recorded: the first token (inverse
 CDF of the prefill's softmax), each draft token (inverse CDF of the draft
@@ -31,14 +33,16 @@ import oracle.kv as okv
 import oracle.loop as ol
 import spec.loop as loop
 from cache.kv import KVCache
+from lm import graphs
 from lm.model import SMOLLM2_135M, SMOLLM2_1_7B, Llama, random_state_dict
 from spec.draft import ModelDraft
 from spec.ngram import NGramDraft
-from specdec.workloads import planted_rows
+from workloads import planted_rows
 
 pytestmark = pytest.mark.gpu
 V = 49152
-B, PROMPT, NEW, T = 8, 1024, 32, 0.8
+PROMPT, NEW, T = 1024, 32, 0.8
+BUCKET = PROMPT + 16  # context bucket of the captured graphs in these tests
 REL = 1e-4  # fp32 forward tolerance (GPU vs CPU probabilities, decision margins)
 
 
@@ -145,10 +149,16 @@ def explain_round(g, c, k):
     return margins
 
 
-@pytest.mark.parametrize("drafter,k", [("model", 4), ("model", 8), ("ngram", 4), ("ngram", 8)])
-def test_batched_sampled_loop_matches_oracle(models, drafter, k):
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("B,drafter,k", [(8, "model", 4), (8, "model", 8), (8, "ngram", 4), (8, "ngram", 8),
+                                         (32, "model", 8), (32, "ngram", 8)])
+def test_batched_sampled_loop_matches_oracle(models, monkeypatch, B, drafter, k):
     (target, draft), (otarget, odraft) = models
     print(f"[case] batched sampled B={B} T={T} k={k} {drafter}", flush=True)
+    monkeypatch.setattr(graphs, "BUCKET", BUCKET)
+    buckets = set()
+    real_bucket_for = graphs.bucket_for
+    monkeypatch.setattr(graphs, "bucket_for", lambda m: buckets.add(real_bucket_for(m)) or real_bucket_for(m))
     prompts = planted_rows(B, PROMPT, V, seed=B * 100 + k)
     ts, ds = shapes()
     blocks = B * ((PROMPT + NEW + 2 * k + 32) // 16 + 2)
@@ -164,6 +174,7 @@ def test_batched_sampled_loop_matches_oracle(models, drafter, k):
                                                                                        torch.float32),
                                        cpu_drafter, prompts, k, seed=5)
     assert g_stats.rounds > 0
+    assert len(buckets) >= 2, buckets  # the run crossed a context bucket
 
     # first token
     gp, gu, gx = g_rec["first"]

@@ -7,16 +7,25 @@ fp32: GPU speculative decoding == GPU plain greedy decoding == the oracle's
 fp32 greedy decoding on the CPU (the reference's fp32 path restated).
 Speculative and plain decoding on the GPU must agree exactly (the verify
 rows are computed with the arithmetic of decode rows).  Against the oracle,
-a token may flip only where the two implementations' logits round the
-top-2 choice differently: at the first difference the decode steps' logits
-of both sides (same context) are compared, as the reference diagnoses its
-own flips (scripts/greedy_identity.py:43-57), and the test requires the
-top-2 gap there to be smaller than the largest logit difference between the
-two implementations.
+a token may flip only at a near-tie: at the first difference the decode
+steps' logits of both sides (same context) are compared, as the reference
+diagnoses its own flips (scripts/greedy_identity.py:43-57).  The fp32 bound
+is stated, not taken from the run: every logit of every step up to and
+including the flip agrees within FP32_REL * max|logit|, and a flip is
+allowed only where the oracle's top-2 gap is below that same bound.
 
-bf16: the same diagnosis for the GPU and CPU bf16 paths, whose GEMMs round
-differently (the reference flips 6 of 200 real-weight prompts in bf16 the
-same way, README.md:514-548)."""
+bf16: the same diagnosis for the GPU and CPU bf16 paths, whose GEMMs and
+bf16 rounding points differ (the reference flips 6 of 200 real-weight
+prompts in bf16 the same way, README.md:514-548).  A flip is allowed only
+where the top-2 gap is below BF16_ULPS bf16 ulps of the largest logit.
+
+With SPECDEC_IDENTITY_RECORD set to a directory, each test writes its
+diagnosis there as JSON (identical, or the flip's position, tokens, gaps
+and logit difference)."""
+import json
+import os
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -31,6 +40,8 @@ from spec.loop import generate
 
 pytestmark = pytest.mark.gpu
 V, PROMPT, NEW, K = 49152, 256, 32, 4
+FP32_REL = 1e-4  # fp32 accumulation-order differences, relative to the largest logit
+BF16_ULPS = 4.0  # bf16 rounding-point differences, in bf16 ulps of the largest logit
 
 
 def oracle_model(shape, state):
@@ -82,6 +93,13 @@ def diagnose(gpu_tokens, cpu_tokens, gpu_logits, cpu_logits):
             "gap_in_bf16_ulps": top2_gap(c) / ulp}
 
 
+def record(name: str, data: dict) -> None:
+    where = os.environ.get("SPECDEC_IDENTITY_RECORD")
+    if where:
+        Path(where).mkdir(parents=True, exist_ok=True)
+        (Path(where) / f"{name}.json").write_text(json.dumps(data, indent=1) + "\n")
+
+
 def run_both(monkeypatch, dtype):
     """GPU spec and plain greedy decoding, and the oracle's greedy decoding,
     of the same prompt with the same weights; the plain decoders' per-step
@@ -107,24 +125,32 @@ def run_both(monkeypatch, dtype):
 def test_fp32_full_size_spec_equals_plain_equals_oracle(monkeypatch):
     print("[case] full-size fp32 greedy identity 1.7B/135M shapes, prompt 256, 32 tokens", flush=True)
     spec_out, plain, ref, gl, cl, stats = run_both(monkeypatch, torch.float32)
+    d = diagnose(plain, ref, gl, cl)
+    n = len(gl) if d is None else d["position"] + 1
+    scale = max(c.abs().max().item() for c in cl[:n])
+    worst = max((g - c).abs().max().item() for g, c in zip(gl[:n], cl[:n]))
+    record("identity_full_fp32", {"tokens": NEW, "spec_equals_plain": spec_out == plain,
+                                  "equals_oracle": d is None, "first_difference": d, "steps_compared": n,
+                                  "max_abs_logit": scale, "max_logit_diff_up_to_flip": worst,
+                                  "bound": FP32_REL * scale, "rounds": stats.rounds})
+    print(f"[fp32] first difference against the oracle: {d}; worst logit diff {worst:.3e} (bound "
+          f"{FP32_REL * scale:.3e})")
     assert stats.rounds > 0
     assert spec_out == plain
-    d = diagnose(plain, ref, gl, cl)
-    print(f"[fp32] first difference against the oracle: {d}")
+    # every step's logits, the flip step's included, within the fp32 bound
+    assert worst < FP32_REL * scale, (worst, scale)
     if d is not None:
-        # a flip only where the implementations' logit difference exceeds the top-2 gap
-        assert d["cpu_top2_gap"] < d["max_logit_diff"], d
-    # the decode steps' logits agree within fp32 accumulation differences
-    n = len(gl) if d is None else d["position"] + 1
-    worst = max((g - c).abs().max().item() for g, c in zip(gl[:n], cl[:n]))
-    assert worst < 1e-3, worst
+        # a flip only at a near-tie of the oracle's top two
+        assert d["cpu_top2_gap"] < FP32_REL * scale, d
 
 
 def test_bf16_full_size_spec_equals_plain_and_flips_are_rounding(monkeypatch):
     print("[case] full-size bf16 greedy identity 1.7B/135M shapes, prompt 256, 32 tokens", flush=True)
     spec_out, plain, ref, gl, cl, stats = run_both(monkeypatch, torch.bfloat16)
-    assert spec_out == plain
     d = diagnose(plain, ref, gl, cl)
+    record("identity_full_bf16", {"tokens": NEW, "spec_equals_plain": spec_out == plain,
+                                  "equals_cpu_bf16": d is None, "first_difference": d, "rounds": stats.rounds})
     print(f"[bf16] first difference against the CPU bf16 path: {d}")
+    assert spec_out == plain
     if d is not None:
-        assert d["cpu_top2_gap"] < d["max_logit_diff"], d
+        assert d["gap_in_bf16_ulps"] < BF16_ULPS, d

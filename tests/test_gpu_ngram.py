@@ -7,7 +7,7 @@ import torch
 
 import oracle.ngram as on
 from helpers import golden
-from specdec.workloads import planted_rows
+from workloads import planted_rows
 from spec.ngram import NGramDraft, lookup, lookup_batch
 
 pytestmark = pytest.mark.gpu

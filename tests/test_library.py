@@ -71,3 +71,36 @@ def test_spin_wait_is_a_plain_request():
                          capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
     assert out.stdout.strip() in ("True", "False")
+
+
+def test_accept_entry_points_check_shapes_before_launch():
+    import ctypes
+
+    lib = _lib.load()
+    nbytes = ctypes.c_int64()
+    # arrival counters, the epoch and padding (16 words), then per row the
+    # meeting words: 2 + 2 per chunk, 2 per logit row (<= 33) and chunk, 64 chunks
+    assert lib.specdec_accept_workspace(3, ctypes.byref(nbytes)) == 0
+    assert nbytes.value == (16 + 3 * (4 * 64 + 2 * 33 * 64)) * 8
+    # the logits form: more than 16 drafted positions, or bf16 logits, are
+    # unsupported; a negative temperature is invalid (no pointer is touched)
+    fake, ws = 1 << 20, 1 << 24
+    args = lambda dtype, temp, k: (fake, fake, dtype, (k + 1) * 64, 64, k * 64, 64, temp, fake, fake, fake, 1, k, 64,
+                                   fake, ws, nbytes.value, 0, None)
+    assert lib.specdec_accept_reject_logits(*args(0, 1.0, 17)) == 3
+    assert lib.specdec_accept_reject_logits(*args(2, 1.0, 4)) == 3
+    assert lib.specdec_accept_reject_logits(*args(0, -1.0, 4)) == 1
+
+
+def test_verdict_is_the_reference_two_field_dataclass():
+    import dataclasses
+
+    import torch
+
+    from spec.accept import Verdict, host_draft
+
+    assert [f.name for f in dataclasses.fields(Verdict)] == ["n_accepted", "next_token"]
+    v = Verdict(torch.tensor([1]), torch.tensor([2]))
+    assert host_draft(v) is None and len(dataclasses.astuple(v)) == 2
+    with __import__("pytest").raises(dataclasses.FrozenInstanceError):
+        v.n_accepted = torch.tensor([0])

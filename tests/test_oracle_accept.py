@@ -7,7 +7,7 @@ import torch
 
 import oracle.accept as oa
 from helpers import golden
-from specdec.workloads import accept_inputs
+from workloads import accept_inputs
 
 P = [Fraction(4, 10), Fraction(3, 10), Fraction(2, 10), Fraction(1, 10), Fraction(0)]
 Q = [Fraction(1, 10), Fraction(2, 10), Fraction(3, 10), Fraction(1, 10), Fraction(3, 10)]

@@ -7,7 +7,7 @@ import torch
 
 import oracle.ngram as on
 from helpers import golden
-from specdec.workloads import planted_rows
+from workloads import planted_rows
 
 
 def brute(ctx, k, max_n):
