@@ -526,19 +526,26 @@ def bench_kernels(attention_grid=True):
         both = torch.cat([tl.view(-1, V), dl.view(-1, V)])
         us_soft = time_fn(lambda: ops.probabilities(both, 1.0), graph=True)
         us_acc = time_fn(lambda: ops.accept_reject(p, q, draft, ua, ur), graph=True)
+        # one launch from the logits: softmax, accept test, residual, sample
+        assert ops.accept_reject_logits(tl, dl, 1.0, draft, ua, ur) is not None
+        us_fused = time_fn(lambda: ops.accept_reject_logits(tl, dl, 1.0, draft, ua, ur), graph=True)
+        # a round's algorithmic bytes: the 2k+1 logit rows read once
         logit_bytes = (2 * k + 1) * V * 4 * b
-        # the accept kernel reads the rejected position's p and q rows (and
-        # gathers 2k probabilities): 2 V fp32 per batch entry
-        accept_bytes = 2 * V * 4 * b
-        log(f"accept b{b} k{k}: softmax {us_soft:.2f} us, accept {us_acc:.2f} us")
-        res[f"accept_b{b}_k{k}"] = {"softmax_us": us_soft, "accept_us": us_acc, "logit_bytes": logit_bytes,
-                                    "softmax_gbs": 2 * logit_bytes / us_soft / 1e3,
-                                    "softmax_frac_of_peak": 2 * logit_bytes / us_soft / 1e3 / HBM_PEAK_GBS,
-                                    "accept_bytes": accept_bytes, "accept_gbs": accept_bytes / us_acc / 1e3,
-                                    "accept_frac_of_peak": accept_bytes / us_acc / 1e3 / HBM_PEAK_GBS,
-                                    "round_us": us_soft + us_acc,
-                                    "round_frac_of_peak": (2 * logit_bytes + accept_bytes) / (us_soft + us_acc) / 1e3
-                                    / HBM_PEAK_GBS}
+        log(f"accept b{b} k{k}: softmax {us_soft:.2f} us + accept {us_acc:.2f} us; fused {us_fused:.2f} us")
+        res[f"accept_b{b}_k{k}"] = {
+            "round_bytes": logit_bytes,
+            "fused_us": us_fused, "fused_gbs": logit_bytes / us_fused / 1e3,
+            "fused_frac_of_peak": logit_bytes / us_fused / 1e3 / HBM_PEAK_GBS,
+            "softmax_us": us_soft, "accept_us": us_acc, "two_launch_us": us_soft + us_acc,
+            "two_launch_frac_of_peak": logit_bytes / (us_soft + us_acc) / 1e3 / HBM_PEAK_GBS,
+            # what the two kernels move themselves: the softmax reads the
+            # logits and writes p and q; the accept kernel reads the residual
+            # position's p and q rows (2 V fp32 per batch entry)
+            "softmax_traffic_gbs": 2 * logit_bytes / us_soft / 1e3,
+            "accept_traffic_gbs": 2 * V * 4 * b / us_acc / 1e3,
+            "what": "fused: specdec_accept_reject_logits (one launch from logits); two-launch: "
+                    "specdec_probabilities of the 2k+1 rows, then specdec_accept_reject; "
+                    "fractions over the logits read once"}
     # config 3: n-gram, B=16
     for length in (2048, 4096, 8192):
         rows = planted_rows(16, length, V, seed=length)
@@ -577,7 +584,7 @@ def bench_kernels(attention_grid=True):
     return res
 
 
-def bench_rollback(batch=8, length=1010):
+def bench_rollback(batch=8, length=1010, iters=100):
     """Config 2': one round's cache bookkeeping at batch 8 as the device sees
     it -- every row rolls back its rejected tail block (a push) and regrows
     one block for the next verify (a pop) -- i.e. one block-plan launch.
@@ -600,7 +607,7 @@ def bench_rollback(batch=8, length=1010):
     ent = torch.tensor(entries, dtype=torch.int32, device="cuda")
     top = alloc._dev_top
     us = time_fn(lambda: ops.block_plan(cache.table_tensor, alloc._stack, alloc._used, top, ent, batch, batch),
-                 graph=True)
+                 iters=iters, graph=True)
     # entries read + per block: table read, stack write, mark write (push);
     # stack read, table write, mark write (pop)
     nbytes = ent.numel() * 4 + batch * (4 + 4 + 1) * 2
@@ -629,7 +636,7 @@ class LoopTimer:
 
     def __init__(self, every: int = 32):
         self.every = every
-        self.accept, self.verify, self.attention = [], [], []
+        self.accept, self.verify, self.attention, self.draft = [], [], [], []
         # wall time spent outside the loop's own work: one-time graph
         # captures of new shapes, and the sampled attention replays
         self.excluded = 0.0
@@ -639,11 +646,28 @@ class LoopTimer:
         import lm.graphs as graphs
         from specdec import ops
 
-        self._ops, self._graphs = ops, graphs
+        import spec.draft as sd
+        import spec.ngram as sn
+
+        self._ops, self._graphs, self._drafters = ops, graphs, (sd.ModelDraft, sn.NGramDraft)
         self._real_accept = ops.accept_reject
         self._real_run = graphs.VerifyGraph.run
         self._real_capture = graphs._capture
+        self._real_propose = {cls: cls.propose for cls in self._drafters}
         timer = self
+
+        def timed_propose(real):
+            def propose(drafter, *a, **kw):
+                st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                st.record()
+                out = real(drafter, *a, **kw)
+                en.record()
+                timer.draft.append((st, en))
+                return out
+            return propose
+
+        for cls in self._drafters:
+            cls.propose = timed_propose(self._real_propose[cls])
 
         def accept(*a, **kw):
             st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -704,6 +728,8 @@ class LoopTimer:
         self.attention.append((st, en, layers, attention_bytes(b, past, t_new=width, h=h, hkv=hkv, d=d)))
 
     def __exit__(self, *exc):
+        for cls, real in self._real_propose.items():
+            cls.propose = real
         self._ops.accept_reject = self._real_accept
         self._graphs.VerifyGraph.run = self._real_run
         self._graphs._capture = self._real_capture
@@ -714,8 +740,13 @@ class LoopTimer:
         acc = [s.elapsed_time(e) * 1000 for s, e in self.accept]
         ver = [s.elapsed_time(e) * 1000 for s, e in self.verify]
         att = [(s.elapsed_time(e) * 1000 / n, nbytes) for s, e, n, nbytes in self.attention]
+        dra = [s.elapsed_time(e) * 1000 for s, e in self.draft]
         out = {"accept_kernel_us_per_round": {"mean": statistics.fmean(acc), "p50": pct(acc, 50), "p99": pct(acc, 99)},
-               "verify_us_per_round": {"mean": statistics.fmean(ver), "p50": pct(ver, 50), "p99": pct(ver, 99)}}
+               "verify_us_per_round": {"mean": statistics.fmean(ver), "p50": pct(ver, 50), "p99": pct(ver, 99)},
+               # the drafter's k steps (model: two graph replays; n-gram: the
+               # lookup launch, its history upload and the one-hot q), GPU
+               # time between events around propose()
+               "draft_us_per_round": {"mean": statistics.fmean(dra), "p50": pct(dra, 50), "p99": pct(dra, 99)}}
         if att:
             us = statistics.fmean(a for a, _ in att)
             nbytes = statistics.fmean(b for _, b in att)
@@ -991,26 +1022,111 @@ def cpu_kernel_baselines(seconds=1.0):
     return res
 
 
-def cpu_batched_baseline(tm, dm, batch=8, prompt_len=128, new_tokens=8, k=4, temperature=0.8):
-    """Config 5 on the host cores, bounded: the oracle loop at batch 8, k = 4,
-    T = 0.8, model drafter, on 128-token planted prompts for 8 new tokens."""
+class _Stop(Exception):
+    """Ends a loop once its measured rounds are in."""
+
+
+def cpu_batched_interleaved(target, draft, tm, dm, batch, k, kind, warmup_rounds=2, rounds=5, prompt_len=1024,
+                            temperature=0.8):
+    """Config 5 on the host cores at the config's own shapes: the oracle loop
+    (bf16, the reference's gather + SDPA forward and host accept-reject) and
+    the GPU loop on the same `batch` planted 1024-token prompts, k, T = 0.8,
+    the model or n-gram drafter, their rounds alternating one for one
+    (_Turns).  Each side stops after `warmup_rounds` + `rounds` rounds.  The
+    CPU side skips the prompt's prefill (32 x 1024 prompt tokens through the
+    1.7B shapes would take minutes on the host): its caches hold the prompt
+    length of zero K/V and its first token comes from seeded random logits,
+    so its rounds run the config's shapes -- contexts, batch, k, both
+    models' full depth -- on other values.  Per side: p50 / p99 round time
+    and emitted tokens/s over the measured rounds."""
+    import oracle.draft as od
     import oracle.kv as okv
     import oracle.loop as ol
-    from oracle.draft import ModelDraft as OModelDraft
+    import spec.loop as loop
+    from spec.draft import ModelDraft
+    from spec.ngram import NGramDraft
     from workloads import planted_rows
 
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     prompts = planted_rows(batch, prompt_len, V, seed=batch * 100 + k)
+    limit = warmup_rounds + rounds
+    new_tokens = 4 * limit + 8  # rows outlast the measured rounds (at least one token per round)
     blocks = batch * ((prompt_len + new_tokens + 2 * k + 2 * BLOCK) // BLOCK + 2)
-    t0 = time.perf_counter()
-    outs, stats = ol.generate(tm, okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16),
-                              OModelDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16)),
-                              prompts, new_tokens, k, temperature=temperature,
-                              generator=torch.Generator().manual_seed(5))
-    dt = time.perf_counter() - t0
-    return {"tokens_per_s": sum(len(o) for o in outs) / dt, "seconds": dt, "rounds": stats.rounds,
-            "mean_accept_len": mean_accept_len(stats),
-            "sample": f"{batch} rows, {prompt_len}-token planted prompts, {new_tokens} new tokens, T={temperature}, "
-                      f"k={k}, model drafter, bf16"}
+    turns = _Turns()
+    emitted = {"gpu": [], "cpu": []}
+    real = {"gpu": loop.accept_reject, "cpu": ol.accept_reject}
+    real_run = ol.run
+
+    def hooked(side):
+        def accept(p, q, draft_ids, generator=None, **kw):
+            v = real[side](p, q, draft_ids, generator=generator, **kw)
+            emitted[side].append(int(v.n_accepted.sum()) + len(v.n_accepted))
+            turns.hand_over(side)
+            if len(turns.rounds[side]) >= limit:
+                raise _Stop()
+            return v
+        return accept
+
+    def synthetic_prefill(model, cache, seq_ids, chunks):
+        cache.append(seq_ids, [len(c) for c in chunks])  # the pools start zeroed
+        return torch.randn(len(seq_ids), V, generator=torch.Generator().manual_seed(batch + k))
+
+    class SyntheticDraft(od.ModelDraft):
+        def prefill(self, seq_ids, prompts):
+            for s in seq_ids:
+                self.cache.add(s)
+            self.cache.append(seq_ids, [len(p) for p in prompts])
+
+    errors = []
+
+    def cpu_side():
+        try:
+            turns.start("cpu")
+            tc = okv.KVCache.for_model(tm.config, blocks, BLOCK, torch.bfloat16)
+            dr = (SyntheticDraft(dm, okv.KVCache.for_model(dm.config, blocks, BLOCK, torch.bfloat16))
+                  if kind == "model" else od.NGramDraft(V))
+            ol.generate(tm, tc, dr, prompts, new_tokens, k, temperature=temperature,
+                        generator=torch.Generator().manual_seed(5))
+        except _Stop:
+            pass
+        except BaseException as e:  # surfaced in the main thread
+            errors.append(e)
+        finally:
+            turns.finish("cpu")
+
+    loop.accept_reject, ol.accept_reject, ol.run = hooked("gpu"), hooked("cpu"), synthetic_prefill
+    worker = threading.Thread(target=cpu_side, daemon=True)
+    try:
+        tc, dc = caches_for(target, draft if kind == "model" else None, batch, prompt_len + new_tokens + 64, k)
+        drafter = ModelDraft(draft, dc) if kind == "model" else NGramDraft(V)
+        turns.start("gpu")
+        worker.start()
+        try:
+            loop.generate(target, tc, drafter, prompts, new_tokens, k=k, temperature=temperature,
+                          generator=torch.Generator().manual_seed(5))
+        except _Stop:
+            pass
+        turns.finish("gpu")
+        worker.join(timeout=900)
+    finally:
+        loop.accept_reject, ol.accept_reject, ol.run = real["gpu"], real["cpu"], real_run
+    if errors:
+        raise errors[0]
+    del tc, dc
+    torch.cuda.empty_cache()
+    out = {}
+    for side in ("gpu", "cpu"):
+        measured = turns.rounds[side][warmup_rounds:limit]
+        toks = emitted[side][warmup_rounds:limit]
+        out[side] = {"rounds": len(measured), "round_ms_p50": 1000 * pct(measured, 50),
+                     "round_ms_p99": 1000 * pct(measured, 99), "tokens_per_s": sum(toks) / sum(measured),
+                     "tokens_per_round": sum(toks) / max(len(toks), 1)}
+    out["speedup"] = out["gpu"]["tokens_per_s"] / out["cpu"]["tokens_per_s"]
+    out["sample"] = (f"{batch} rows, {prompt_len}-token planted prompts, k={k}, T={temperature}, {kind} drafter, "
+                     f"bf16; {warmup_rounds} warm-up + {rounds} measured rounds per side, interleaved one for one; "
+                     f"CPU side with zero prompt K/V instead of a prefill")
+    return out
 
 
 def kernel_speedups(kernels, ck, attn8, attn1, cpu_attn1, cpu_attn8):
@@ -1038,7 +1154,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--only", choices=["all", "e2e", "batched", "attention", "kernels", "small", "copy", "head"],
+    ap.add_argument("--only", choices=["all", "e2e", "batched", "batched-cpu", "attention", "kernels", "small", "copy",
+                                       "head", "rollback"],
                     default="all",
                     help="small: the kernels of configs 1-3 without the attention grid (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1090,6 +1207,19 @@ def main():
         target, draft, _, _ = build_models()
         print(json.dumps({"batched_sampled": bench_batched(target, draft, context=args.context)}))
         return
+    if args.only == "batched-cpu":
+        target, draft, t_state, d_state = build_models()
+        tm, dm = oracle_models(t_state, d_state)
+        out = {}
+        for b, k, kind in ((8, 4, "model"), (32, 8, "model"), (8, 4, "ngram"), (32, 8, "ngram")):
+            out[f"batched_b{b}_k{k}_{kind}"] = cpu_batched_interleaved(
+                target, draft, tm, dm, b, k, kind, warmup_rounds=2 if b <= 8 else 1, rounds=6 if b <= 8 else 4)
+            log(f"b{b} k{k} {kind}: {out[f'batched_b{b}_k{k}_{kind}']}")
+        print(json.dumps(out))
+        return
+    if args.only == "rollback":
+        print(json.dumps({"rollback_grow_b8": bench_rollback(iters=max(args.steps, 1) * 100)}))
+        return
 
     e2e, (target, draft, t_state, d_state, prompt, gpu_tokens) = bench_e2e(args.steps, args.warmup)
     log(f"e2e {e2e}")
@@ -1111,9 +1241,15 @@ def main():
         log("cpu baseline (rounds interleaved with the GPU loop)")
         rounds, extra = cpu_e2e_interleaved(target, draft, t_state, d_state, prompt)
         log(f"cpu rounds {rounds} {extra}")
+        tm, dm = oracle_models(t_state, d_state)
+        batched_cpu = {}
+        for b, k, kind in ((8, 4, "model"), (8, 4, "ngram"), (32, 8, "model"), (32, 8, "ngram")):
+            key = f"batched_b{b}_k{k}_{kind}"
+            batched_cpu[key] = cpu_batched_interleaved(target, draft, tm, dm, b, k, kind,
+                                                       warmup_rounds=2 if b <= 8 else 1, rounds=6 if b <= 8 else 4)
+            log(f"cpu {key}: {batched_cpu[key]}")
         del target, draft
         torch.cuda.empty_cache()
-        tm, dm = oracle_models(t_state, d_state)
         ck = cpu_kernel_baselines()
         log("cpu kernels done")
         cpu_attn1, cpu_attn8 = cpu_attention_baseline(), cpu_attention_baseline(batch=8)
@@ -1124,8 +1260,7 @@ def main():
                          f"3 warm-up rounds excluded, 20 measured; torch threads={extra['threads']}",
                "rounds": rounds, **extra,
                "steady_state_speedup": rounds["gpu"]["tokens_per_s"] / rounds["cpu"]["tokens_per_s"],
-               "attention_b1_L4096": cpu_attn1, "attention_b8_L4096": cpu_attn8, "kernels": ck,
-               "batched_b8_k4_model": cpu_batched_baseline(tm, dm)}
+               "attention_b1_L4096": cpu_attn1, "attention_b8_L4096": cpu_attn8, "kernels": ck, **batched_cpu}
         cpu["kernel_speedups"] = kernel_speedups(kernels, ck, attn, attn1, cpu_attn1, cpu_attn8)
         cpu["speedup"] = e2e["tokens_per_s"] / cpu["value"]
     line = {
