@@ -86,9 +86,11 @@ class _Request:
     output: list[int] = field(default_factory=list)
 
     def extend(self, tokens: list[int]) -> None:
-        # fresh lists: a drafter may hold on to the context it was shown
-        self.context = self.context + tokens
-        self.output = self.output + tokens
+        # in place: a drafter that keeps a device copy of the context (the
+        # n-gram drafter) sees the same list grow and uploads only the new
+        # tokens, a cost independent of the context's length
+        self.context.extend(tokens)
+        self.output.extend(tokens)
 
     def done(self, max_new_tokens: int, eos_id: int | None) -> bool:
         return len(self.output) >= max_new_tokens or (eos_id is not None and self.output[-1] == eos_id)
@@ -163,7 +165,7 @@ def generate(target, cache: KVCache, drafter: Drafter, prompts: list[list[int]],
         cache.add(s)
     firsts = sample(probabilities(run(target, cache, seq_ids, prompts), temperature), gen).tolist()
     event("first_token")
-    drafter.prefill(seq_ids, prompts)
+    drafter.prefill(seq_ids, [r.context for r in requests])  # the prompts, as the lists that will grow
     event("draft_prefilled")
     live = []
     for req, token in zip(requests, firsts):

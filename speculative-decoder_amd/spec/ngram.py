@@ -57,10 +57,15 @@ class _History:
     def sync(self, seq_ids: list[int], contexts: list[list[int]]) -> torch.Tensor:
         """Bring each sequence's device row up to its context; returns the
         int32 lengths [B] on the device.  Only the tokens past the row's are
-        uploaded when the context extends them: the same list as last time
-        (the round loop appends to it in place) whose token at the row's end
-        is unchanged, or another list whose prefix equals the row's tokens
-        (compared once, on the host).  Anything else is uploaded whole."""
+        uploaded when the context extends them.  The same list object as last
+        time (this package's round loop appends to its contexts in place) is
+        taken to have been appended to, which is checked at the row's last
+        token only: O(new tokens) host work per row, whatever the context's
+        length.  A different list (the reference's loop builds a new one each
+        round) is compared with the row's tokens on the host, O(length); a
+        list that does not extend them is uploaded whole.  A caller that
+        edits a context it passed before anywhere but at its end must pass a
+        new list, or release the sequence first."""
         need = max(len(c) for c in contexts)
         if need > self.buf.shape[1]:
             self._grow(self.buf.shape[0], max(need, 2 * self.buf.shape[1]))

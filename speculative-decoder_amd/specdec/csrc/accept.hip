@@ -651,7 +651,6 @@ constexpr int64_t kMwHead = 16;             // words before the rows: arrival co
 // a row's words: B (2 per chunk), C (2 per chunk), A (2 per logit row and chunk)
 constexpr int64_t kMwB = 0, kMwC = 2 * kMwMaxG, kMwA = 4 * kMwMaxG;
 constexpr int64_t kMwRowWords = kMwA + 2 * (int64_t)kMwMaxR * kMwMaxG;
-constexpr int kMwPollMax = (int)((2 * kMwMaxR * kMwMaxG + kMwThreads - 1) / kMwThreads);
 constexpr int kMwUnroll = 8;  // drafted positions whose scalar loads go out together
 constexpr float kMwLog2e = 1.4426950408889634f;
 
@@ -700,129 +699,179 @@ __device__ __forceinline__ double from_words(uint32_t hi, uint32_t lo) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
+// Arrival: the count only decides who advances the epoch -- the last
+// workgroup of the launch to arrive, when every workgroup has read it (a
+// workgroup's count goes to the counter of its epoch's parity, so its epoch
+// read has completed before it counts).  The fetch-add is issued before the
+// workgroup's first publish and its result used only at the end
+// (mw_advance), so its round trip overlaps the work; the next call, which
+// reads the new epoch, starts only after this one ends.
+__device__ __forceinline__ uint64_t mw_arrive(uint64_t *ws, uint64_t epoch) {
+  if (threadIdx.x != 0) return 0;
+  return __hip_atomic_fetch_add(ws + (epoch & 1), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void mw_advance(uint64_t *ws, uint64_t epoch, uint64_t before) {
+  if (threadIdx.x == 0 && before == (uint64_t)gridDim.x - 1) {  // ready the next call's counter and tag
+    __hip_atomic_store(ws + ((epoch + 1) & 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ws + 2, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // One meeting: chunk c's `per` words lie at slots[c * per ..]; this
 // workgroup's own chunk `own` is not read (its payloads are set by the
 // caller).  Payloads of the words seen with the call's tag land in
 // pay[c * per + i]; miss[c] = 1 for a chunk with a word still missing after
 // the first read and `spin` more rounds (every word is missing for
-// spin < 0).  Each round issues all of a thread's reads before it checks
-// any.  Ends with a barrier.
-__device__ void gather_meeting(const uint64_t *slots, int G, int per, int own, uint32_t tag, int spin,
+// spin < 0).  A thread reads up to kMwPoll words per pass, all issued
+// before any is checked; more words than kMwPoll * 256 take more passes.
+// Returns whether any chunk is missing (the same in every thread); ends
+// with a barrier.
+constexpr int kMwPoll = 4;
+__device__ bool gather_meeting(const uint64_t *slots, int G, int per, int own, uint32_t tag, int spin,
                                uint32_t *pay, int *miss) {
   const int tid = threadIdx.x, n = G * per;
+  bool late = false;
   for (int c = tid; c < G; c += kMwThreads) miss[c] = 0;
-  unsigned pending = 0;  // bit j: word tid + j * kMwThreads not seen yet
+  if (spin < 0) __syncthreads();  // otherwise the rounds' barriers order the zeroing before any mark
+  for (int i0 = 0; i0 < n; i0 += kMwPoll * kMwThreads) {
+    unsigned pending = 0;  // bit j: word i0 + tid + j * kMwThreads not seen yet
 #pragma unroll
-  for (int j = 0; j < kMwPollMax; ++j) {
-    const int i = tid + j * kMwThreads;
-    if (i < n && i / per != own) pending |= 1u << j;
-  }
-  if (spin >= 0) {
-    for (int round = 0;; ++round) {
-      uint64_t w[kMwPollMax];
-#pragma unroll
-      for (int j = 0; j < kMwPollMax; ++j) w[j] = (pending >> j & 1u) ? get_word(slots + tid + j * kMwThreads) : 0;
-#pragma unroll
-      for (int j = 0; j < kMwPollMax; ++j) {
-        if ((pending >> j & 1u) && (uint32_t)(w[j] >> 32) == tag) {
-          pay[tid + j * kMwThreads] = (uint32_t)w[j];
-          pending &= ~(1u << j);
-        }
-      }
-      if (!__syncthreads_or(pending != 0u) || round >= spin) break;
-      __builtin_amdgcn_s_sleep(1);
+    for (int j = 0; j < kMwPoll; ++j) {
+      const int i = i0 + tid + j * kMwThreads;
+      if (i < n && i / per != own) pending |= 1u << j;
     }
-  }
-  __syncthreads();  // the zeroed miss[] before any mark
+    if (spin >= 0) {
+      for (int round = 0;; ++round) {
+        uint64_t w[kMwPoll];
 #pragma unroll
-  for (int j = 0; j < kMwPollMax; ++j)
-    if (pending >> j & 1u) miss[(tid + j * kMwThreads) / per] = 1;
-  __syncthreads();
+        for (int j = 0; j < kMwPoll; ++j)
+          w[j] = (pending >> j & 1u) ? get_word(slots + i0 + tid + j * kMwThreads) : 0;
+#pragma unroll
+        for (int j = 0; j < kMwPoll; ++j) {
+          if ((pending >> j & 1u) && (uint32_t)(w[j] >> 32) == tag) {
+            pay[i0 + tid + j * kMwThreads] = (uint32_t)w[j];
+            pending &= ~(1u << j);
+          }
+        }
+        if (!__syncthreads_or(pending != 0u) || round >= spin) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kMwPoll; ++j)
+      if (pending >> j & 1u) miss[(i0 + tid + j * kMwThreads) / per] = 1;
+    late |= pending != 0u;
+  }
+  return __syncthreads_or(late);
 }
 
 // ---- statistics of the logits form (meeting A) ----
-// Two threads' (max, sum of 2^((y - max) log2 e)) merged.  Both products
-// are rounded before the add (no contraction), so the merge is commutative
-// bit for bit and every lane of a butterfly ends with the same pair.
-__device__ __forceinline__ void stat_merge(float &m, float &s, float m2, float s2) {
-#pragma clang fp contract(off)
-  const float mx = fmaxf(m, m2);
-  if (mx == -INFINITY) {
-    m = mx;
-    s = 0.0f;
-    return;
-  }
-  const float f1 = __builtin_amdgcn_exp2f((m - mx) * kMwLog2e);
-  const float f2 = __builtin_amdgcn_exp2f((m2 - mx) * kMwLog2e);
-  s = s * f1 + s2 * f2;
-  m = mx;
+// Row r of the logits form: the target's rows 0..k, then the draft's 0..k-1.
+// The bases are SSA values chosen by a select (selecting between two fields
+// of the argument struct would make the compiler index the struct in
+// scratch memory).
+__device__ __forceinline__ const float *logit_row(const float *t_b, const float *d_b, int64_t t_rs, int64_t d_rs,
+                                                  int64_t k, int r) {
+  return r <= k ? t_b + (int64_t)r * t_rs : d_b + (int64_t)(r - k - 1) * d_rs;
 }
 
-// Row r of the logits form: the target's rows 0..k, then the draft's 0..k-1.
-__device__ __forceinline__ const float *logit_row(const MwArgs &a, int64_t b, int r) {
-  return r <= a.k ? a.p + b * a.p_bs + (int64_t)r * a.p_rs : a.q + b * a.q_bs + (int64_t)(r - a.k - 1) * a.q_rs;
-}
+// Logit rows a thread loads at once in chunk_stats: the nine rows of k = 4
+// for E <= 16, else about 144 elements in flight per thread.
+constexpr int mw_rows_per_batch(int E) { return E <= 16 ? 9 : E >= 144 ? 1 : 144 / E; }
 
 // Meeting A payloads of chunk gc, every logit row: pay[2r] = the max bits,
 // pay[2r + 1] = the sum bits (T > 0) or the index (T = 0).  RB rows are
-// loaded together.  Uses s_red; ends with a barrier.
+// loaded together.  T > 0 takes two reductions per row, each in a fixed
+// order: the chunk's max M of y = l / T (wave_max_dpp, then the four
+// waves), then the sum of 2^((y - M) log2 e) over the chunk (each thread
+// its elements in order, wave_sum_dpp, then the waves in order).
+// Uses s_red; ends with a barrier.
+// The batch entry's rows are given as values (t_b, d_b: its first target
+// and draft rows), not through the argument struct, which would be copied
+// to scratch memory for the select between its fields.
 template <int E, bool VEC4>
-__device__ void chunk_stats(const MwArgs &a, int64_t b, int gc, int R, uint32_t *pay, float (*s_red)[4][2]) {
+__device__ __forceinline__ void chunk_stats(const float *t_b, const float *d_b, int64_t t_rs, int64_t d_rs, int64_t k,
+                                            int64_t vocab, float T, int gc, int R, uint32_t *pay,
+                                            float (*s_red)[4][2]) {
 #pragma clang fp contract(off)
-  constexpr int RB = E >= 32 ? 1 : 32 / E;  // rows per batch of loads
+  constexpr int RB = mw_rows_per_batch(E);  // rows whose loads are in flight together
+  constexpr int nw = kMwThreads / kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const unsigned first = (unsigned)gc * (kMwThreads * E) + (unsigned)tid * E;
-  const float T = a.temperature;
   for (int r0 = 0; r0 < R; r0 += RB) {
+    // every load unconditional (rows past R load row R - 1 again, unused):
+    // a row filled with zeros on one path and loaded on another made the
+    // compiler wait for each row's loads before the next row's went out
     float v[RB][E];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      if (r0 + rb < R) {
-        load_elems<E, VEC4>(row_buffer(logit_row(a, b, r0 + rb), (unsigned)a.vocab), first, v[rb]);
-      } else {
+    for (int rb = 0; rb < RB; ++rb)
+      load_elems<E, VEC4>(row_buffer(logit_row(t_b, d_b, t_rs, d_rs, k, min(r0 + rb, R - 1)), (unsigned)vocab), first,
+                          v[rb]);
+    if (T == 0.0f) {  // the max and its lowest index
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[rb][e] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float m = -INFINITY, s = 0.0f;
-      int idx = INT32_MAX;
-      if (T == 0.0f) {
+      for (int rb = 0; rb < RB; ++rb) {
+        float m = -INFINITY;
+        int idx = INT32_MAX;
 #pragma unroll
         for (int e = 0; e < E; ++e)
-          if (first + e < (unsigned)a.vocab) argmax_merge(m, idx, v[rb][e], (int)(first + e));
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) argmax_merge(m, idx, __shfl_xor(m, o, kWave), __shfl_xor(idx, o, kWave));
-      } else {
-        float y[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          y[e] = first + e < (unsigned)a.vocab ? (T == 1.0f ? v[rb][e] : v[rb][e] / T) : -INFINITY;
-          m = fmaxf(m, y[e]);
+          if (first + e < (unsigned)vocab) argmax_merge(m, idx, v[rb][e], (int)(first + e));
+        wave_argmax_dpp(m, idx);
+        if (lane == 0) {
+          s_red[rb][wave][0] = m;
+          s_red[rb][wave][1] = __int_as_float(idx);
         }
-        if (m != -INFINITY) {
-#pragma unroll
-          for (int e = 0; e < E; ++e) s += __builtin_amdgcn_exp2f((y[e] - m) * kMwLog2e);
-        }
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) stat_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
       }
-      if (lane == 0) {
-        s_red[rb][wave][0] = m;
-        s_red[rb][wave][1] = T == 0.0f ? __int_as_float(idx) : s;
+      __syncthreads();
+      if (tid < RB && r0 + tid < R) {
+        float m = s_red[tid][0][0];
+        int idx = __float_as_int(s_red[tid][0][1]);
+        for (int w = 1; w < nw; ++w) argmax_merge(m, idx, s_red[tid][w][0], __float_as_int(s_red[tid][w][1]));
+        pay[2 * (r0 + tid)] = __float_as_uint(m);
+        pay[2 * (r0 + tid) + 1] = (uint32_t)idx;
       }
+      __syncthreads();
+      continue;
+    }
+    // y = l / T (x / 1 is x exactly: no division at T = 1); -inf past the row
+    if (T != 1.0f) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[rb][e] = v[rb][e] / T;
+    }
+    float mt[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      mt[rb] = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (!(first + e < (unsigned)vocab)) v[rb][e] = -INFINITY;
+        mt[rb] = fmaxf(mt[rb], v[rb][e]);
+      }
+      mt[rb] = wave_max_dpp(mt[rb]);
+      if (lane == 0) s_red[rb][wave][0] = mt[rb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float m = s_red[rb][0][0];
+      for (int w = 1; w < nw; ++w) m = fmaxf(m, s_red[rb][w][0]);
+      float sum = 0.0f;
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) sum += __builtin_amdgcn_exp2f((v[rb][e] - m) * kMwLog2e);
+      }
+      sum = wave_sum_dpp(sum);
+      if (lane == 0) s_red[rb][wave][1] = sum;
     }
     __syncthreads();
     if (tid < RB && r0 + tid < R) {
-      float m = s_red[tid][0][0], s = s_red[tid][0][1];
-      int idx = __float_as_int(s);
-      for (int w = 1; w < kMwThreads / kWave; ++w) {
-        if (T == 0.0f) argmax_merge(m, idx, s_red[tid][w][0], __float_as_int(s_red[tid][w][1]));
-        else stat_merge(m, s, s_red[tid][w][0], s_red[tid][w][1]);
-      }
+      float sum = s_red[tid][0][1];
+      for (int w = 1; w < nw; ++w) sum += s_red[tid][w][1];
+      float m = s_red[tid][0][0];
+      for (int w = 1; w < nw; ++w) m = fmaxf(m, s_red[tid][w][0]);
       pay[2 * (r0 + tid)] = __float_as_uint(m);
-      pay[2 * (r0 + tid) + 1] = T == 0.0f ? (uint32_t)idx : __float_as_uint(s);
+      pay[2 * (r0 + tid) + 1] = __float_as_uint(sum);
     }
     __syncthreads();
   }
@@ -848,8 +897,8 @@ __device__ __forceinline__ void residual_elems(const MwArgs &a, int64_t b, int64
   const unsigned first = (unsigned)gc * (kMwThreads * E) + (unsigned)threadIdx.x * E;
   float pr[E], qr[E];
   if constexpr (LOGITS) {
-    load_elems<E, VEC4>(row_buffer(logit_row(a, b, (int)n), (unsigned)a.vocab), first, pr);
-    if (n < a.k) load_elems<E, VEC4>(row_buffer(logit_row(a, b, (int)(a.k + 1 + n)), (unsigned)a.vocab), first, qr);
+    load_elems<E, VEC4>(row_buffer(a.p + b * a.p_bs + n * a.p_rs, (unsigned)a.vocab), first, pr);
+    if (n < a.k) load_elems<E, VEC4>(row_buffer(a.q + b * a.q_bs + n * a.q_rs, (unsigned)a.vocab), first, qr);
     const float Mp = s_fin[n][0], Ip = s_fin[n][1];
     const float Mq = n < a.k ? s_fin[a.k + 1 + n][0] : 0.0f, Iq = n < a.k ? s_fin[a.k + 1 + n][1] : 0.0f;
 #pragma unroll
@@ -942,7 +991,8 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   __shared__ uint32_t s_pay[2 * kMwMaxR * kMwMaxG];  // one meeting's payloads
   __shared__ int s_miss[kMwMaxG];
   __shared__ float s_fin[LOGITS ? kMwMaxR : 1][2];   // per logit row: (M, 1 / S) or (max, index)
-  __shared__ float s_red[LOGITS ? (E >= 32 ? 1 : 32 / E) : 1][4][2];
+  __shared__ float s_terms[LOGITS ? kMwMaxR * kMwMaxG : 1];  // the fold's per-chunk terms
+  __shared__ float s_red[LOGITS ? mw_rows_per_batch(E) : 1][4][2];
   __shared__ float s_px[LOGITS ? kMwMaxK : 1][2];     // p(x_t), q(x_t)
   __shared__ int s_flag[LOGITS ? kMwMaxK : 1];        // bit 0: rejected, bit 1: bad draft
   __shared__ double s_last;
@@ -952,50 +1002,78 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   const int tid = threadIdx.x;
   constexpr int kChunk = kMwThreads * E;
   uint64_t *row_ws = a.ws + kMwHead + b * kMwRowWords;
-  // the call's tag: the epoch before anyone arrives, plus one (never 0)
-  const uint64_t epoch = get_word(a.ws + 2);
+  // the call's tag: the epoch before anyone arrives (mw_arrive), plus one
+  // (never 0).  A plain load: the epoch changes only between launches (the
+  // last arrival of the previous call wrote it), and a launch sees what the
+  // launches before it on the stream wrote.
+  typedef const __attribute__((address_space(4))) uint64_t const_u64;
+  const uint64_t epoch = ((const_u64 *)a.ws)[2];  // a scalar load: no vector-memory wait
   const uint32_t tag = (uint32_t)(epoch % 0xFFFFFFFFull) + 1u;
-  const float ur = a.u_residual[b];
+  // inputs read through the constant address space: scalar loads, which
+  // wait on their own counter, not behind the vector loads
+  typedef const __attribute__((address_space(4))) float const_f32;
+  typedef const __attribute__((address_space(4))) int64_t const_i64;
+  const float ur = ((const_f32 *)a.u_residual)[b];
   __asm__ volatile("" ::"s"(ur));  // loaded now, not after a meeting
 
+  uint64_t arrived = 0;  // thread 0: the arrival count before this workgroup's
   int64_t n = k, bad = 0;
   if constexpr (LOGITS) {
-    // the drafted ids and their two logits, one thread per position, in
-    // flight during meeting A
     const int R = (int)(2 * k + 1);
+    // A: this chunk's statistics, published; the other chunks', gathered
+    uint32_t *pay = s_pay;
+    const float *t_b = a.p + b * a.p_bs, *d_b = a.q + b * a.q_bs;
+    chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, g, R, pay + 2 * R * g, s_red);
+    arrived = mw_arrive(a.ws, epoch);
+    uint64_t *slots = row_ws + kMwA;
+    for (int i = tid; i < 2 * R; i += kMwThreads) put_word(slots + 2 * R * g + i, tagged(tag, pay[2 * R * g + i]));
+    // the drafted ids and their two logits, one thread per position, in
+    // flight during the meeting (loaded after the chunk's rows, so no wait
+    // for them comes before those loads)
     float lt = 0.0f, ld = 0.0f, uacc = 0.0f;
     int64_t x = -1;
     if (tid < k) {
       x = a.draft[b * k + tid];
       uacc = a.u_accept[b * k + tid];
       if (x >= 0 && x < vocab) {
-        lt = logit_row(a, b, tid)[x];
-        ld = logit_row(a, b, (int)(k + 1 + tid))[x];
+        lt = a.p[b * a.p_bs + tid * a.p_rs + x];
+        ld = a.q[b * a.q_bs + tid * a.q_rs + x];
       }
     }
-    // A: this chunk's statistics, published; the other chunks', gathered
-    uint32_t *pay = s_pay;
-    chunk_stats<E, VEC4>(a, b, g, R, pay + 2 * R * g, s_red);
-    uint64_t *slots = row_ws + kMwA;
-    for (int i = tid; i < 2 * R; i += kMwThreads) put_word(slots + 2 * R * g + i, tagged(tag, pay[2 * R * g + i]));
-    gather_meeting(slots, G, 2 * R, g, tag, a.spin, pay, s_miss);
-    for (int c = 0; c < G; ++c)
-      if (s_miss[c]) chunk_stats<E, VEC4>(a, b, c, R, pay + 2 * R * c, s_red);
-    // every row's (M, 1 / S) -- or (max, index) -- folded in chunk order
+    if (gather_meeting(slots, G, 2 * R, g, tag, a.spin, pay, s_miss))
+      for (int c = 0; c < G; ++c)
+        if (s_miss[c])
+          chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, c, R, pay + 2 * R * c, s_red);
+    // every row's (M, 1 / S) -- or (max, index) -- folded in chunk order:
+    // M = the chunks' max; S = the sum over chunks, in chunk order, of
+    // S_c 2^((M_c - M) log2 e), the terms computed one per thread
     if (tid < R) {
-#pragma clang fp contract(off)
-      float m = __uint_as_float(pay[2 * tid]), s = __uint_as_float(pay[2 * tid + 1]);
+      float m = __uint_as_float(pay[2 * tid]);
       int idx = (int)pay[2 * tid + 1];
       for (int c = 1; c < G; ++c) {
         const float mc = __uint_as_float(pay[2 * R * c + 2 * tid]);
-        const uint32_t sc = pay[2 * R * c + 2 * tid + 1];
-        if (a.temperature == 0.0f) argmax_merge(m, idx, mc, (int)sc);
-        else stat_merge(m, s, mc, __uint_as_float(sc));
+        if (a.temperature == 0.0f) argmax_merge(m, idx, mc, (int)pay[2 * R * c + 2 * tid + 1]);
+        else m = fmaxf(m, mc);
       }
       s_fin[tid][0] = m;
-      s_fin[tid][1] = a.temperature == 0.0f ? __int_as_float(idx) : 1.0f / s;
+      s_fin[tid][1] = __int_as_float(idx);
     }
     __syncthreads();
+    if (a.temperature != 0.0f) {
+#pragma clang fp contract(off)
+      for (int i = tid; i < R * G; i += kMwThreads) {
+        const int r = i / G, c = i - r * G;
+        const float mc = __uint_as_float(pay[2 * R * c + 2 * r]), sc = __uint_as_float(pay[2 * R * c + 2 * r + 1]);
+        s_terms[i] = mc == -INFINITY ? 0.0f : sc * __builtin_amdgcn_exp2f((mc - s_fin[r][0]) * kMwLog2e);
+      }
+      __syncthreads();
+      if (tid < R) {
+        float sum = 0.0f;
+        for (int c = 0; c < G; ++c) sum += s_terms[tid * G + c];
+        s_fin[tid][1] = 1.0f / sum;
+      }
+      __syncthreads();
+    }
     // the accept test of every position: u * q(x) < p(x)
     if (tid < k) {
       int f = 0;
@@ -1020,20 +1098,22 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
     // the accept count n and the bad-draft flag, the same in every thread
     // (accept_stage's test, u * q(x) < p(x) as a product; an id outside the
     // vocabulary is never read through)
-    const float *p_b = a.p + b * a.p_bs, *q_b = a.q + b * a.q_bs;
+    const_f32 *p_b = (const_f32 *)(a.p + b * a.p_bs), *q_b = (const_f32 *)(a.q + b * a.q_bs);
+    const_i64 *dr = (const_i64 *)(a.draft + b * k);
+    const_f32 *ua = (const_f32 *)(a.u_accept + b * k);
     for (int64_t t0 = 0; t0 < k; t0 += kMwUnroll) {
       int64_t xs[kMwUnroll];
       float pxs[kMwUnroll], qxs[kMwUnroll], us[kMwUnroll];
 #pragma unroll
       for (int j = 0; j < kMwUnroll; ++j) {
         xs[j] = -1;
-        if (t0 + j < k) xs[j] = a.draft[b * k + t0 + j];
+        if (t0 + j < k) xs[j] = dr[t0 + j];
       }
 #pragma unroll
       for (int j = 0; j < kMwUnroll; ++j) {
         const int64_t t = t0 + j, x = xs[j];
         pxs[j] = qxs[j] = us[j] = 0.0f;
-        if (t < k) us[j] = a.u_accept[b * k + t];
+        if (t < k) us[j] = ua[t];
         if (t < k && x >= 0 && x < vocab) {
           pxs[j] = p_b[t * a.p_rs + x];
           qxs[j] = q_b[t * a.q_rs + x];
@@ -1061,8 +1141,10 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   // B: the chunk's residual sum
   float x[E], pv[E];  // this thread's residual elements and p, then the quotients
   residual_elems<E, VEC4, LOGITS>(a, b, n, g, s_fin, x, pv);
+
   {
     const double sum = chunk_residual_sum(x, scratch);
+    if constexpr (!LOGITS) arrived = mw_arrive(a.ws, epoch);
     if (tid == 0) {
       s_pay[2 * g] = hi32(sum);
       s_pay[2 * g + 1] = lo32(sum);
@@ -1070,8 +1152,8 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
       put_word(row_ws + kMwB + 2 * g + 1, tagged(tag, lo32(sum)));
     }
   }
-  gather_meeting(row_ws + kMwB, G, 2, g, tag, a.spin, s_pay, s_miss);
-  for (int c = 0; c < G; ++c) {
+  const bool late_b = gather_meeting(row_ws + kMwB, G, 2, g, tag, a.spin, s_pay, s_miss);
+  for (int c = 0; late_b && c < G; ++c) {
     if (!s_miss[c]) continue;
     float xc[E], pc[E];
     residual_elems<E, VEC4, LOGITS>(a, b, n, c, s_fin, xc, pc);
@@ -1098,8 +1180,8 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
       put_word(row_ws + kMwC + 2 * g + 1, tagged(tag, lo32(L)));
     }
   }
-  gather_meeting(row_ws + kMwC, G, 2, g, tag, a.spin, s_pay, s_miss);
-  for (int c = 0; c < G; ++c) {
+  const bool late_c = gather_meeting(row_ws + kMwC, G, 2, g, tag, a.spin, s_pay, s_miss);
+  for (int c = 0; late_c && c < G; ++c) {
     if (!s_miss[c]) continue;
     float xc[E], pc[E];
     residual_elems<E, VEC4, LOGITS>(a, b, n, c, s_fin, xc, pc);
@@ -1129,16 +1211,7 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   } else if (g == G - 1 && !(target < (float)c)) {
     if (tid == 0) a.out[a.batch + b] = vocab - 1;  // no prefix exceeds the target
   }
-  // arrive: the count only decides who advances the epoch -- the last to
-  // arrive, once every workgroup has read it
-  if (tid == 0) {
-    const uint64_t before = __hip_atomic_fetch_add(a.ws + (epoch & 1), 1ull, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-    if (before == (uint64_t)gridDim.x - 1) {  // ready the next call's counter and tag
-      put_word(a.ws + ((epoch + 1) & 1), 0ull);
-      put_word(a.ws + 2, epoch + 1);
-    }
-  }
+  mw_advance(a.ws, epoch, arrived);
 }
 
 __global__ void one_hot_kernel(const int64_t *__restrict__ ids, int64_t n, int64_t vocab,
@@ -1227,7 +1300,7 @@ template <int E, bool LOGITS>
 static void launch_mw_e(bool vec4, const MwArgs &a, hipStream_t s) {
   dim3 grid((unsigned)(a.batch * a.G)), block(kMwThreads);
   if (vec4) accept_reject_mw_kernel<E, true, LOGITS><<<grid, block, 0, s>>>(a);
-  else accept_reject_mw_kernel<E, false, LOGITS><<<grid, block, 0, s>>>(a);
+  else if constexpr (!LOGITS) accept_reject_mw_kernel<E, false, LOGITS><<<grid, block, 0, s>>>(a);
 }
 
 static int64_t mw_workspace_bytes(int64_t batch) { return (kMwHead + batch * kMwRowWords) * (int64_t)sizeof(uint64_t); }
@@ -1327,7 +1400,7 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
       !mw_vec4(target_logits, draft_logits, t_batch_stride, t_row_stride, d_batch_stride, d_row_stride, k, vocab))
     return SPECDEC_EUNSUPPORTED;
   MwPlan pl;
-  if (!plan_mw(batch, vocab, {4, 8, 16, 24, 32, 48}, pl)) return SPECDEC_EUNSUPPORTED;
+  if (!plan_mw(batch, vocab, {8, 16, 24, 32, 48}, pl)) return SPECDEC_EUNSUPPORTED;
   MwArgs a{};
   a.p = (const float *)target_logits;
   a.q = (const float *)draft_logits;
@@ -1342,7 +1415,6 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
   a.ws = (uint64_t *)workspace;
   hipStream_t s = as_stream(stream);
   switch (pl.E) {
-    case 4: launch_mw_e<4, true>(true, a, s); break;
     case 8: launch_mw_e<8, true>(true, a, s); break;
     case 16: launch_mw_e<16, true>(true, a, s); break;
     case 24: launch_mw_e<24, true>(true, a, s); break;

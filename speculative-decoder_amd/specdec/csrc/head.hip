@@ -211,57 +211,6 @@ __device__ __forceinline__ void slice_logits(const HeadArgs &a, uint16_t *s_x, i
 // wave per hidden row, lane taking entries lane, lane + 64, ...; every
 // reduction has a fixed order, so the owner and any workgroup recomputing
 // the slice get the same bits.
-__device__ __forceinline__ void argmax_keep(float &best, int &best_i, float v, int i) {
-  if (v > best || (v == best && i < best_i)) {
-    best = v;
-    best_i = i;
-  }
-}
-
-// The same reductions through DPP row moves (xor 1, xor 2, the half-row and
-// row mirrors), then the four row results read into scalars and combined in
-// row order: every lane returns the same value, in a fixed order.
-template <int CTRL> __device__ __forceinline__ int dpp_move(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
-}
-
-template <int CTRL> __device__ __forceinline__ float dpp_max_step(float v) {
-  return fmaxf(v, __int_as_float(dpp_move<CTRL>(__float_as_int(v))));
-}
-
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = dpp_max_step<0xB1>(v);
-  v = dpp_max_step<0x4E>(v);
-  v = dpp_max_step<0x141>(v);
-  v = dpp_max_step<0x140>(v);
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
-template <int CTRL> __device__ __forceinline__ void dpp_argmax_step(float &best, int &best_i) {
-  const float ob = __int_as_float(dpp_move<CTRL>(__float_as_int(best)));
-  const int oi = dpp_move<CTRL>(best_i);
-  argmax_keep(best, best_i, ob, oi);
-}
-
-__device__ __forceinline__ void wave_argmax_dpp(float &best, int &best_i) {
-  dpp_argmax_step<0xB1>(best, best_i);
-  dpp_argmax_step<0x4E>(best, best_i);
-  dpp_argmax_step<0x141>(best, best_i);
-  dpp_argmax_step<0x140>(best, best_i);
-  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), 0));
-  int bi = __builtin_amdgcn_readlane(best_i, 0);
-#pragma unroll
-  for (int row = 1; row < 4; ++row)
-    argmax_keep(b, bi, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), 16 * row)),
-                __builtin_amdgcn_readlane(best_i, 16 * row));
-  best = b;
-  best_i = bi;
-}
-
 __device__ __forceinline__ float scaled(const HeadArgs &a, float l) {
   return a.temperature == 1.0f ? l : l / a.temperature;  // x / 1 is x
 }

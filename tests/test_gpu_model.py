@@ -159,6 +159,25 @@ def test_identical_batched(tiny, tiny_draft, prompts, expected, batch):
         assert out == expected[i:i + batch]
 
 
+@pytest.mark.parametrize("batch,k", [(1, 4), (2, 4), (3, 4), (1, 15)])
+def test_bf16_identical_while_every_projection_is_row_invariant(batch, k):
+    """bf16, calls of at most 16 rows (the verify's B * (k+1) and plain
+    decoding's B): every projection runs on specdec_linear, whose rows do not
+    depend on the other rows of the call, so speculative greedy decoding
+    emits plain greedy decoding's tokens at these batches too.  (Larger
+    verify calls run on hipBLASLt, whose bits depend on the call's row
+    count; there, as on the reference's GPU path, only fp32 is exact.)"""
+    model = tiny64(5, torch.bfloat16)
+    draft = early_exit(model)
+    ps = random_prompts(6, model.config.vocab_size, seed=11, low=20, high=40)
+    for i in range(0, len(ps), batch):
+        chunk = ps[i:i + batch]
+        want = cached_autoregressive.generate_batch(model, new_cache(model, 512, 16, torch.bfloat16), chunk, MAX_NEW)
+        out, _ = generate(model, new_cache(model, 512, 16, torch.bfloat16),
+                          ModelDraft(draft, new_cache(draft, 512, 16, torch.bfloat16)), chunk, MAX_NEW, k=k)
+        assert out == want, (batch, k, i)
+
+
 @pytest.mark.parametrize("k", [1, 2, 3, 8])
 def test_identical_across_draft_lengths(tiny, tiny_draft, prompts, expected, k):
     out, _ = generate(tiny, new_cache(tiny), ModelDraft(tiny_draft, new_cache(tiny_draft)), prompts[:16], MAX_NEW, k=k)
