@@ -49,8 +49,10 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 HOST_WAIT = "default"  # how the host waits for the GPU (main() may switch HIP to spinning)
 # HBM bytes per launch of the B=8, context-4096 verify attention (one tiled
-# launch): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention`,
-# each scaled by what the counter reads for a copy of known size.
+# launch): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention
+# --batch 8`, each scaled by what the counter reads for a copy of known size.
+# A stored figure from counter runs of the current kernel (hardware counters
+# cannot be read from inside this process); the line says so.
 ATTN_B8_TRAFFIC = 270_661_099
 V = 49152
 PROMPT = 256
@@ -1282,6 +1284,9 @@ def main():
                    "host_wait": HOST_WAIT},
         "roofline": {"bound": "hbm", "achieved": attn["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": ATTN_B8_TRAFFIC,
+                     "traffic_source": "stored: rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE runs of "
+                                       "`bench.py --only attention --batch 8` (x2.0 / x1.0, the factors a "
+                                       "256 MiB copy gives), not counters read during this run",
                      "kernel": "verify paged attention (attention_bf16_kernel<1, 16, true>: one 16-wave workgroup "
                                "per (row, kv head) tile taking its 512-token splits in rounds, no combine launch), "
                                "B=8, context 4096 (+5 appended), 32/32 heads x 64, bf16, block 16, K/V from HBM",
