@@ -53,7 +53,7 @@ HOST_WAIT = "default"  # how the host waits for the GPU (main() may switch HIP t
 # --batch 8`, each scaled by what the counter reads for a copy of known size.
 # A stored figure from counter runs of the current kernel (hardware counters
 # cannot be read from inside this process); the line says so.
-ATTN_B8_TRAFFIC = 270_661_099
+ATTN_B8_TRAFFIC = 270_692_966
 V = 49152
 PROMPT = 256
 NEW_TOKENS = 128
