@@ -775,9 +775,12 @@ __device__ __forceinline__ const float *logit_row(const float *t_b, const float 
   return r <= k ? t_b + (int64_t)r * t_rs : d_b + (int64_t)(r - k - 1) * d_rs;
 }
 
-// Logit rows a thread loads at once in chunk_stats: the nine rows of k = 4
-// for E <= 16, else about 144 elements in flight per thread.
-constexpr int mw_rows_per_batch(int E) { return E <= 16 ? 9 : E >= 144 ? 1 : 144 / E; }
+// Logit rows a thread loads at once in chunk_stats.  E = 8 and 16 run one
+// workgroup per compute unit and take the nine rows of k = 4 together; the
+// other widths run two per compute unit, which needs the kernel within 256
+// VGPRs: about 72 elements in flight per thread (nine rows at E = 16 take
+// 256 VGPRs and 152 AGPRs, and spill at E = 24).
+constexpr int mw_rows_per_batch(int E) { return E == 8 || E == 16 ? 9 : E >= 72 ? 1 : 72 / E; }
 
 // Meeting A payloads of chunk gc, every logit row: pay[2r] = the max bits,
 // pay[2r + 1] = the sum bits (T > 0) or the index (T = 0).  RB rows are
@@ -1275,20 +1278,26 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
 
 // Grid of the many-CU accept-reject: E elements per thread, taken from
 // `choices` in order, the first whose G chunks per row keep the grid within
-// one workgroup per compute unit; false when none fits.  The probabilities
-// form prefers 16 (12 chunks of a 49152 vocabulary, the fastest measured at
-// batch 1 and 8); the logits form reads 2k+1 rows per chunk and prefers the
-// smallest chunks that fill the GPU.
+// `per_cu` workgroups per compute unit; false when none fits.  The
+// probabilities form prefers 16 (12 chunks of a 49152 vocabulary, the
+// fastest measured at batch 1 and 8).  The logits form reads 2k+1 rows per
+// chunk: up to 21 rows of a 49152 vocabulary it takes one workgroup per
+// compute unit (E = 8, then 16), beyond that two, with narrower loads
+// (E = 12, 24, 32, 48), so that a compute unit's second workgroup loads
+// while the first reduces (batch 32, k = 8: 53.3 -> 44.6 us; batch 64:
+// 85 -> 66 us).  Every workgroup of a grid is resident at once when the
+// GPU is otherwise idle; when it is not, the meetings' fallback finishes
+// the call with the same bits.
 struct MwPlan {
   int E = 0, G = 0;
 };
 
-static bool plan_mw(int64_t batch, int64_t vocab, std::initializer_list<int> choices, MwPlan &pl) {
+static bool plan_mw(int64_t batch, int64_t vocab, std::initializer_list<int> choices, MwPlan &pl, int per_cu = 1) {
   const int cus = cu_count();
   if (cus <= 0) return false;
   for (int E : choices) {
     const int64_t G = (vocab + (int64_t)kMwThreads * E - 1) / ((int64_t)kMwThreads * E);
-    if (G > kMwMaxG || batch * G > cus) continue;
+    if (G > kMwMaxG || batch * G > (int64_t)per_cu * cus) continue;
     pl.E = E;
     pl.G = (int)G;
     return true;
@@ -1400,7 +1409,8 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
       !mw_vec4(target_logits, draft_logits, t_batch_stride, t_row_stride, d_batch_stride, d_row_stride, k, vocab))
     return SPECDEC_EUNSUPPORTED;
   MwPlan pl;
-  if (!plan_mw(batch, vocab, {8, 16, 24, 32, 48}, pl)) return SPECDEC_EUNSUPPORTED;
+  if (!plan_mw(batch, vocab, {8, 16}, pl) && !plan_mw(batch, vocab, {12, 24, 32, 48}, pl, 2))
+    return SPECDEC_EUNSUPPORTED;
   MwArgs a{};
   a.p = (const float *)target_logits;
   a.q = (const float *)draft_logits;
@@ -1416,6 +1426,7 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
   hipStream_t s = as_stream(stream);
   switch (pl.E) {
     case 8: launch_mw_e<8, true>(true, a, s); break;
+    case 12: launch_mw_e<12, true>(true, a, s); break;
     case 16: launch_mw_e<16, true>(true, a, s); break;
     case 24: launch_mw_e<24, true>(true, a, s); break;
     case 32: launch_mw_e<32, true>(true, a, s); break;

@@ -57,7 +57,8 @@ def check_vs_oracle(tl, dl, temperature, draft, ua, ur, got):
 
 @pytest.mark.parametrize("seed", range(4))
 @pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (1, 4, 0.8), (8, 4, 1.0), (8, 8, 0.8), (32, 8, 0.8),
-                                             (32, 4, 1.0), (3, 2, 1.3), (1, 1, 1.0), (2, 16, 0.8)])
+                                             (32, 4, 1.0), (3, 2, 1.3), (1, 1, 1.0), (2, 16, 0.8), (16, 4, 0.8),
+                                             (24, 8, 1.0), (48, 8, 0.8), (64, 4, 1.0)])
 def test_fused_matches_oracle(seed, b, k, temperature):
     tl, dl, g = logits(b, k, V, seed=seed * 101 + b * 7 + k)
     draft = drafts_from(dl, temperature, g)
@@ -84,7 +85,7 @@ def test_greedy_is_argmax_verification(b, k):
         assert int(got[0, r]) == n and int(got[1, r]) == int(targ[r, n])
 
 
-@pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (8, 4, 0.8), (32, 8, 0.8)])
+@pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (8, 4, 0.8), (32, 8, 0.8), (48, 8, 1.0)])
 def test_fused_matches_two_launch_gpu_path(b, k, temperature):
     """The same decisions as the softmax kernel followed by the many-CU
     accept kernel, except rows decided within 1e-6 of a threshold."""
@@ -102,7 +103,8 @@ def test_fused_matches_two_launch_gpu_path(b, k, temperature):
 
 
 @pytest.mark.parametrize("spin", [-1, 0])
-@pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (8, 8, 0.8), (32, 8, 0.8), (4, 4, 0.0)])
+@pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (8, 8, 0.8), (32, 8, 0.8), (4, 4, 0.0), (16, 4, 0.8),
+                                             (64, 4, 0.8)])
 def test_workgroups_that_stop_waiting_compute_the_same_bits(spin, b, k, temperature):
     """No workgroup waits (spin < 0), or each reads once (spin 0): every
     missing chunk's statistics, sums and prefixes are computed by the reader
