@@ -708,7 +708,15 @@ __device__ __forceinline__ double from_words(uint32_t hi, uint32_t lo) {
 // reads the new epoch, starts only after this one ends.
 __device__ __forceinline__ uint64_t mw_arrive(uint64_t *ws, uint64_t epoch) {
   if (threadIdx.x != 0) return 0;
-  return __hip_atomic_fetch_add(ws + (epoch & 1), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The counter's address passes through a VGPR the compiler cannot see
+  // into: for a uniform address it would rewrite the add as a wave-combined
+  // atomic whose result is spread to the lanes at once, waiting for the
+  // round trip here instead of where the count is first used.  The pointer
+  // is a global one: a generic pointer would make the add a flat atomic,
+  // which the compiler's wait counting treats as unordered with every load.
+  __attribute__((address_space(1))) uint64_t *counter = (__attribute__((address_space(1))) uint64_t *)(ws + (epoch & 1));
+  __asm__ volatile("" : "+v"(counter));
+  return __hip_atomic_fetch_add(counter, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void mw_advance(uint64_t *ws, uint64_t epoch, uint64_t before) {
   if (threadIdx.x == 0 && before == (uint64_t)gridDim.x - 1) {  // ready the next call's counter and tag
@@ -776,11 +784,11 @@ __device__ __forceinline__ const float *logit_row(const float *t_b, const float 
 }
 
 // Logit rows a thread loads at once in chunk_stats.  E = 8 and 16 run one
-// workgroup per compute unit and take the nine rows of k = 4 together; the
-// other widths run two per compute unit, which needs the kernel within 256
-// VGPRs: about 72 elements in flight per thread (nine rows at E = 16 take
-// 256 VGPRs and 152 AGPRs, and spill at E = 24).
-constexpr int mw_rows_per_batch(int E) { return E == 8 || E == 16 ? 9 : E >= 72 ? 1 : 72 / E; }
+// workgroup per compute unit and take the nine rows of k = 4 together; E =
+// 12 and 24 run two per compute unit, which needs the kernel within 256
+// VGPRs: 72 or 48 elements in flight per thread (nine rows at E = 16 take
+// 256 VGPRs and 163 AGPRs).
+constexpr int mw_rows_per_batch(int E) { return E == 8 || E == 16 ? 9 : E == 12 ? 6 : E >= 48 ? 1 : 48 / E; }
 
 // Meeting A payloads of chunk gc, every logit row: pay[2r] = the max bits,
 // pay[2r + 1] = the sum bits (T > 0) or the index (T = 0).  RB rows are
@@ -788,28 +796,31 @@ constexpr int mw_rows_per_batch(int E) { return E == 8 || E == 16 ? 9 : E >= 72 
 // order: the chunk's max M of y = l / T (wave_max_dpp, then the four
 // waves), then the sum of 2^((y - M) log2 e) over the chunk (each thread
 // its elements in order, wave_sum_dpp, then the waves in order).
-// Uses s_red; ends with a barrier.
+// Uses s_red; ends with a barrier.  `issued` runs once, right after the
+// first batch's loads go out (loads that depend on a value requested before
+// them are issued there, waiting only for that value).
 // The batch entry's rows are given as values (t_b, d_b: its first target
 // and draft rows), not through the argument struct, which would be copied
 // to scratch memory for the select between its fields.
-template <int E, bool VEC4>
+template <int E, bool VEC4, typename F>
 __device__ __forceinline__ void chunk_stats(const float *t_b, const float *d_b, int64_t t_rs, int64_t d_rs, int64_t k,
                                             int64_t vocab, float T, int gc, int R, uint32_t *pay,
-                                            float (*s_red)[4][2]) {
+                                            float (*s_red)[4][2], F &&issued) {
 #pragma clang fp contract(off)
   constexpr int RB = mw_rows_per_batch(E);  // rows whose loads are in flight together
   constexpr int nw = kMwThreads / kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const unsigned first = (unsigned)gc * (kMwThreads * E) + (unsigned)tid * E;
-  for (int r0 = 0; r0 < R; r0 += RB) {
-    // every load unconditional (rows past R load row R - 1 again, unused):
-    // a row filled with zeros on one path and loaded on another made the
-    // compiler wait for each row's loads before the next row's went out
-    float v[RB][E];
+  // every load unconditional (rows past R load row R - 1 again, unused):
+  // a row filled with zeros on one path and loaded on another made the
+  // compiler wait for each row's loads before the next row's went out
+  auto load = [&](int r0, float (&v)[RB][E]) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
       load_elems<E, VEC4>(row_buffer(logit_row(t_b, d_b, t_rs, d_rs, k, min(r0 + rb, R - 1)), (unsigned)vocab), first,
                           v[rb]);
+  };
+  auto reduce = [&](int r0, float (&v)[RB][E]) {
     if (T == 0.0f) {  // the max and its lowest index
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -833,7 +844,7 @@ __device__ __forceinline__ void chunk_stats(const float *t_b, const float *d_b, 
         pay[2 * (r0 + tid) + 1] = (uint32_t)idx;
       }
       __syncthreads();
-      continue;
+      return;
     }
     // y = l / T (x / 1 is x exactly: no division at T = 1); -inf past the row
     if (T != 1.0f) {
@@ -877,6 +888,17 @@ __device__ __forceinline__ void chunk_stats(const float *t_b, const float *d_b, 
       pay[2 * (r0 + tid) + 1] = __float_as_uint(sum);
     }
     __syncthreads();
+  };
+  // the first batch outside the loop: its loads follow the caller's
+  // straight-line code (no loop header in between, where every load still
+  // in flight would be waited for)
+  float v[RB][E];
+  load(0, v);
+  issued();
+  reduce(0, v);
+  for (int r0 = RB; r0 < R; r0 += RB) {
+    load(r0, v);
+    reduce(r0, v);
   }
 }
 
@@ -996,7 +1018,6 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   __shared__ float s_fin[LOGITS ? kMwMaxR : 1][2];   // per logit row: (M, 1 / S) or (max, index)
   __shared__ float s_terms[LOGITS ? kMwMaxR * kMwMaxG : 1];  // the fold's per-chunk terms
   __shared__ float s_red[LOGITS ? mw_rows_per_batch(E) : 1][4][2];
-  __shared__ float s_px[LOGITS ? kMwMaxK : 1][2];     // p(x_t), q(x_t)
   __shared__ int s_flag[LOGITS ? kMwMaxK : 1];        // bit 0: rejected, bit 1: bad draft
   __shared__ double s_last;
   const int G = a.G;
@@ -1006,18 +1027,47 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
   constexpr int kChunk = kMwThreads * E;
   uint64_t *row_ws = a.ws + kMwHead + b * kMwRowWords;
   // the call's tag: the epoch before anyone arrives (mw_arrive), plus one
-  // (never 0).  A plain load: the epoch changes only between launches (the
-  // last arrival of the previous call wrote it), and a launch sees what the
-  // launches before it on the stream wrote.
+  // (never 0).  Read once at the start: the epoch changes only between
+  // launches (the last arrival of the previous call wrote it), and a launch
+  // sees what the launches before it on the stream wrote.
   typedef const __attribute__((address_space(4))) uint64_t const_u64;
-  const uint64_t epoch = ((const_u64 *)a.ws)[2];  // a scalar load: no vector-memory wait
-  const uint32_t tag = (uint32_t)(epoch % 0xFFFFFFFFull) + 1u;
-  // inputs read through the constant address space: scalar loads, which
-  // wait on their own counter, not behind the vector loads
   typedef const __attribute__((address_space(4))) float const_f32;
   typedef const __attribute__((address_space(4))) int64_t const_i64;
-  const float ur = ((const_f32 *)a.u_residual)[b];
-  __asm__ volatile("" ::"s"(ur));  // loaded now, not after a meeting
+  uint64_t epoch;
+  float ur;
+  float lt = 0.0f, ld = 0.0f, uacc = 0.0f;  // logits form: position tid's inputs
+  int64_t xid = -1;
+  if constexpr (LOGITS) {
+    // The epoch, the residual's uniform and, one thread per position, the
+    // drafted id and its uniform are requested before the chunk's rows, as
+    // vector loads (atomic, so they are neither turned into scalar loads
+    // nor moved to their uses): they complete ahead of the rows, in order,
+    // so no round trip of their own comes before the rows' loads go out.
+    // The drafted ids' two logits follow the first batch of rows.  The
+    // addresses pass through VGPRs the compiler cannot see into, so the
+    // values stay in VGPRs: copying a uniform value to a scalar register
+    // would wait for it at once.
+    typedef const __attribute__((address_space(1))) uint64_t global_u64;
+    typedef const __attribute__((address_space(1))) uint32_t global_u32;
+    global_u64 *ep = (global_u64 *)(a.ws + 2);
+    global_u32 *up = (global_u32 *)a.u_residual + b;
+    __asm__ volatile("" : "+v"(ep), "+v"(up));
+    epoch = __hip_atomic_load(ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ur = __uint_as_float(__hip_atomic_load(up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (tid < k) {
+      xid = __hip_atomic_load(a.draft + b * k + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uacc = __uint_as_float(__hip_atomic_load((const uint32_t *)a.u_accept + b * k + tid, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+    }
+  } else {
+    // scalar loads through the constant address space, which wait on their
+    // own counter, not behind the vector loads; both in one round trip now,
+    // not after the chunk's work
+    epoch = ((const_u64 *)a.ws)[2];
+    ur = ((const_f32 *)a.u_residual)[b];
+    __asm__ volatile("" ::"s"(ur), "s"(epoch));
+  }
+  const uint32_t tag = (uint32_t)(epoch % 0xFFFFFFFFull) + 1u;
 
   uint64_t arrived = 0;  // thread 0: the arrival count before this workgroup's
   int64_t n = k, bad = 0;
@@ -1026,40 +1076,45 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
     // A: this chunk's statistics, published; the other chunks', gathered
     uint32_t *pay = s_pay;
     const float *t_b = a.p + b * a.p_bs, *d_b = a.q + b * a.q_bs;
-    chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, g, R, pay + 2 * R * g, s_red);
+    chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, g, R, pay + 2 * R * g, s_red, [&] {
+      // issued by every thread (a valid element where tid >= k or the id is
+      // out of range; those values go unused): loads under a branch would
+      // make the compiler wait for every load in flight where the paths
+      // join, the chunk's rows included
+      const bool mine = tid < k && xid >= 0 && xid < vocab;
+      const int64_t t = mine ? tid : 0, col = mine ? xid : 0;
+      const float *d_rows = k > 0 ? d_b : t_b;
+      const int64_t d_rs = k > 0 ? a.q_rs : a.p_rs;
+      lt = __uint_as_float(__hip_atomic_load((const uint32_t *)t_b + t * a.p_rs + col, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+      ld = __uint_as_float(__hip_atomic_load((const uint32_t *)d_rows + t * d_rs + col, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+    });
     arrived = mw_arrive(a.ws, epoch);
     uint64_t *slots = row_ws + kMwA;
     for (int i = tid; i < 2 * R; i += kMwThreads) put_word(slots + 2 * R * g + i, tagged(tag, pay[2 * R * g + i]));
-    // the drafted ids and their two logits, one thread per position, in
-    // flight during the meeting (loaded after the chunk's rows, so no wait
-    // for them comes before those loads)
-    float lt = 0.0f, ld = 0.0f, uacc = 0.0f;
-    int64_t x = -1;
-    if (tid < k) {
-      x = a.draft[b * k + tid];
-      uacc = a.u_accept[b * k + tid];
-      if (x >= 0 && x < vocab) {
-        lt = a.p[b * a.p_bs + tid * a.p_rs + x];
-        ld = a.q[b * a.q_bs + tid * a.q_rs + x];
-      }
-    }
     if (gather_meeting(slots, G, 2 * R, g, tag, a.spin, pay, s_miss))
       for (int c = 0; c < G; ++c)
         if (s_miss[c])
-          chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, c, R, pay + 2 * R * c, s_red);
-    // every row's (M, 1 / S) -- or (max, index) -- folded in chunk order:
-    // M = the chunks' max; S = the sum over chunks, in chunk order, of
-    // S_c 2^((M_c - M) log2 e), the terms computed one per thread
-    if (tid < R) {
-      float m = __uint_as_float(pay[2 * tid]);
-      int idx = (int)pay[2 * tid + 1];
-      for (int c = 1; c < G; ++c) {
-        const float mc = __uint_as_float(pay[2 * R * c + 2 * tid]);
-        if (a.temperature == 0.0f) argmax_merge(m, idx, mc, (int)pay[2 * R * c + 2 * tid + 1]);
-        else m = fmaxf(m, mc);
+          chunk_stats<E, VEC4>(t_b, d_b, a.p_rs, a.q_rs, k, vocab, a.temperature, c, R, pay + 2 * R * c, s_red,
+                               [] {});
+    // every row's (M, 1 / S) -- or (max, index) -- folded over the chunks:
+    // M = the chunks' max (one wave per row, lane c holding chunk c: a max,
+    // or a (max, lowest index) merge, has the same result in any order);
+    // S = the sum over chunks, in chunk order, of S_c 2^((M_c - M) log2 e),
+    // the terms computed one per thread
+    {
+      const int lane = tid & (kWave - 1);
+      for (int r = tid / kWave; r < R; r += kMwThreads / kWave) {
+        float m = lane < G ? __uint_as_float(pay[2 * R * lane + 2 * r]) : -INFINITY;
+        int idx = lane < G ? (int)pay[2 * R * lane + 2 * r + 1] : INT32_MAX;
+        if (a.temperature == 0.0f) wave_argmax_dpp(m, idx);
+        else m = wave_max_dpp(m);
+        if (lane == 0) {
+          s_fin[r][0] = m;
+          s_fin[r][1] = __int_as_float(idx);
+        }
       }
-      s_fin[tid][0] = m;
-      s_fin[tid][1] = __int_as_float(idx);
     }
     __syncthreads();
     if (a.temperature != 0.0f) {
@@ -1072,7 +1127,14 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
       __syncthreads();
       if (tid < R) {
         float sum = 0.0f;
-        for (int c = 0; c < G; ++c) sum += s_terms[tid * G + c];
+        for (int c0 = 0; c0 < G; c0 += 16) {  // each 16 terms read together, added in order
+          float t[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) t[i] = s_terms[tid * G + min(c0 + i, G - 1)];
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (c0 + i < G) sum += t[i];
+        }
         s_fin[tid][1] = 1.0f / sum;
       }
       __syncthreads();
@@ -1080,13 +1142,11 @@ __global__ __launch_bounds__(kMwThreads) void accept_reject_mw_kernel(MwArgs a) 
     // the accept test of every position: u * q(x) < p(x)
     if (tid < k) {
       int f = 0;
-      if (x < 0 || x >= vocab) {
+      if (xid < 0 || xid >= vocab) {
         f = 3;
       } else {
-        const float px = prob_of(lt, x, a.temperature, s_fin[tid][0], s_fin[tid][1]);
-        const float qx = prob_of(ld, x, a.temperature, s_fin[k + 1 + tid][0], s_fin[k + 1 + tid][1]);
-        s_px[tid][0] = px;
-        s_px[tid][1] = qx;
+        const float px = prob_of(lt, xid, a.temperature, s_fin[tid][0], s_fin[tid][1]);
+        const float qx = prob_of(ld, xid, a.temperature, s_fin[k + 1 + tid][0], s_fin[k + 1 + tid][1]);
         f = (uacc * qx < px ? 0 : 1) | (qx > 0.0f ? 0 : 2);
       }
       s_flag[tid] = f;
@@ -1283,11 +1343,11 @@ SPECDEC_API int specdec_probabilities(const void *logits, int dtype, int64_t row
 // fastest measured at batch 1 and 8).  The logits form reads 2k+1 rows per
 // chunk: up to 21 rows of a 49152 vocabulary it takes one workgroup per
 // compute unit (E = 8, then 16), beyond that two, with narrower loads
-// (E = 12, 24, 32, 48), so that a compute unit's second workgroup loads
-// while the first reduces (batch 32, k = 8: 53.3 -> 44.6 us; batch 64:
-// 85 -> 66 us).  Every workgroup of a grid is resident at once when the
-// GPU is otherwise idle; when it is not, the meetings' fallback finishes
-// the call with the same bits.
+// (E = 12, then 24: up to 64 rows on 256 compute units), so that a compute
+// unit's second workgroup loads while the first reduces (batch 32, k = 8:
+// 53.3 -> 44.6 us; batch 64: 85 -> 66 us).  Every workgroup of a grid is
+// resident at once when the GPU is otherwise idle; when it is not, the
+// meetings' fallback finishes the call with the same bits.
 struct MwPlan {
   int E = 0, G = 0;
 };
@@ -1409,7 +1469,7 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
       !mw_vec4(target_logits, draft_logits, t_batch_stride, t_row_stride, d_batch_stride, d_row_stride, k, vocab))
     return SPECDEC_EUNSUPPORTED;
   MwPlan pl;
-  if (!plan_mw(batch, vocab, {8, 16}, pl) && !plan_mw(batch, vocab, {12, 24, 32, 48}, pl, 2))
+  if (!plan_mw(batch, vocab, {8, 16}, pl) && !plan_mw(batch, vocab, {12, 24}, pl, 2))
     return SPECDEC_EUNSUPPORTED;
   MwArgs a{};
   a.p = (const float *)target_logits;
@@ -1428,9 +1488,7 @@ SPECDEC_API int specdec_accept_reject_logits(const void *target_logits, const vo
     case 8: launch_mw_e<8, true>(true, a, s); break;
     case 12: launch_mw_e<12, true>(true, a, s); break;
     case 16: launch_mw_e<16, true>(true, a, s); break;
-    case 24: launch_mw_e<24, true>(true, a, s); break;
-    case 32: launch_mw_e<32, true>(true, a, s); break;
-    default: launch_mw_e<48, true>(true, a, s); break;
+    default: launch_mw_e<24, true>(true, a, s); break;
   }
   return launch_status();
 }

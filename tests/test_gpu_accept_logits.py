@@ -200,11 +200,13 @@ def test_config1_distribution_matches_target_softmax():
     assert chisquare(obs.numpy(), exp.numpy()).pvalue > 1e-3
 
 
-def test_shapes_the_kernel_does_not_take_run_two_steps():
-    """More than 16 drafted positions: the wrapper says so (None) and the API
-    runs probabilities + accept_reject instead, with the same decisions."""
-    b, k = 2, 17
-    tl, dl, g = logits(b, k, 4096, seed=2)
+@pytest.mark.parametrize("b,k,v", [(2, 17, 4096), (65, 2, V)])
+def test_shapes_the_kernel_does_not_take_run_two_steps(b, k, v):
+    """More than 16 drafted positions, or more rows than two workgroups per
+    compute unit hold (65 rows of a 49152 vocabulary): the wrapper says so
+    (None) and the API runs probabilities + accept_reject instead, with the
+    same decisions."""
+    tl, dl, g = logits(b, k, v, seed=2)
     draft = drafts_from(dl, 1.0, g)
     ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
     assert ops.accept_reject_logits(tl.cuda(), dl.cuda(), 1.0, draft.cuda(), ua.cuda(), ur.cuda()) is None
