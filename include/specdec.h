@@ -127,7 +127,9 @@ int specdec_accept_reject(const void *p, const void *q, int dtype,
  * (16-byte aligned rows: vocab and the strides multiples of 4), k <= 16;
  * draft, u_accept, u_residual, out, workspace and spin as above (the
  * workspace is required).  SPECDEC_EUNSUPPORTED when the shapes do not fit
- * (then probabilities + accept_reject give the same decisions).
+ * (more rows than two workgroups per compute unit hold: 64 rows of a 49152
+ * vocabulary on 256 compute units), and then probabilities + accept_reject
+ * give the same decisions.
  * Replaces lm/sampling.py:13-18 `probabilities` of the target and draft
  * rows followed by spec/accept.py:44-79 `accept_reject`. */
 int specdec_accept_reject_logits(const void *target_logits, const void *draft_logits, int dtype,
