@@ -533,11 +533,28 @@ def bench_kernels(attention_grid=True):
         us_fused = time_fn(lambda: ops.accept_reject_logits(tl, dl, 1.0, draft, ua, ur), graph=True)
         # a round's algorithmic bytes: the 2k+1 logit rows read once
         logit_bytes = (2 * k + 1) * V * 4 * b
-        log(f"accept b{b} k{k}: softmax {us_soft:.2f} us + accept {us_acc:.2f} us; fused {us_fused:.2f} us")
+        # the same with the logits cycled over copies that together exceed
+        # the last-level cache three times, so every launch reads them from
+        # HBM (the timing above reuses one set, as a loop whose output head
+        # has just written them would find them in the cache)
+        copies = min(512, -(-3 * MALL_BYTES // logit_bytes))
+        sets = [(tl.clone(), dl.clone()) for _ in range(copies)]
+        turn = [0]
+
+        def fused_cycled():
+            t_, d_ = sets[turn[0] % copies]
+            turn[0] += 1
+            ops.accept_reject_logits(t_, d_, 1.0, draft, ua, ur)
+
+        us_fused_hbm = graph_time_us(fused_cycled, per_graph=copies, replays=max(1, 2000 // copies))
+        del sets
+        log(f"accept b{b} k{k}: softmax {us_soft:.2f} us + accept {us_acc:.2f} us; fused {us_fused:.2f} us "
+            f"({us_fused_hbm:.2f} us with the logits from HBM)")
         res[f"accept_b{b}_k{k}"] = {
             "round_bytes": logit_bytes,
             "fused_us": us_fused, "fused_gbs": logit_bytes / us_fused / 1e3,
             "fused_frac_of_peak": logit_bytes / us_fused / 1e3 / HBM_PEAK_GBS,
+            "fused_hbm_us": us_fused_hbm, "fused_hbm_frac_of_peak": logit_bytes / us_fused_hbm / 1e3 / HBM_PEAK_GBS,
             "softmax_us": us_soft, "accept_us": us_acc, "two_launch_us": us_soft + us_acc,
             "two_launch_frac_of_peak": logit_bytes / (us_soft + us_acc) / 1e3 / HBM_PEAK_GBS,
             # what the two kernels move themselves: the softmax reads the
@@ -545,7 +562,8 @@ def bench_kernels(attention_grid=True):
             # position's p and q rows (2 V fp32 per batch entry)
             "softmax_traffic_gbs": 2 * logit_bytes / us_soft / 1e3,
             "accept_traffic_gbs": 2 * V * 4 * b / us_acc / 1e3,
-            "what": "fused: specdec_accept_reject_logits (one launch from logits); two-launch: "
+            "what": "fused: specdec_accept_reject_logits (one launch from logits; fused_hbm: the logits "
+                    "cycled over copies so each launch reads them from HBM); two-launch: "
                     "specdec_probabilities of the 2k+1 rows, then specdec_accept_reject; "
                     "fractions over the logits read once"}
     # config 3: n-gram, B=16
