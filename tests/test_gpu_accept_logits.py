@@ -66,6 +66,18 @@ def test_fused_matches_oracle(seed, b, k, temperature):
     check_vs_oracle(tl, dl, temperature, draft, ua, ur, fused(tl, dl, temperature, draft, ua, ur))
 
 
+@pytest.mark.parametrize("b,k,v,temperature", [(1, 4, 4100, 1.0), (2, 4, 40004, 0.8), (3, 3, 1000, 1.3),
+                                               (8, 2, 50000, 0.0), (24, 8, 12, 0.8)])
+def test_ragged_last_chunk_matches_oracle(b, k, v, temperature):
+    """Vocabularies that are not a multiple of a chunk (and one smaller than
+    a thread's elements): the last chunk's missing elements take no part in
+    any row's max, sum, residual or prefix."""
+    tl, dl, g = logits(b, k, v, seed=v + b)
+    draft = drafts_from(dl, temperature, g) if temperature > 0 else dl.argmax(-1)
+    ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
+    check_vs_oracle(tl, dl, temperature, draft, ua, ur, fused(tl, dl, temperature, draft, ua, ur))
+
+
 @pytest.mark.parametrize("b,k", [(1, 4), (8, 4), (32, 8)])
 def test_greedy_is_argmax_verification(b, k):
     """T = 0: p and q are one-hot rows of the argmax (lowest id among ties);
@@ -103,14 +115,14 @@ def test_fused_matches_two_launch_gpu_path(b, k, temperature):
 
 
 @pytest.mark.parametrize("spin", [-1, 0])
-@pytest.mark.parametrize("b,k,temperature", [(1, 4, 1.0), (8, 8, 0.8), (32, 8, 0.8), (4, 4, 0.0), (16, 4, 0.8),
-                                             (64, 4, 0.8)])
-def test_workgroups_that_stop_waiting_compute_the_same_bits(spin, b, k, temperature):
+@pytest.mark.parametrize("b,k,temperature,v", [(1, 4, 1.0, V), (8, 8, 0.8, V), (32, 8, 0.8, V), (4, 4, 0.0, V),
+                                               (16, 4, 0.8, V), (64, 4, 0.8, V), (3, 4, 0.8, 40004)])
+def test_workgroups_that_stop_waiting_compute_the_same_bits(spin, b, k, temperature, v):
     """No workgroup waits (spin < 0), or each reads once (spin 0): every
     missing chunk's statistics, sums and prefixes are computed by the reader
     with the code of the chunk's own workgroup, so the output has the bits
     of the waiting path."""
-    tl, dl, g = logits(b, k, V, seed=77 + b)
+    tl, dl, g = logits(b, k, v, seed=77 + b)
     draft = drafts_from(dl, temperature, g) if temperature > 0 else dl.argmax(-1)
     ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
     want = fused(tl, dl, temperature, draft, ua, ur)
@@ -200,12 +212,13 @@ def test_config1_distribution_matches_target_softmax():
     assert chisquare(obs.numpy(), exp.numpy()).pvalue > 1e-3
 
 
-@pytest.mark.parametrize("b,k,v", [(2, 17, 4096), (65, 2, V)])
+@pytest.mark.parametrize("b,k,v", [(2, 17, 4096), (65, 2, V), (2, 4, 4099)])
 def test_shapes_the_kernel_does_not_take_run_two_steps(b, k, v):
-    """More than 16 drafted positions, or more rows than two workgroups per
-    compute unit hold (65 rows of a 49152 vocabulary): the wrapper says so
-    (None) and the API runs probabilities + accept_reject instead, with the
-    same decisions."""
+    """More than 16 drafted positions, more rows than two workgroups per
+    compute unit hold (65 rows of a 49152 vocabulary), or rows that are not
+    16-byte aligned (a vocabulary of 4099): the wrapper says so (None) and
+    the API runs probabilities + accept_reject instead, with the same
+    decisions."""
     tl, dl, g = logits(b, k, v, seed=2)
     draft = drafts_from(dl, 1.0, g)
     ua, ur = torch.rand(b, k, generator=g), torch.rand(b, generator=g)
