@@ -14,7 +14,12 @@
 // together, with the last tokens), then compares from LDS; agreements that
 // run past the staged overlap or the staged tail read ctx from memory.
 // Once some position of a tile agrees over the longest admissible n,
-// nothing earlier can win and the scan stops.
+// nothing earlier can win and the scan stops.  The first
+// kNgramTile + kNgramOverlap positions of the row are requested before the
+// row's length is known (a buffer whose extent is the row stride, so
+// positions past it read 0): a history of up to that many tokens is then
+// one tile from position 0 whose loads overlap the length's round trip, and
+// its last tokens are read from the staged tile.
 #include "common.h"
 
 namespace specdec {
@@ -36,6 +41,12 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
   __shared__ long long s_key[kNgramThreads / kWave];
   const int64_t b = blockIdx.x;
   const int32_t *ctx = history + b * row_stride;
+  const __amdgpu_buffer_rsrc_t row = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t *>(ctx), 0, (int)min(row_stride * 4, (int64_t)0x7FFFFFFC), 0x00020000);
+  int32_t head[kNgramLoads];  // positions tid + u * kNgramThreads
+#pragma unroll
+  for (int u = 0; u < kNgramLoads; ++u)
+    head[u] = __builtin_amdgcn_raw_buffer_load_b32(row, (unsigned)(threadIdx.x + u * kNgramThreads) * 4u, 0, 0);
   const int L = lengths[b];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int nmax = min(max_n, L - 1);  // may be <= 0: no n-gram to match
@@ -48,6 +59,8 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
     return;
   }
 
+  // the whole history (last token included) is in the first tile
+  const bool one_tile = L <= kNgramTile + kNgramOverlap;
   // (l, e) packed as l << 32 | e; -1: no match yet
   long long key = -1;
   int tile_base = 0, tile_hi = -1;  // ctx[tile_base .. tile_hi] is in s_ctx
@@ -56,20 +69,28 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
     const int base = max(lo - kNgramOverlap, 0);
     const int cnt = hi - base + 1;
     if (tile_hi >= 0) __syncthreads();  // every read of the previous tile is done
-    int32_t v[kNgramLoads];
+    if (one_tile) {  // base = 0: the tile is the requested head, last token included
 #pragma unroll
-    for (int u = 0; u < kNgramLoads; ++u) {
-      const int i = tid + u * kNgramThreads;
-      v[u] = i < cnt ? ctx[base + i] : 0;
-    }
-    int32_t tv = 0;
-    if (tile_hi < 0 && tid < kNgramTail && tid < nmax) tv = ctx[L - 1 - tid];
+      for (int u = 0; u < kNgramLoads; ++u) {
+        const int i = tid + u * kNgramThreads;
+        if (i < kNgramTile + kNgramOverlap) s_ctx[i] = head[u];
+      }
+    } else {
+      int32_t v[kNgramLoads];
 #pragma unroll
-    for (int u = 0; u < kNgramLoads; ++u) {
-      const int i = tid + u * kNgramThreads;
-      if (i < cnt) s_ctx[i] = v[u];
+      for (int u = 0; u < kNgramLoads; ++u) {
+        const int i = tid + u * kNgramThreads;
+        v[u] = i < cnt ? ctx[base + i] : 0;
+      }
+      int32_t tv = 0;
+      if (tile_hi < 0 && tid < kNgramTail && tid < nmax) tv = ctx[L - 1 - tid];
+#pragma unroll
+      for (int u = 0; u < kNgramLoads; ++u) {
+        const int i = tid + u * kNgramThreads;
+        if (i < cnt) s_ctx[i] = v[u];
+      }
+      if (tile_hi < 0 && tid < kNgramTail) s_tail[tid] = tv;
     }
-    if (tile_hi < 0 && tid < kNgramTail) s_tail[tid] = tv;
     __syncthreads();  // the tile (and, the first time, the tail) is in LDS
     tile_base = base;
     tile_hi = hi;
@@ -82,7 +103,7 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
       while (len < cap) {
         const int p = e - len;
         const int32_t x = p >= base ? s_ctx[p - base] : ctx[p];
-        const int32_t y = len < kNgramTail ? s_tail[len] : ctx[L - 1 - len];
+        const int32_t y = one_tile ? s_ctx[L - 1 - len] : len < kNgramTail ? s_tail[len] : ctx[L - 1 - len];
         if (x != y) break;
         ++len;
       }
@@ -106,7 +127,8 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
   __syncthreads();
   if (tid != 0) return;
   for (int w = 0; w < kNgramThreads / kWave; ++w) key = lex_max(key, s_key[w]);
-  const int32_t last = ctx[L - 1];
+  // (staged only when a tile was scanned: none for a one-token history or max_n 0)
+  const int32_t last = one_tile && tile_hi >= 0 ? s_ctx[L - 1] : ctx[L - 1];
   int64_t *out = draft + b * k;
   if (key < 0) {
     for (int i = 0; i < k; ++i) out[i] = last;

@@ -101,6 +101,18 @@ def test_any_max_n_matches_oracle(max_n):
             assert gt == want and tuple(m) == (start, n), (len(row), k, max_n)
 
 
+@pytest.mark.parametrize("max_n", [0, 1, 3])
+def test_one_token_histories_and_no_ngram(max_n):
+    """Histories too short for any n-gram (one token), and max_n 0: no tile
+    is scanned and the proposal repeats the last token."""
+    rows = [[7], [1, 2, 1], [5, 6, 7, 5], [9, 9]]
+    for k in (1, 4):
+        got, match = lookup_batch(rows, k, max_n)
+        for row, gt, m in zip(rows, got, match):
+            want, start, n = on.lookup_match(row, k, max_n)
+            assert gt == want and tuple(m) == (start, n), (row, k, max_n)
+
+
 def test_empty_context_raises():
     with pytest.raises(IndexError):
         lookup([], 3, 3)
@@ -131,7 +143,7 @@ def test_long_histories_across_lds_tiles():
         e = lo0 - shift
         r[e - 2: e + 1] = [1, 2, 3]
         rows.append(r)
-    for length in (8192, 8193, 8194, 8195, 16387):
+    for length in (8192, 8193, 8194, 8195, 8255, 8256, 8257, 16387):
         r = _unique_row(length)
         r[-1] = r[0]  # a single 1-gram match at the very start
         rows.append(r)
