@@ -109,6 +109,7 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
       }
       if (len > 0) key = lex_max(key, ((long long)len << 32) | (long long)e);
     }
+    if (lo == 0) break;  // the last tile: nothing earlier to skip
     // has a position of this tile agreed over the longest admissible n?
     int hit = (int)(key >> 32) == nmax;
     for (int o = kWave / 2; o > 0; o >>= 1) hit |= __shfl_xor(hit, o, kWave);
@@ -125,15 +126,20 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
   __syncthreads();  // s_key's hit flags are read
   if (lane == 0) s_key[wid] = key;
   __syncthreads();
-  if (tid != 0) return;
+  if (wid != 0) return;
+  // wave 0: every lane takes the workgroup's key; lane i writes proposal i
+  key = -1;
+#pragma unroll
   for (int w = 0; w < kNgramThreads / kWave; ++w) key = lex_max(key, s_key[w]);
   // (staged only when a tile was scanned: none for a one-token history or max_n 0)
   const int32_t last = one_tile && tile_hi >= 0 ? s_ctx[L - 1] : ctx[L - 1];
   int64_t *out = draft + b * k;
   if (key < 0) {
-    for (int i = 0; i < k; ++i) out[i] = last;
-    match[2 * b] = -1;
-    match[2 * b + 1] = 0;
+    for (int i = lane; i < k; i += kWave) out[i] = last;
+    if (lane == 0) {
+      match[2 * b] = -1;
+      match[2 * b + 1] = 0;
+    }
     return;
   }
   const int chosen_n = (int)(key >> 32), chosen_e = (int)(key & 0xFFFFFFFF);
@@ -141,12 +147,14 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
   // Its tokens come from the tile still in LDS (it holds e), or are ctx[L-1];
   // only a source reaching into a tile scanned before is read from memory.
   const int src = chosen_e + 1, src_len = L - src;
-  for (int i = 0; i < k; ++i) {
+  for (int i = lane; i < k; i += kWave) {
     const int pos = src + (i % src_len);
     out[i] = pos == L - 1 ? last : (pos <= tile_hi ? s_ctx[pos - tile_base] : ctx[pos]);
   }
-  match[2 * b] = chosen_e - chosen_n + 1;
-  match[2 * b + 1] = chosen_n;
+  if (lane == 0) {
+    match[2 * b] = chosen_e - chosen_n + 1;
+    match[2 * b + 1] = chosen_n;
+  }
 }
 
 }  // namespace specdec
