@@ -49,11 +49,15 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 HOST_WAIT = "default"  # how the host waits for the GPU (main() may switch HIP to spinning)
 # HBM bytes per launch of the B=8, context-4096 verify attention (one tiled
-# launch): rocprofv3 FETCH_SIZE + WRITE_SIZE of `bench.py --only attention
-# --batch 8`, each scaled by what the counter reads for a copy of known size.
-# A stored figure from counter runs of the current kernel (hardware counters
-# cannot be read from inside this process); the line says so.
+# launch) from earlier counter runs of the current kernel: rocprofv3
+# FETCH_SIZE + WRITE_SIZE of `bench.py --only attention --batch 8`, each
+# scaled by what the counter reads for a copy of known size.  The default run
+# measures the figure itself (measure_attention_traffic); this one is reported
+# only when that measurement fails, and the line says which it is.
 ATTN_B8_TRAFFIC = 270_692_966
+COPY_BYTES = 256 << 20  # the copy of known size the counters are scaled by
+STORED_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE runs of `bench.py --only attention --batch 8` "
+                         "(x2.0 / x1.0, the factors a 256 MiB copy gives), not counters read during this run")
 V = 49152
 PROMPT = 256
 NEW_TOKENS = 128
@@ -824,6 +828,106 @@ def bench_batched(target, draft, combos=((8, 4, "model"), (8, 4, "ngram"), (32, 
     return results
 
 
+# ------------------------------------------------- HBM traffic counters ----
+def traffic_workload(launches=6):
+    """What the counter runs profile (`--only traffic`): a copy of COPY_BYTES
+    (three launches), then `launches` launches of the B=8, context-4096 verify
+    attention cycling its layer pools, so each reads K/V from HBM."""
+    from specdec import ops
+
+    x = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    layers = attention_layers(8, 4096)
+    cache, step, q, out = setup_attention(8, 4096, layers=layers)
+    ws = ops.AttentionWorkspace(q.device)
+    for i in range(launches):
+        ops.paged_attention(q, q.stride(1), cache.k[i % layers], cache.v[i % layers], cache.table_tensor, step.meta,
+                            8, 5, 32, 32, 64, BLOCK, 0.125, step.max_total, out, out.stride(1), ws)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": COPY_BYTES, "attention_launches": launches, "layer_pools": layers}
+
+
+def _counter_means(csv_path, counter):
+    """Mean per-dispatch value (KiB) of `counter` for the copy kernel and for
+    the tiled verify attention kernel in a rocprofv3 counter CSV."""
+    import csv
+
+    vals = {"copy": [], "attention": []}
+    copies = []  # (grid, value) of every copy dispatch: the largest grid is the known copy
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"]
+            if "copyBuffer" in name:
+                copies.append((int(r["Grid_Size"]), float(r["Counter_Value"])))
+            elif "attention_bf16_kernel<1, 16, true" in name:
+                vals["attention"].append(float(r["Counter_Value"]))
+    if copies:
+        top = max(g for g, _ in copies)
+        vals["copy"] = [v for g, v in copies if g == top]
+    if not vals["copy"] or not vals["attention"]:
+        raise RuntimeError(f"{counter}: no {'copy' if not vals['copy'] else 'attention'} dispatch in {csv_path}")
+    return statistics.mean(vals["copy"]), statistics.mean(vals["attention"]), len(vals["attention"])
+
+
+def measure_attention_traffic(timeout_s=300):
+    """HBM bytes per launch of the B=8, context-4096 verify attention, read by
+    rocprofv3 in two child runs of `bench.py --only traffic`: FETCH_SIZE, then
+    WRITE_SIZE (one pass cannot collect both).  Each counter is scaled by what
+    it reads for the copy of COPY_BYTES in the same child run.  Runs before
+    this process touches the GPU.  Returns (bytes or None, description)."""
+    import shutil
+    import signal
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    env = dict(os.environ)
+    env.setdefault("TMPDIR", "/tmp")
+    parts = {}
+    with tempfile.TemporaryDirectory(prefix="specdec_traffic_", dir=env["TMPDIR"]) as tmp:
+        for counter, tag in (("FETCH_SIZE", "f"), ("WRITE_SIZE", "w")):
+            out_dir = os.path.join(tmp, tag)
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", tag, "--",
+                   sys.executable, "-u", str(ROOT / "bench.py"), "--only", "traffic"]
+            t0 = time.perf_counter()
+            proc = subprocess.Popen(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                    text=True, start_new_session=True)
+            try:
+                text, _ = proc.communicate(timeout=timeout_s)
+            except subprocess.TimeoutExpired:
+                os.killpg(proc.pid, signal.SIGKILL)
+                proc.communicate()
+                return None, f"{counter} counter run exceeded {timeout_s} s"
+            csv_path = os.path.join(out_dir, f"{tag}_counter_collection.csv")
+            # the profiler can exit non-zero after a complete run; the CSV decides
+            if not os.path.exists(csv_path):
+                tail = " | ".join(text.strip().splitlines()[-3:])
+                return None, f"{counter} counter run (exit {proc.returncode}) wrote no CSV: {tail}"
+            try:
+                copy_kib, attn_kib, n = _counter_means(csv_path, counter)
+            except (RuntimeError, KeyError, ValueError) as e:
+                return None, str(e)
+            scale = COPY_BYTES / (copy_kib * 1024)
+            parts[counter] = {"attention_kib_per_dispatch": attn_kib, "dispatches": n,
+                              "copy_kib_per_dispatch": copy_kib, "scale": scale,
+                              "bytes": attn_kib * 1024 * scale, "seconds": time.perf_counter() - t0}
+            log(f"traffic {counter}: {parts[counter]}")
+    total = parts["FETCH_SIZE"]["bytes"] + parts["WRITE_SIZE"]["bytes"]
+    desc = ("measured in this run: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, child runs of "
+            "`bench.py --only traffic` ({} and {} attention dispatches), each scaled by what the counter reads "
+            "for a 256 MiB copy in the same child run (x{:.3f} / x{:.3f})").format(
+        parts["FETCH_SIZE"]["dispatches"], parts["WRITE_SIZE"]["dispatches"], parts["FETCH_SIZE"]["scale"],
+        parts["WRITE_SIZE"]["scale"])
+    return int(round(total)), desc
+
+
 # ------------------------------------------------------------ CPU side ------
 def cpu_model():
     try:
@@ -1175,11 +1279,13 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--only", choices=["all", "e2e", "batched", "batched-cpu", "attention", "kernels", "small", "copy",
-                                       "head", "rollback"],
+                                       "head", "rollback", "traffic"],
                     default="all",
                     help="small: the kernels of configs 1-3 without the attention grid (for counter runs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 counter runs of the attention's HBM traffic (the stored figure is reported)")
     ap.add_argument("--batch", type=int, default=8, help="batch of the --only attention run")
     ap.add_argument("--one-pool", action="store_true", help="--only attention: re-read one layer pool")
     ap.add_argument("--context", type=int, default=4096, help="--only batched: context the rows decode to")
@@ -1188,6 +1294,16 @@ def main():
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (the path is built and "
               "measured on a single GPU; sharding across GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
+    # the roofline's traffic: counter runs in child processes, before this
+    # one touches the GPU
+    traffic, traffic_source = ATTN_B8_TRAFFIC, "stored (--no-traffic): " + STORED_TRAFFIC_SOURCE
+    if args.only == "all" and not args.no_traffic:
+        measured, why = measure_attention_traffic()
+        if measured is not None:
+            traffic, traffic_source = measured, why
+        else:
+            traffic_source = f"stored (the counter runs failed: {why}): " + STORED_TRAFFIC_SOURCE
+        log(f"attention traffic {traffic} B: {traffic_source}")
     # the host spins while it waits for each round's verdict (before anything
     # touches the GPU); SPECDEC_SPIN_WAIT=0 keeps HIP's default wait
     global HOST_WAIT
@@ -1209,6 +1325,9 @@ def main():
         return
     if args.only in ("kernels", "small"):
         print(json.dumps(bench_kernels(attention_grid=args.only == "kernels")))
+        return
+    if args.only == "traffic":
+        print(json.dumps(traffic_workload()))
         return
     if args.only == "copy":
         # reference copy of a known size for scaling the FETCH_SIZE / WRITE_SIZE counters
@@ -1301,10 +1420,8 @@ def main():
                    "batch": 1, "k": K, "prompt": PROMPT, "new_tokens": NEW_TOKENS, "block_size": BLOCK,
                    "host_wait": HOST_WAIT},
         "roofline": {"bound": "hbm", "achieved": attn["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": ATTN_B8_TRAFFIC,
-                     "traffic_source": "stored: rocprofv3 --pmc FETCH_SIZE then WRITE_SIZE runs of "
-                                       "`bench.py --only attention --batch 8` (x2.0 / x1.0, the factors a "
-                                       "256 MiB copy gives), not counters read during this run",
+                     "frac": attn["gbs"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_over_algorithmic": traffic / attn["bytes"], "traffic_source": traffic_source,
                      "kernel": "verify paged attention (attention_bf16_kernel<1, 16, true>: one 16-wave workgroup "
                                "per (row, kv head) tile taking its 512-token splits in rounds, no combine launch), "
                                "B=8, context 4096 (+5 appended), 32/32 heads x 64, bf16, block 16, K/V from HBM",
