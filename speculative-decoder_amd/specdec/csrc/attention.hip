@@ -1781,6 +1781,10 @@ static int plan_attention(AttnArgs &a, AttnPlan &plan, int dtype, int32_t batch,
     return SPECDEC_OK;
   }
   if (!a.q || !a.k || !a.v || !a.tables || !a.meta || !a.out) return SPECDEC_EINVAL;
+  // a token's row of q (of qkv, with rope) and of out holds all of its
+  // heads, so the rows of a call never overlap
+  const int64_t q_row = (int64_t)(a.rope ? n_heads + 2 * n_kv_heads : n_heads) * head_dim;
+  if (a.q_stride < q_row || a.out_stride < (int64_t)n_heads * head_dim) return SPECDEC_EINVAL;
   a.batch = batch;
   a.width = width;
   a.H = n_heads;

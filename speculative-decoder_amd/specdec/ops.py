@@ -58,6 +58,21 @@ def _on(dev: torch.device, t: torch.Tensor, name: str, dtype: torch.dtype | None
     return t
 
 
+def _token_rows(t: torch.Tensor, tokens: int, stride: int, row: int, name: str) -> None:
+    """Host-side check that t's memory, from its first element, holds `tokens`
+    rows of `row` elements `stride` apart (the rows a kernel reads or writes
+    through t's pointer and the stride it is given)."""
+    if tokens <= 0:
+        return
+    if stride < row:
+        raise ValueError(f"{name}: a token stride of {stride} is shorter than a token's {row} elements")
+    have = t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+    need = (tokens - 1) * stride + row
+    if need > have:
+        raise ValueError(f"{name} holds {have} elements from its start; {tokens} token rows of {row} "
+                         f"elements at stride {stride} need {need}")
+
+
 def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -539,6 +554,7 @@ def rope_append(qkv, n_heads, n_kv_heads, head_dim, cos, sin, meta, batch, width
                 k_pool, v_pool) -> None:
     dev = gpu(qkv, "qkv").device
     _qkv_side(dev, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool)
+    _token_rows(qkv, batch * width, qkv.stride(1), (n_heads + 2 * n_kv_heads) * head_dim, "qkv")
     st = lib().specdec_rope_append(qkv.data_ptr(), dtype_code(qkv), qkv.stride(1), n_heads, n_kv_heads, head_dim,
                                    cos.data_ptr(), sin.data_ptr(), cos.shape[0], meta.data_ptr(), batch, width,
                                    tables.data_ptr(), tables.stride(0), block_size, k_pool.data_ptr(),
@@ -713,6 +729,7 @@ def rope_paged_attention_parts(qkv, cos, sin, k_pool, v_pool, tables, meta, batc
     bits rope_paged_attention produces) and projects them."""
     dev = gpu(qkv, "qkv").device
     _qkv_side(dev, qkv, cos, sin, meta, batch, 1, tables, k_pool, v_pool)
+    _token_rows(qkv, batch, qkv.stride(1), (n_heads + 2 * n_kv_heads) * head_dim, "qkv")
     nparts = _parts_of(parts, dev, batch, n_heads)
     hidden_dim = 0
     if norm_of is not None:
@@ -789,6 +806,8 @@ def paged_attention(q, q_token_stride, k_pool, v_pool, tables, meta, batch, widt
                     block_size, scale, max_kv_len, out, out_token_stride, workspace: AttentionWorkspace | None = None,
                     split_tokens: int = 0):
     _qkv_side(gpu(q, "q").device, q, None, None, meta, batch, width, tables, k_pool, v_pool, out)
+    _token_rows(q, batch * width, q_token_stride, n_heads * head_dim, "q")
+    _token_rows(out, batch * width, out_token_stride, n_heads * head_dim, "out")
     ws = workspace or workspace_for(q.device)
     ws.reserve(attention_workspace_floats(batch, width, n_heads, n_kv_heads, head_dim, max_kv_len, split_tokens))
     st = lib().specdec_paged_attention(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
@@ -807,6 +826,8 @@ def paged_attention_static(q, q_token_stride, k_pool, v_pool, tables, meta, batc
     call allocates nothing.  Raises KernelError if the call needs more
     partials than that buffer holds; calls overlapping on one GPU race."""
     _qkv_side(gpu(q, "q").device, q, None, None, meta, batch, width, tables, k_pool, v_pool, out)
+    _token_rows(q, batch * width, q_token_stride, n_heads * head_dim, "q")
+    _token_rows(out, batch * width, out_token_stride, n_heads * head_dim, "out")
     st = lib().specdec_paged_attention_static(q.data_ptr(), dtype_code(q), q_token_stride, k_pool.data_ptr(),
                                               v_pool.data_ptr(), tables.data_ptr(), tables.stride(0),
                                               meta.data_ptr(), batch, width, n_heads, n_kv_heads, head_dim,
@@ -838,6 +859,8 @@ def rope_paged_attention(qkv, cos, sin, k_pool, v_pool, tables, meta, batch, wid
     after the projection (`norm_in_attention` tells which shapes allow it)."""
     dev = gpu(qkv, "qkv").device
     _qkv_side(dev, qkv, cos, sin, meta, batch, width, tables, k_pool, v_pool, out)
+    _token_rows(qkv, batch * width, qkv.stride(1), (n_heads + 2 * n_kv_heads) * head_dim, "qkv")
+    _token_rows(out, batch * width, out_token_stride, n_heads * head_dim, "out")
     hidden_dim = 0
     if norm_of is not None:
         if not norm_in_attention(qkv.dtype, block_size, width):

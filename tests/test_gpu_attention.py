@@ -783,3 +783,40 @@ def test_rows_beyond_max_kv_len_get_nan(dtype, max_kv_len):
                         torch.tensor([105]), d ** -0.5)
     tol = 2e-2 if dtype == torch.bfloat16 else 2e-5
     assert (got[0].view(t_new, h, d).transpose(0, 1) - want[0]).abs().max().item() < tol
+
+
+def test_short_token_buffers_are_refused_before_launch():
+    """q, qkv and out must hold batch x width token rows at the strides the
+    call is given: a shorter buffer, or a stride shorter than a token's heads,
+    is refused on the host (a kernel would read or write past it)."""
+    d, h, hkv, bs, t_new = 64, 4, 4, 16, 5
+    cache = make_cache(1, hkv, d, 16, bs, torch.bfloat16, 3)
+    cache.add(0)
+    cache.append([0], [32])
+    step = cache.append([0], [t_new])
+    q = torch.zeros(1, t_new, h * d, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros_like(q)
+    args = (cache.k[0], cache.v[0], cache.table_tensor, step.meta, 1, t_new, h, hkv, d, bs, 0.125, 37)
+    # (a view into a larger buffer is memory the kernel may use: the short
+    # buffers are tensors of their own)
+    short_q = torch.zeros(1, 4, h * d, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="q holds"):
+        ops.paged_attention(short_q, short_q.stride(1), *args, out, out.stride(1))
+    short_out = torch.zeros(1, 3, h * d, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="out holds"):
+        ops.paged_attention(q, q.stride(1), *args, short_out, short_out.stride(1))
+    with pytest.raises(ValueError, match="token stride"):
+        ops.paged_attention(q, h * d - 64, *args, out, out.stride(1))
+    with pytest.raises(ValueError, match="q holds"):
+        ops.paged_attention_static(short_q, short_q.stride(1), *args, out, out.stride(1))
+    short_qkv = torch.zeros(1, 2, (h + 2 * hkv) * d, dtype=torch.bfloat16, device="cuda")
+    cos = torch.ones(64, d // 2, device="cuda")
+    sin = torch.zeros(64, d // 2, device="cuda")
+    with pytest.raises(ValueError, match="qkv holds"):
+        ops.rope_paged_attention(short_qkv, cos, sin, *args, out, out.stride(1))
+    with pytest.raises(ValueError, match="qkv holds"):
+        ops.rope_append(short_qkv, h, hkv, d, cos, sin, step.meta, 1, t_new, cache.table_tensor, bs, cache.k[0],
+                        cache.v[0])
+    # the same buffers at full length run
+    ops.paged_attention(q, q.stride(1), *args, out, out.stride(1))
+    torch.cuda.synchronize()

@@ -44,6 +44,22 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.specdec_block_plan(None, 1, None, None, 4, 5, None, 1, 0, None, None) == 1  # top > num_blocks
 
 
+def test_attention_entry_points_check_token_strides_before_launch():
+    lib = _lib.load()
+    fake = 1 << 20  # never dereferenced: the call returns before any launch
+    # q [tokens, 32 heads x 64], out likewise: a token stride shorter than a
+    # token's heads would make rows overlap -- invalid
+    def call(q_stride, out_stride):
+        return lib.specdec_paged_attention(fake, 2, q_stride, fake, fake, fake, 8, fake, 1, 5, 32, 32, 64, 16, 0.125,
+                                           64, 0, fake, 1 << 20, fake, out_stride, None)
+    assert call(32 * 64 - 8, 32 * 64) == 1
+    assert call(32 * 64, 32 * 64 - 8) == 1
+    # with rope the rows are qkv rows: (32 + 2 x 32) x 64 elements
+    assert lib.specdec_rope_paged_attention(fake, 2, 32 * 64, fake, fake, None, 0, 0.0, fake, fake, fake, 8, fake, 1,
+                                            5, 32, 32, 64, 16, 0.125, 64, 0, fake, 1 << 20, fake, 32 * 64,
+                                            None) == 1
+
+
 def test_head_entry_points_check_shapes_before_launch():
     import ctypes
 
