@@ -47,7 +47,8 @@ __global__ __launch_bounds__(kNgramThreads) void ngram_lookup_kernel(
 #pragma unroll
   for (int u = 0; u < kNgramLoads; ++u)
     head[u] = __builtin_amdgcn_raw_buffer_load_b32(row, (unsigned)(threadIdx.x + u * kNgramThreads) * 4u, 0, 0);
-  const int L = lengths[b];
+  // a length past the row's stride is taken as the stride: no read leaves the row
+  const int L = (int)min((int64_t)lengths[b], row_stride);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int nmax = min(max_n, L - 1);  // may be <= 0: no n-gram to match
   if (L <= 0) {  // no last token to fall back on (callers reject empty histories)

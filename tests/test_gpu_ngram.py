@@ -113,6 +113,21 @@ def test_one_token_histories_and_no_ngram(max_n):
             assert gt == want and tuple(m) == (start, n), (row, k, max_n)
 
 
+def test_lengths_past_the_row_are_taken_as_the_row():
+    """A length beyond the history buffer's row stride (a caller's mistake
+    the host cannot see: lengths live on the GPU) reads nothing outside the
+    row: the kernel takes the row's whole stride as the history."""
+    from specdec import ops
+
+    g = torch.Generator().manual_seed(4)
+    hist = torch.randint(0, 5, (3, 40), generator=g, dtype=torch.int32)
+    want = [on.lookup_match(row.tolist(), 4, 3) for row in hist]
+    lengths = torch.tensor([40, 41, 1 << 30], dtype=torch.int32)
+    draft, match = ops.ngram_lookup(hist.cuda(), lengths.cuda(), 4, 3)
+    for (w, start, n), gt, m in zip(want, draft.cpu().tolist(), match.cpu().tolist()):
+        assert gt == w and tuple(m) == (start, n)
+
+
 def test_empty_context_raises():
     with pytest.raises(IndexError):
         lookup([], 3, 3)
