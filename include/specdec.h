@@ -313,8 +313,12 @@ int specdec_attention_split(int32_t batch, int32_t width, int32_t n_heads,
  * most 8 query rows per kv head: the workspace is then not used); calls
  * sharing a workspace must be ordered.  max_kv_len must bound every row's
  * cached length after the call (past + n_new): the grid is sized from it,
- * and a row beyond it gets NaN in its output rows (and, in the fused-append
- * entry point, nothing appended) instead of a silent skip.
+ * and a query tile whose keys pass it (16 query rows of a kv head) gets NaN
+ * in its output rows (and, in the fused-append entry point, nothing
+ * appended) instead of a silent skip; no key past it is read.  q_token_stride
+ * and out_token_stride must cover a token's n_heads * head_dim elements (for
+ * the fused-append entry point, the qkv row's (n_heads + 2 n_kv_heads) *
+ * head_dim), else SPECDEC_EINVAL.
  * Replaces lm/forward.py:44-49,62-63 (mask, gather copy, SDPA) and
  * cache/kv.py:108-112. */
 int specdec_paged_attention(const void *q, int dtype, int64_t q_token_stride,

@@ -80,6 +80,7 @@ struct AttnArgs {
   int batch, width, H, Hkv, bs;
   float scale;
   int split, max_splits, n_qtiles;
+  int max_kv;  // the call's max_kv_len: no row may hold more keys
   // split partial slots per unit in the workspace (1 when no combine runs)
   int parts;
   // 16-wave launches only: one split over every key, wave w taking the
@@ -95,7 +96,7 @@ struct AttnArgs {
 
 struct TileInfo {
   int b, h, qt, group, row, past, nnew, nrows, kv_len, nsplit, unit;
-  bool overflow;  // the row's keys need more splits than max_kv_len allows
+  bool overflow;  // the tile's keys pass the call's max_kv_len
 };
 
 // A unit's coordinates from the grid alone (no memory read): query tile,
@@ -110,8 +111,7 @@ __device__ __forceinline__ void tile_coords(const AttnArgs &a, int unit, TileInf
 }
 
 // The row metadata of a unit whose coordinates are set; false when the
-// tile holds no live query row (or needs more splits than max_kv_len
-// allows: ti.overflow).  The three words are read through the constant
+// tile holds no live query row (or its keys pass max_kv_len: ti.overflow).  The three words are read through the constant
 // address space (the host writes them before the launch), as one scalar
 // round trip that vector loads issued earlier do not hold up.
 __device__ __forceinline__ bool tile_meta(const AttnArgs &a, TileInfo &ti, bool any_split) {
@@ -130,7 +130,7 @@ __device__ __forceinline__ bool tile_meta(const AttnArgs &a, TileInfo &ti, bool 
   const int t_hi = min(r0 + kRows - 1, ti.nrows - 1) / ti.group;
   ti.kv_len = ti.past + t_hi + 1;
   ti.nsplit = (ti.kv_len + a.split - 1) / a.split;
-  ti.overflow = ti.nsplit > a.max_splits;
+  ti.overflow = ti.kv_len > a.max_kv || ti.nsplit > a.max_splits;
   if (ti.overflow) return false;
   if (!any_split && (int)blockIdx.y >= ti.nsplit) return false;
   return true;
@@ -1397,7 +1397,7 @@ __global__ __launch_bounds__(kPrefillThreads) void attention_prefill_kernel(Attn
   // (tiles whose keys would pass max_kv_len took the NaN branch above)
   const int last_qt = min(qb * kPrefillTiles + kPrefillTiles - 1, (t0.nrows - 1) / kRows);
   const int t_last = min(min(last_qt * kRows + kRows - 1, t0.nrows - 1) / t0.group,
-                         a.max_splits * a.split - 1 - t0.past);
+                         a.max_kv - 1 - t0.past);
   const int wg_kv = t0.past + t_last + 1;
   const int bs = (MODE == 1) ? 16 : a.bs;
   const int Hkv = a.Hkv;
@@ -1796,6 +1796,7 @@ static int plan_attention(AttnArgs &a, AttnPlan &plan, int dtype, int32_t batch,
     a.split = split_tokens > 0 ? round_split(split_tokens, max_kv_len)
                                : choose_split(batch, width, n_heads, n_kv_heads, max_kv_len);
   a.max_splits = (max_kv_len + a.split - 1) / a.split;
+  a.max_kv = max_kv_len;
   a.n_qtiles = qtiles(width, n_heads, n_kv_heads);
   const int64_t units = (int64_t)batch * n_kv_heads * a.n_qtiles;
   // bf16 tiles with more than four splits (at most kTSplits), when every CU
@@ -2042,6 +2043,7 @@ SPECDEC_API int specdec_rope_paged_attention_parts(void *qkv, int64_t token_stri
   a.flat = 1;  // one split over every key
   a.split = (max_kv_len + 63) / 64 * 64;
   a.max_splits = 1;
+  a.max_kv = max_kv_len;
   a.n_qtiles = 1;
   a.parts = 1;
   hipStream_t s = as_stream(stream);

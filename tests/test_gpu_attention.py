@@ -654,8 +654,9 @@ def test_decode_parts_counts_follow_the_context():
 def test_decode_parts_rows_beyond_max_kv_len_are_nan():
     """A row whose cached length exceeds the call's max_kv_len (a broken
     contract) gets NaN, as from the attention-only kernel."""
-    (ref, _), (got, _) = _parts_case(16, [300], 9, 3, 576, seed=5, max_kv_len=64)
-    assert torch.isnan(ref.float()).all() and torch.isnan(got.float()).all()
+    for max_kv_len in (64, 300):  # 300: one key short of the row's 301, within its last 64-key step
+        (ref, _), (got, _) = _parts_case(16, [300], 9, 3, 576, seed=5, max_kv_len=max_kv_len)
+        assert torch.isnan(ref.float()).all() and torch.isnan(got.float()).all()
 
 
 def test_decode_parts_reject_other_shapes():
@@ -751,13 +752,15 @@ def test_bf16_prefill_matches_oracle(width, bs, heads, past):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("max_kv_len", [1030, 2600])
-def test_rows_beyond_max_kv_len_get_nan(dtype, max_kv_len):
-    """A caller passing a max_kv_len below a row's cached length breaks the
-    contract: that row's output is NaN (not left stale), the other rows are
-    exact.  1030 keys: the one-workgroup grid; 2600: split partials and the
-    combine launch."""
-    d, h, hkv, bs, t_new = 64, 8, 8, 16, 5
+@pytest.mark.parametrize("t_new,max_kv_len", [(5, 1030), (5, 2600), (5, 4004), (20, 4010)])
+def test_rows_beyond_max_kv_len_get_nan(dtype, t_new, max_kv_len):
+    """A caller passing a max_kv_len below a row's key count breaks the
+    contract: that row's output is NaN (not left stale, and no key past
+    max_kv_len is read), the other rows are exact.  1030 keys: the
+    one-workgroup grid; 2600: split partials and the combine launch; 4004:
+    one key short of the row's 4005, within the last split; 20 new tokens:
+    the prompt-sized kernel (bf16), every query tile of the row past 4010."""
+    d, h, hkv, bs = 64, 8, 8, 16
     lengths = [100, 4000]
     g = torch.Generator().manual_seed(9)
     cache = make_cache(1, hkv, d, sum(L // bs + 2 for L in lengths) + 8, bs, dtype, 9)
@@ -780,7 +783,7 @@ def test_rows_beyond_max_kv_len_get_nan(dtype, max_kv_len):
     k0 = torch.cat([kh[0, :, :100], kn[0]], dim=1).float()[None]
     v0 = torch.cat([vh[0, :, :100], vn[0]], dim=1).float()[None]
     want = of.attention(q[:1].view(1, t_new, h, d).transpose(1, 2).float().cpu(), k0, v0, torch.tensor([100]),
-                        torch.tensor([105]), d ** -0.5)
+                        torch.tensor([100 + t_new]), d ** -0.5)
     tol = 2e-2 if dtype == torch.bfloat16 else 2e-5
     assert (got[0].view(t_new, h, d).transpose(0, 1) - want[0]).abs().max().item() < tol
 
