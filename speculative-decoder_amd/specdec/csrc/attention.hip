@@ -111,9 +111,10 @@ __device__ __forceinline__ void tile_coords(const AttnArgs &a, int unit, TileInf
 }
 
 // The row metadata of a unit whose coordinates are set; false when the
-// tile holds no live query row (or its keys pass max_kv_len: ti.overflow).  The three words are read through the constant
-// address space (the host writes them before the launch), as one scalar
-// round trip that vector loads issued earlier do not hold up.
+// tile holds no live query row (or its keys pass max_kv_len: ti.overflow).
+// The three words are read through the constant address space (the host
+// writes them before the launch), as one scalar round trip that vector
+// loads issued earlier do not hold up.
 __device__ __forceinline__ bool tile_meta(const AttnArgs &a, TileInfo &ti, bool any_split) {
   typedef const __attribute__((address_space(4))) int32_t const_i32;
   const_i32 *meta = (const_i32 *)a.meta;
