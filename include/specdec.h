@@ -173,7 +173,8 @@ int specdec_one_hot(const int64_t *ids, int64_t n, int64_t vocab, float *out,
  * k tokens that followed it are proposed, the copy reading its own output
  * once it passes the end of the history.  Without a match the last token is
  * repeated k times.  draft int64 [batch, k]; match int32 [batch, 2] = (start
- * of the matched n-gram, n), or (-1, 0) when nothing matched.
+ * of the matched n-gram, n), or (-1, 0) when nothing matched.  A length
+ * beyond row_stride is taken as row_stride (no read leaves a row).
  * Replaces spec/ngram.py:32-45 `lookup` (and the per-row loop of :19-23). */
 int specdec_ngram_lookup(const int32_t *history, int64_t row_stride,
                          const int32_t *lengths, int64_t batch, int32_t k,
